@@ -1,0 +1,184 @@
+/*
+ * miq_qconv.h - C-ABI of the MI355X (gfx950) quantized NHWC convolution library.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream, returns a
+ * miq_status code and never throws.  The C++ drop-in surface (conv_types.h) and the
+ * Python binding (my_own_cnn_amd) are thin layers over these functions.
+ *
+ * Conventions
+ *   - Tensors are dense and live in device memory owned by the caller:
+ *       input  x: NHWC, n*h*w*c elements
+ *       filter w: KRSC, k*r*s*(c/groups) elements
+ *       output y: NHWC, n*ho*wo*k elements, fully overwritten
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Calls are
+ *     asynchronous with respect to the host; the caller synchronises.
+ *   - Arguments are validated on the host before anything is enqueued; a failed
+ *     validation returns a non-zero status and leaves the output untouched.
+ *   - The library allocates no device memory and keeps no mutable global state, so
+ *     calls are re-entrant; calls on different streams may overlap.
+ *   - miq_last_error_message() returns the text of the last non-OK status raised on
+ *     the calling thread.
+ */
+#ifndef MIQ_QCONV_H_
+#define MIQ_QCONV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIQ_VERSION 100 /* 1.0.0 */
+
+typedef enum miq_status {
+  MIQ_OK = 0,
+  MIQ_ERR_NULL_POINTER = 1,     /* a required pointer argument is NULL */
+  MIQ_ERR_INVALID_ARGUMENT = 2, /* shape or parameter rejected (same rules as the reference) */
+  MIQ_ERR_UNSUPPORTED = 3,      /* valid problem the requested algorithm cannot run */
+  MIQ_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed */
+} miq_status;
+
+/* Kernel families of the int8 entry points (miq_qconv_desc.algo). */
+typedef enum miq_algo {
+  MIQ_ALGO_AUTO = 0,   /* pick by shape: implicit GEMM if eligible, stem kernel for thin C, else direct */
+  MIQ_ALGO_DIRECT = 1, /* VALU direct convolution: any shape, bandwidth-bound fallback */
+  MIQ_ALGO_IGEMM = 2,  /* int8 MFMA implicit GEMM: needs (c/groups) % 16 == 0, 16-byte aligned tensors */
+  MIQ_ALGO_STEM = 3    /* int8 MFMA thin-channel kernel: c/groups < 16, groups == 1 */
+} miq_algo;
+
+/* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */
+typedef struct miq_conv2d_params {
+  int32_t pad_h;
+  int32_t pad_w;
+  int32_t stride_h;
+  int32_t stride_w;
+  int32_t dilation_h;
+  int32_t dilation_w;
+  int32_t groups;
+} miq_conv2d_params;
+
+/* Same layout as BlockConv2DParams (/root/reference/src/conv_types.h:31-35). */
+typedef struct miq_block_conv2d_params {
+  miq_conv2d_params conv;
+  int32_t block_by;
+  int32_t block_bx;
+} miq_block_conv2d_params;
+
+/* Byte layout of QuantizationParameters<LinQuantU8> (nnalgebra_quantization.h:29-34):
+ * 12 bytes, zero_point at 0, scale at 4, symmetric at 8. */
+typedef struct miq_qparams_u8 {
+  uint8_t zero_point;
+  float scale;
+  uint8_t symmetric;
+} miq_qparams_u8;
+
+/* Byte layout of QuantizationParameters<LinQuantS5> (nnalgebra_quantization.h:36-41):
+ * 8 bytes, zero_point at 0, n_bins at 1, scale at 4. */
+typedef struct miq_qparams_s5 {
+  int8_t zero_point;
+  uint8_t n_bins;
+  float scale;
+} miq_qparams_s5;
+
+/* Problem description of the native int8 convolution.
+ *   y[n,ho,wo,k] = requant( sum_{r,s,ci} x[n, ho*sh-ph+r*dh, wo*sw-pw+s*dw, g*c/groups+ci]
+ *                                        * w[k, r, s, ci] )
+ * over in-bounds taps only (padded taps contribute 0), g = k / (k_total/groups).
+ * Requantization of one int32 accumulator `acc` of output channel k:
+ *   a  = in_scale / out_scale                (fp32, computed once on the host)
+ *   m  = a * w_scale[k]                      (fp32 multiply, round to nearest even)
+ *   v  = (float)(acc + bias[k]) * m          (int32 wrap-around add, exact-RNE convert, fp32 multiply)
+ *   q  = rint(v) (ties to even), then q < lo -> lo (NaN -> lo), q > 127 -> 127
+ *   lo = 0 when relu != 0, else -128.
+ * Zero points are 0 (symmetric int8, nnalgebra::DataType::LinQuantI8). */
+typedef struct miq_qconv_desc {
+  int32_t n, h, w, c;      /* input NHWC */
+  int32_t k, r, s;         /* filter: k output channels, r x s taps, c/groups input channels */
+  miq_conv2d_params conv;  /* padding, stride, dilation, groups */
+  int32_t relu;            /* non-zero: clamp the output below at 0 */
+  float in_scale;          /* real value of one input code step */
+  float out_scale;         /* real value of one output code step */
+  int32_t algo;            /* miq_algo; MIQ_ALGO_AUTO selects by shape */
+} miq_qconv_desc;
+
+/* ---- library information (host only) ---------------------------------------------- */
+
+int miq_version(void);
+const char* miq_status_string(int status);
+const char* miq_last_error_message(void);
+
+/* ---- shape inference (host only, no GPU access) ------------------------------------ */
+
+/* Output spatial size with the validation rules of infer_conv_shape
+ * (/root/reference/src/conv_types.h:125-146). */
+int miq_conv2d_output_shape(int32_t n, int32_t h, int32_t w, int32_t c,
+                            int32_t r, int32_t s, int32_t k,
+                            const miq_conv2d_params* p, int32_t* ho, int32_t* wo);
+
+/* Output size and per-block extent with the rules of infer_block_conv_shape
+ * (/root/reference/src/conv_types.h:148-169). */
+int miq_block_conv2d_output_shape(int32_t n, int32_t h, int32_t w, int32_t c,
+                                  int32_t r, int32_t s, int32_t k,
+                                  const miq_block_conv2d_params* p, int32_t* ho, int32_t* wo,
+                                  int32_t* block_ho, int32_t* block_wo);
+
+/* Validates `d` and reports the kernel family the int8 entry points will run
+ * (resolving MIQ_ALGO_AUTO).  No GPU access. */
+int miq_qconv2d_plan(const miq_qconv_desc* d, int32_t* algo);
+
+/* ---- int32-accumulator convolution on quantized float codes ------------------------ */
+/* acc = sum over in-bounds taps of (int32(x) - zp_x[n]) * (int32(w) - zp_w), where int32()
+ * truncates toward zero; in_qp is a device array of n parameter structs (one per batch
+ * sample) and f_qp a device pointer to one struct. */
+
+/* Replaces conv_quant_detail::launch_fprop_nhwc_qi32_u8 (/root/reference/src/cuda_kernels.cu:1467-1473). */
+int miq_fprop_nhwc_qi32_u8(const float* x, const float* w, int32_t* y,
+                           int32_t n, int32_t h, int32_t wdt, int32_t c,
+                           int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
+                           const miq_qparams_u8* in_qp, const miq_qparams_u8* f_qp, void* stream);
+
+/* Replaces conv_quant_detail::launch_fprop_nhwc_qi32_s5 (/root/reference/src/cuda_kernels.cu:1475-1481). */
+int miq_fprop_nhwc_qi32_s5(const float* x, const float* w, int32_t* y,
+                           int32_t n, int32_t h, int32_t wdt, int32_t c,
+                           int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
+                           const miq_qparams_s5* in_qp, const miq_qparams_s5* f_qp, void* stream);
+
+/* Blocked filters [K, By, Bx, R, S, C/groups]: output pixel (ho, wo) uses filter block
+ * (ho / block_ho, wo / block_wo).
+ * Replaces conv_quant_detail::launch_block_fprop_nhwc_qi32_u8 (/root/reference/src/cuda_kernels.cu:1483-1489). */
+int miq_block_fprop_nhwc_qi32_u8(const float* x, const float* w, int32_t* y,
+                                 int32_t n, int32_t h, int32_t wdt, int32_t c,
+                                 int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p,
+                                 const miq_qparams_u8* in_qp, const miq_qparams_u8* f_qp, void* stream);
+
+/* Replaces conv_quant_detail::launch_block_fprop_nhwc_qi32_s5 (/root/reference/src/cuda_kernels.cu:1491-1497). */
+int miq_block_fprop_nhwc_qi32_s5(const float* x, const float* w, int32_t* y,
+                                 int32_t n, int32_t h, int32_t wdt, int32_t c,
+                                 int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p,
+                                 const miq_qparams_s5* in_qp, const miq_qparams_s5* f_qp, void* stream);
+
+/* ---- native int8 convolution ------------------------------------------------------- */
+/* No reference counterpart: the int8 activation / int8 weight / int32 bias /
+ * per-channel scale / int8 output surface that the reference's quantization types
+ * describe but never implement.  Its int32 accumulators equal those of
+ * cpu_fprop_nhwc_qi32 (/root/reference/src/cpu_ref.cpp:36-72) with zero points 0. */
+
+/* Fused conv + bias + per-channel requantize + optional ReLU + int8 saturate.
+ * bias: device int32[k] or NULL (treated as 0); w_scale: device float[k]. */
+int miq_qconv2d_nhwc_i8(const miq_qconv_desc* d, const int8_t* x, const int8_t* w,
+                        const int32_t* bias, const float* w_scale, int8_t* y, void* stream);
+
+/* Raw int32 accumulators (no bias, no requantization). */
+int miq_qconv2d_nhwc_i8_acc32(const miq_qconv_desc* d, const int8_t* x, const int8_t* w,
+                              int32_t* acc, void* stream);
+
+/* Dequantized fp32 view: v = (float)(acc + bias[k]) * m as defined above (no rint, no
+ * clamp); with relu, v <= 0 or NaN becomes +0. */
+int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const int8_t* w,
+                                const int32_t* bias, const float* w_scale, float* y, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* MIQ_QCONV_H_ */

@@ -1,0 +1,231 @@
+"""Python mirror of the quantized-convolution interface, over libmiq_qconv's C-ABI.
+
+Names, argument order and error behaviour follow the reference's C++ surface
+(/root/reference/src/conv_types.h:125-169, :255-340): shape inference raises with the
+reference's messages, a missing quantization parameter raises before anything runs, and
+every launch is asynchronous on the given (default: PyTorch's current) HIP stream.
+
+Device tensors are ``torch`` tensors on a ROCm device (PyTorch is used only to own device
+memory and streams) or raw integer device addresses.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+from typing import Optional, Sequence, Tuple, Union
+
+import numpy as np
+
+from . import _capi
+from ._capi import (ALGO_NAMES, ALGOS, BlockConv2DParams, Conv2DParams, MiqError, QConvDesc, QParamsS5,
+                    QParamsU8, check, lib)
+
+try:
+    import torch
+except ImportError:  # pragma: no cover
+    torch = None
+
+Pointer = Union[int, "torch.Tensor", None]
+
+
+class DataType(enum.IntEnum):
+    """Mirror of nnalgebra::DataType (nnalgebra_quantization.h:19-24, plus LinQuantI8)."""
+
+    Real32 = 0
+    LinQuantU8 = 1
+    LinQuantS5 = 2
+    LinQuantI32 = 3
+    LinQuantI8 = 4
+
+
+SUPPORTED_QI32_INPUTS = (DataType.LinQuantU8, DataType.LinQuantS5)
+
+# numpy views of the raw parameter structs, for building the device arrays in_qp / f_qp
+QPARAMS_U8_DTYPE = np.dtype({"names": ["zero_point", "scale", "symmetric"],
+                             "formats": [np.uint8, np.float32, np.uint8], "offsets": [0, 4, 8], "itemsize": 12})
+QPARAMS_S5_DTYPE = np.dtype({"names": ["zero_point", "n_bins", "scale"],
+                             "formats": [np.int8, np.uint8, np.float32], "offsets": [0, 1, 4], "itemsize": 8})
+
+
+def qparams_array(tin: DataType, zero_points: Sequence[int], scales: Optional[Sequence[float]] = None,
+                  n_bins: int = 0, symmetric: bool = False) -> np.ndarray:
+    """Host array of QuantizationParameters<tin> structs with the reference's byte layout."""
+    tin = DataType(tin)
+    count = len(zero_points)
+    scales = [1.0] * count if scales is None else list(scales)
+    if tin == DataType.LinQuantU8:
+        a = np.zeros(count, dtype=QPARAMS_U8_DTYPE)
+        a["zero_point"] = np.asarray(zero_points, dtype=np.int64).astype(np.uint8)
+        a["scale"] = scales
+        a["symmetric"] = 1 if symmetric else 0
+    elif tin == DataType.LinQuantS5:
+        a = np.zeros(count, dtype=QPARAMS_S5_DTYPE)
+        a["zero_point"] = np.asarray(zero_points, dtype=np.int64).astype(np.int8)
+        a["n_bins"] = n_bins
+        a["scale"] = scales
+    else:
+        raise ValueError("quantized int32 convolution supports only LinQuantU8 and LinQuantS5")
+    return a
+
+
+def _addr(t: Pointer) -> Optional[int]:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_cuda:
+        raise ValueError("tensor arguments must live in device memory")
+    if not t.is_contiguous():
+        raise ValueError("tensor arguments must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        if torch is None:
+            return None
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _as_params(p) -> Conv2DParams:
+    if p is None:
+        return Conv2DParams()
+    if isinstance(p, Conv2DParams):
+        return p
+    return Conv2DParams(*p)
+
+
+def _pair(v) -> Tuple[int, int]:
+    return (v, v) if isinstance(v, int) else (int(v[0]), int(v[1]))
+
+
+# ---- shape inference ---------------------------------------------------------------------
+
+def infer_conv_shape(n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=None) -> Tuple[int, int]:
+    """(Ho, Wo); raises MiqError with infer_conv_shape's message on a rejected shape."""
+    ho, wo = C.c_int32(), C.c_int32()
+    params = _as_params(p)
+    check(lib().miq_conv2d_output_shape(n, h, w, c, r, s, k, C.byref(params), C.byref(ho), C.byref(wo)),
+          "infer_conv_shape")
+    return ho.value, wo.value
+
+
+def infer_block_conv_shape(n, h, w, c, r, s, k, p: BlockConv2DParams) -> Tuple[int, int, int, int]:
+    """(Ho, Wo, block_ho, block_wo) with infer_block_conv_shape's rules."""
+    out = [C.c_int32() for _ in range(4)]
+    check(lib().miq_block_conv2d_output_shape(n, h, w, c, r, s, k, C.byref(p), *[C.byref(o) for o in out]),
+          "infer_block_conv_shape")
+    return tuple(o.value for o in out)
+
+
+# ---- reference-compatible int32 accumulator path ------------------------------------------
+
+def launch_fprop_nhwc_qi32(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int,
+                           r: int, s: int, k: int, p=None, in_qp: Pointer = None, f_qp: Pointer = None,
+                           stream=None) -> None:
+    """Mirror of launch_fprop_nhwc_qi32<Tin> (conv_types.h:308-323)."""
+    tin = DataType(tin)
+    if tin not in SUPPORTED_QI32_INPUTS:
+        raise TypeError("launch_fprop_nhwc_qi32 supports only LinQuantU8 and LinQuantS5")
+    if in_qp is None or f_qp is None:
+        raise RuntimeError("quantized CUDA fprop requires non-null quantization parameters")
+    fn = lib().miq_fprop_nhwc_qi32_u8 if tin == DataType.LinQuantU8 else lib().miq_fprop_nhwc_qi32_s5
+    params = _as_params(p)
+    check(fn(_addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k, C.byref(params), _addr(in_qp), _addr(f_qp),
+             _stream(stream)), "launch_fprop_nhwc_qi32")
+
+
+def launch_block_fprop_nhwc_qi32(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int,
+                                 c: int, r: int, s: int, k: int, p: BlockConv2DParams, in_qp: Pointer = None,
+                                 f_qp: Pointer = None, stream=None) -> None:
+    """Mirror of launch_block_fprop_nhwc_qi32<Tin> (conv_types.h:325-340)."""
+    tin = DataType(tin)
+    if tin not in SUPPORTED_QI32_INPUTS:
+        raise TypeError("launch_block_fprop_nhwc_qi32 supports only LinQuantU8 and LinQuantS5")
+    if in_qp is None or f_qp is None:
+        raise RuntimeError("quantized blocked CUDA fprop requires non-null quantization parameters")
+    fn = lib().miq_block_fprop_nhwc_qi32_u8 if tin == DataType.LinQuantU8 else lib().miq_block_fprop_nhwc_qi32_s5
+    check(fn(_addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k, C.byref(p), _addr(in_qp), _addr(f_qp),
+             _stream(stream)), "launch_block_fprop_nhwc_qi32")
+
+
+# ---- native int8 path -------------------------------------------------------------------
+
+def make_desc(x_shape, w_shape, *, stride=1, padding=0, dilation=1, groups=1, relu=False, in_scale=1.0,
+              out_scale=1.0, algo="auto") -> QConvDesc:
+    """Descriptor for x NHWC and w KRSC shapes."""
+    n, h, w, c = (int(v) for v in x_shape)
+    k, r, s, _ = (int(v) for v in w_shape)
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    dh, dw = _pair(dilation)
+    d = QConvDesc()
+    d.n, d.h, d.w, d.c = n, h, w, c
+    d.k, d.r, d.s = k, r, s
+    d.conv = Conv2DParams(ph, pw, sh, sw, dh, dw, groups)
+    d.relu = 1 if relu else 0
+    d.in_scale = float(in_scale)
+    d.out_scale = float(out_scale)
+    d.algo = ALGOS[algo] if isinstance(algo, str) else int(algo)
+    return d
+
+
+def plan(desc: QConvDesc) -> str:
+    """Kernel family ('igemm', 'stem' or 'direct') the int8 entry points will run."""
+    a = C.c_int32()
+    check(lib().miq_qconv2d_plan(C.byref(desc), C.byref(a)), "plan")
+    return ALGO_NAMES[a.value]
+
+
+def _out(x, w, desc: QConvDesc, dtype, out):
+    ho, wo = infer_conv_shape(desc.n, desc.h, desc.w, desc.c, desc.r, desc.s, desc.k, desc.conv)
+    shape = (desc.n, ho, wo, desc.k)
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=x.device)
+    if tuple(out.shape) != shape or out.dtype != dtype:
+        raise ValueError(f"out must be {dtype} of shape {shape}")
+    return out
+
+
+def qconv2d_nhwc_i8(x, w, bias, w_scale, *, stride=1, padding=0, dilation=1, groups=1, relu=False,
+                    in_scale=1.0, out_scale=1.0, algo="auto", out=None, stream=None):
+    """int8 NHWC output of conv + bias + per-channel requantize (+ ReLU) + saturate."""
+    desc = make_desc(x.shape, w.shape, stride=stride, padding=padding, dilation=dilation, groups=groups,
+                     relu=relu, in_scale=in_scale, out_scale=out_scale, algo=algo)
+    y = _out(x, w, desc, torch.int8, out)
+    check(lib().miq_qconv2d_nhwc_i8(C.byref(desc), _addr(x), _addr(w), _addr(bias), _addr(w_scale), _addr(y),
+                                    _stream(stream)), "qconv2d_nhwc_i8")
+    return y
+
+
+def qconv2d_nhwc_i8_acc32(x, w, *, stride=1, padding=0, dilation=1, groups=1, algo="auto", out=None,
+                          stream=None):
+    """Raw int32 accumulators of the int8 convolution."""
+    desc = make_desc(x.shape, w.shape, stride=stride, padding=padding, dilation=dilation, groups=groups, algo=algo)
+    y = _out(x, w, desc, torch.int32, out)
+    check(lib().miq_qconv2d_nhwc_i8_acc32(C.byref(desc), _addr(x), _addr(w), _addr(y), _stream(stream)),
+          "qconv2d_nhwc_i8_acc32")
+    return y
+
+
+def qconv2d_nhwc_i8_dequant(x, w, bias, w_scale, *, stride=1, padding=0, dilation=1, groups=1, relu=False,
+                            in_scale=1.0, out_scale=1.0, algo="auto", out=None, stream=None):
+    """fp32 dequantized view (float(acc + bias) * multiplier, optional ReLU)."""
+    desc = make_desc(x.shape, w.shape, stride=stride, padding=padding, dilation=dilation, groups=groups,
+                     relu=relu, in_scale=in_scale, out_scale=out_scale, algo=algo)
+    y = _out(x, w, desc, torch.float32, out)
+    check(lib().miq_qconv2d_nhwc_i8_dequant(C.byref(desc), _addr(x), _addr(w), _addr(bias), _addr(w_scale),
+                                            _addr(y), _stream(stream)), "qconv2d_nhwc_i8_dequant")
+    return y
+
+
+__all__ = [
+    "DataType", "Conv2DParams", "BlockConv2DParams", "QParamsU8", "QParamsS5", "QConvDesc", "MiqError",
+    "qparams_array", "infer_conv_shape", "infer_block_conv_shape", "launch_fprop_nhwc_qi32",
+    "launch_block_fprop_nhwc_qi32", "make_desc", "plan", "qconv2d_nhwc_i8", "qconv2d_nhwc_i8_acc32",
+    "qconv2d_nhwc_i8_dequant",
+]
+_ = _capi

@@ -1,0 +1,269 @@
+// extern "C" entry points of libmiq_qconv: host-side validation, kernel selection and
+// error reporting.  No entry point allocates device memory or touches the GPU before its
+// arguments are validated.
+
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "miq_qconv.h"
+#include "qconv_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(MIQ_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr long long kMaxDirectElems = 0xFFFFFF00LL;  // one thread per output element, 32-bit grid
+
+// Output geometry with the checks, order and messages of infer_conv_shape
+// (/root/reference/src/conv_types.h:125-146).  The filter's cin_per_group is c / groups by
+// construction on this interface (as in cuda_kernels.cu:1341-1343), so the reference's
+// "filter cin_per_group mismatch" cannot arise.  Negative extents, which the reference
+// would pass to std::vector, are rejected here; intermediate sums use 64-bit arithmetic.
+int infer_geom(int32_t n, int32_t h, int32_t w, int32_t c, int32_t r, int32_t s, int32_t k,
+               const miq_conv2d_params* p, miq::Geom* g) {
+  if (p == nullptr) return fail(MIQ_ERR_NULL_POINTER, "convolution parameters pointer is NULL");
+  if (n < 0 || h < 0 || w < 0 || c < 0 || r < 0 || s < 0 || k < 0) {
+    return fail(MIQ_ERR_INVALID_ARGUMENT, "tensor extents must be >= 0");
+  }
+  if (p->groups <= 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "groups must be > 0");
+  if (c % p->groups != 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "input channels must be divisible by groups");
+  if (k % p->groups != 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "output channels must be divisible by groups");
+  const long long rows = static_cast<long long>(h) + 2LL * p->pad_h - static_cast<long long>(p->dilation_h) * (r - 1) - 1;
+  const long long cols = static_cast<long long>(w) + 2LL * p->pad_w - static_cast<long long>(p->dilation_w) * (s - 1) - 1;
+  if (rows < 0 || cols < 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "invalid output size (negative numerator)");
+  if (p->stride_h <= 0 || p->stride_w <= 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "stride must be > 0");
+  const long long ho = rows / p->stride_h + 1;
+  const long long wo = cols / p->stride_w + 1;
+  if (ho <= 0 || wo <= 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "computed output size is <= 0");
+  if (ho > 0x7fffffffLL || wo > 0x7fffffffLL) return fail(MIQ_ERR_INVALID_ARGUMENT, "output size overflows int32");
+  g->N = n; g->H = h; g->W = w; g->C = c;
+  g->K = k; g->R = r; g->S = s;
+  g->Ho = static_cast<int>(ho); g->Wo = static_cast<int>(wo);
+  g->ph = p->pad_h; g->pw = p->pad_w;
+  g->sh = p->stride_h; g->sw = p->stride_w;
+  g->dh = p->dilation_h; g->dw = p->dilation_w;
+  g->G = p->groups; g->Cg = c / p->groups; g->Kg = k / p->groups;
+  return MIQ_OK;
+}
+
+// Blocked geometry with the rules of infer_block_conv_shape (conv_types.h:148-169).
+int infer_block_geom(int32_t n, int32_t h, int32_t w, int32_t c, int32_t r, int32_t s, int32_t k,
+                     const miq_block_conv2d_params* p, miq::Geom* g, miq::BlockGeom* bg) {
+  if (p == nullptr) return fail(MIQ_ERR_NULL_POINTER, "blocked convolution parameters pointer is NULL");
+  if (p->block_by <= 0 || p->block_bx <= 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "block_by and block_bx must be > 0");
+  const int st = infer_geom(n, h, w, c, r, s, k, &p->conv, g);
+  if (st != MIQ_OK) return st;
+  if (g->Ho % p->block_by != 0 || g->Wo % p->block_bx != 0) {
+    return fail(MIQ_ERR_INVALID_ARGUMENT, "blocked convolution requires Ho/Wo divisible by block grid");
+  }
+  bg->By = p->block_by; bg->Bx = p->block_bx;
+  bg->bho = g->Ho / p->block_by; bg->bwo = g->Wo / p->block_bx;
+  return MIQ_OK;
+}
+
+long long out_elems(const miq::Geom& g) { return static_cast<long long>(g.N) * g.Ho * g.Wo * g.K; }
+long long in_elems(const miq::Geom& g) { return static_cast<long long>(g.N) * g.H * g.W * g.C; }
+long long filt_elems(const miq::Geom& g) { return static_cast<long long>(g.K) * g.R * g.S * g.Cg; }
+
+int check_tensors(const miq::Geom& g, long long filt, const void* x, const void* w, const void* y) {
+  if (out_elems(g) > 0 && y == nullptr) return fail(MIQ_ERR_NULL_POINTER, "output pointer is NULL");
+  if (in_elems(g) > 0 && x == nullptr) return fail(MIQ_ERR_NULL_POINTER, "input pointer is NULL");
+  if (filt > 0 && w == nullptr) return fail(MIQ_ERR_NULL_POINTER, "filter pointer is NULL");
+  if (out_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "output has more than 2^32-256 elements");
+  return MIQ_OK;
+}
+
+int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const miq::Geom& g,
+               const miq::BlockGeom& bg, const void* in_qp, const void* f_qp, void* stream) {
+  const long long filt = filt_elems(g) * bg.By * bg.Bx;
+  int st = check_tensors(g, filt, x, w, y);
+  if (st != MIQ_OK) return st;
+  if (in_qp == nullptr || f_qp == nullptr) {
+    return fail(MIQ_ERR_NULL_POINTER, "quantized fprop requires non-null quantization parameters");
+  }
+  if (out_elems(g) == 0) return MIQ_OK;
+  const hipError_t e = miq::launch_qi32_direct(g, bg, qk, x, w, y, in_qp, f_qp, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "qi32 direct convolution launch");
+  return MIQ_OK;
+}
+
+// Validates an int8 problem and resolves the kernel family.
+int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y, miq::Epi epi, miq::Geom* g,
+            int32_t* algo) {
+  if (d == nullptr) return fail(MIQ_ERR_NULL_POINTER, "descriptor pointer is NULL");
+  int st = infer_geom(d->n, d->h, d->w, d->c, d->r, d->s, d->k, &d->conv, g);
+  if (st != MIQ_OK) return st;
+  std::string why;
+  switch (d->algo) {
+    case MIQ_ALGO_AUTO:
+      if (miq::igemm_eligible(*g, x, w, y, epi, nullptr)) {
+        *algo = MIQ_ALGO_IGEMM;
+      } else if (miq::stem_eligible(*g, x, w, y, epi, nullptr)) {
+        *algo = MIQ_ALGO_STEM;
+      } else {
+        *algo = MIQ_ALGO_DIRECT;
+      }
+      break;
+    case MIQ_ALGO_DIRECT:
+      *algo = MIQ_ALGO_DIRECT;
+      break;
+    case MIQ_ALGO_IGEMM:
+      if (!miq::igemm_eligible(*g, x, w, y, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_IGEMM;
+      break;
+    case MIQ_ALGO_STEM:
+      if (!miq::stem_eligible(*g, x, w, y, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_STEM;
+      break;
+    default:
+      return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
+  }
+  return MIQ_OK;
+}
+
+int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_t* w, const int32_t* bias,
+             const float* w_scale, void* y, void* stream) {
+  miq::Geom g;
+  int32_t algo = 0;
+  int st = plan_i8(d, x, w, y, epi, &g, &algo);
+  if (st != MIQ_OK) return st;
+  st = check_tensors(g, filt_elems(g), x, w, y);
+  if (st != MIQ_OK) return st;
+  miq::Requant rq{bias, w_scale, 1.0f, d->relu != 0 ? 1 : 0};
+  if (epi != miq::kEpiAcc32) {
+    if (g.K > 0 && w_scale == nullptr) return fail(MIQ_ERR_NULL_POINTER, "per-channel scale pointer is NULL");
+    if (!std::isfinite(d->in_scale) || !std::isfinite(d->out_scale) || d->out_scale == 0.0f) {
+      return fail(MIQ_ERR_INVALID_ARGUMENT, "in_scale must be finite and out_scale finite and non-zero");
+    }
+    rq.act_scale = d->in_scale / d->out_scale;
+  }
+  if (out_elems(g) == 0) return MIQ_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (algo) {
+    case MIQ_ALGO_IGEMM: e = miq::launch_i8_igemm(g, epi, x, w, y, rq, s); break;
+    case MIQ_ALGO_STEM: e = miq::launch_i8_stem(g, epi, x, w, y, rq, s); break;
+    default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
+  }
+  if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");
+  return MIQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int miq_version(void) { return MIQ_VERSION; }
+
+const char* miq_status_string(int status) {
+  switch (status) {
+    case MIQ_OK: return "success";
+    case MIQ_ERR_NULL_POINTER: return "null pointer argument";
+    case MIQ_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case MIQ_ERR_UNSUPPORTED: return "unsupported by the requested algorithm";
+    case MIQ_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+const char* miq_last_error_message(void) { return g_last_error.c_str(); }
+
+int miq_conv2d_output_shape(int32_t n, int32_t h, int32_t w, int32_t c, int32_t r, int32_t s, int32_t k,
+                            const miq_conv2d_params* p, int32_t* ho, int32_t* wo) {
+  if (ho == nullptr || wo == nullptr) return fail(MIQ_ERR_NULL_POINTER, "output shape pointer is NULL");
+  miq::Geom g;
+  const int st = infer_geom(n, h, w, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  *ho = g.Ho;
+  *wo = g.Wo;
+  return MIQ_OK;
+}
+
+int miq_block_conv2d_output_shape(int32_t n, int32_t h, int32_t w, int32_t c, int32_t r, int32_t s, int32_t k,
+                                  const miq_block_conv2d_params* p, int32_t* ho, int32_t* wo, int32_t* block_ho,
+                                  int32_t* block_wo) {
+  if (ho == nullptr || wo == nullptr || block_ho == nullptr || block_wo == nullptr) {
+    return fail(MIQ_ERR_NULL_POINTER, "output shape pointer is NULL");
+  }
+  miq::Geom g;
+  miq::BlockGeom bg;
+  const int st = infer_block_geom(n, h, w, c, r, s, k, p, &g, &bg);
+  if (st != MIQ_OK) return st;
+  *ho = g.Ho;
+  *wo = g.Wo;
+  *block_ho = bg.bho;
+  *block_wo = bg.bwo;
+  return MIQ_OK;
+}
+
+int miq_qconv2d_plan(const miq_qconv_desc* d, int32_t* algo) {
+  if (algo == nullptr) return fail(MIQ_ERR_NULL_POINTER, "algo output pointer is NULL");
+  miq::Geom g;
+  // Alignment is judged for 256-byte aligned allocations (what hipMalloc returns).
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  return plan_i8(d, kAligned, kAligned, kAligned, miq::kEpiI8, &g, algo);
+}
+
+int miq_fprop_nhwc_qi32_u8(const float* x, const float* w, int32_t* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                           int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, const miq_qparams_u8* in_qp,
+                           const miq_qparams_u8* f_qp, void* stream) {
+  miq::Geom g;
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  return qi32_entry(miq::kQpU8, x, w, y, g, miq::BlockGeom{1, 1, g.Ho, g.Wo}, in_qp, f_qp, stream);
+}
+
+int miq_fprop_nhwc_qi32_s5(const float* x, const float* w, int32_t* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                           int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, const miq_qparams_s5* in_qp,
+                           const miq_qparams_s5* f_qp, void* stream) {
+  miq::Geom g;
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  return qi32_entry(miq::kQpS5, x, w, y, g, miq::BlockGeom{1, 1, g.Ho, g.Wo}, in_qp, f_qp, stream);
+}
+
+int miq_block_fprop_nhwc_qi32_u8(const float* x, const float* w, int32_t* y, int32_t n, int32_t h, int32_t wdt,
+                                 int32_t c, int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p,
+                                 const miq_qparams_u8* in_qp, const miq_qparams_u8* f_qp, void* stream) {
+  miq::Geom g;
+  miq::BlockGeom bg;
+  const int st = infer_block_geom(n, h, wdt, c, r, s, k, p, &g, &bg);
+  if (st != MIQ_OK) return st;
+  return qi32_entry(miq::kQpU8, x, w, y, g, bg, in_qp, f_qp, stream);
+}
+
+int miq_block_fprop_nhwc_qi32_s5(const float* x, const float* w, int32_t* y, int32_t n, int32_t h, int32_t wdt,
+                                 int32_t c, int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p,
+                                 const miq_qparams_s5* in_qp, const miq_qparams_s5* f_qp, void* stream) {
+  miq::Geom g;
+  miq::BlockGeom bg;
+  const int st = infer_block_geom(n, h, wdt, c, r, s, k, p, &g, &bg);
+  if (st != MIQ_OK) return st;
+  return qi32_entry(miq::kQpS5, x, w, y, g, bg, in_qp, f_qp, stream);
+}
+
+int miq_qconv2d_nhwc_i8(const miq_qconv_desc* d, const int8_t* x, const int8_t* w, const int32_t* bias,
+                        const float* w_scale, int8_t* y, void* stream) {
+  return i8_entry(miq::kEpiI8, d, x, w, bias, w_scale, y, stream);
+}
+
+int miq_qconv2d_nhwc_i8_acc32(const miq_qconv_desc* d, const int8_t* x, const int8_t* w, int32_t* acc, void* stream) {
+  return i8_entry(miq::kEpiAcc32, d, x, w, nullptr, nullptr, acc, stream);
+}
+
+int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const int8_t* w, const int32_t* bias,
+                                const float* w_scale, float* y, void* stream) {
+  return i8_entry(miq::kEpiF32, d, x, w, bias, w_scale, y, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,91 @@
+// Internal interface between the C-ABI front end (qconv_capi.cpp) and the HIP kernel
+// translation units.  Not installed; callers use include/miq_qconv.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace miq {
+
+// Validated geometry of one grouped 2-D convolution, NHWC input / KRSC filter.
+struct Geom {
+  int N, H, W, C;      // input
+  int K, R, S;         // filter (K output channels, R x S taps)
+  int Ho, Wo;          // output spatial size
+  int ph, pw;          // padding
+  int sh, sw;          // stride
+  int dh, dw;          // dilation
+  int G, Cg, Kg;       // groups, input / output channels per group
+};
+
+// Output stage of the int8 kernels.
+enum Epi : int {
+  kEpiI8 = 0,     // requantized int8
+  kEpiAcc32 = 1,  // raw int32 accumulators
+  kEpiF32 = 2,    // dequantized fp32 view
+};
+
+// Requantization inputs; act_scale = in_scale / out_scale, computed on the host.
+struct Requant {
+  const int32_t* bias;    // int32[K] or nullptr
+  const float* wscale;    // float[K] (unused for kEpiAcc32)
+  float act_scale;
+  int relu;
+};
+
+// Blocked-filter geometry; By == Bx == 1 describes a plain KRSC filter.
+struct BlockGeom {
+  int By, Bx;          // filter blocks
+  int bho, bwo;        // output rows / cols per block
+};
+
+enum QpKind : int { kQpU8 = 0, kQpS5 = 1 };
+
+// int32 accumulators on float codes with per-sample input zero points (compat surface).
+hipError_t launch_qi32_direct(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w,
+                              int32_t* y, const void* in_qp, const void* f_qp, hipStream_t stream);
+
+// int8 VALU direct convolution: any geometry.
+hipError_t launch_i8_direct(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                            hipStream_t stream);
+
+// int8 MFMA implicit GEMM: (C/groups) % 16 == 0, stride/dilation >= 1, padding >= 0.
+bool igemm_eligible(const Geom& g, const void* x, const void* w, const void* y, Epi epi, std::string* why);
+hipError_t launch_i8_igemm(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                           hipStream_t stream);
+
+// int8 MFMA thin-channel kernel for stems: groups == 1, C < 16.
+bool stem_eligible(const Geom& g, const void* x, const void* w, const void* y, Epi epi, std::string* why);
+hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                          hipStream_t stream);
+
+#if defined(__HIPCC__)
+// ---- epilogue arithmetic shared by every int8 kernel --------------------------------
+// Each step is one IEEE-754 single operation with round-to-nearest-even, in this order,
+// so the GPU result equals the host restatement bit for bit (no contraction: the
+// translation units are compiled with -ffp-contract=off and no step is a*b+c).
+
+__device__ __forceinline__ float requant_multiplier(float act_scale, float wscale) {
+  return act_scale * wscale;
+}
+
+__device__ __forceinline__ int requant_i8(int32_t acc, int32_t bias, float m, float lo) {
+  const int32_t t = static_cast<int32_t>(static_cast<uint32_t>(acc) + static_cast<uint32_t>(bias));
+  const float v = static_cast<float>(t) * m;
+  float q = __builtin_rintf(v);
+  q = (q >= lo) ? q : lo;          // NaN -> lo
+  q = (q > 127.0f) ? 127.0f : q;
+  return static_cast<int>(q);
+}
+
+__device__ __forceinline__ float dequant_f32(int32_t acc, int32_t bias, float m, int relu) {
+  const int32_t t = static_cast<int32_t>(static_cast<uint32_t>(acc) + static_cast<uint32_t>(bias));
+  float v = static_cast<float>(t) * m;
+  if (relu) v = (v > 0.0f) ? v : 0.0f;  // NaN and -0 -> +0
+  return v;
+}
+#endif
+
+}  // namespace miq

@@ -1,0 +1,213 @@
+"""CPU oracle of the quantized NHWC convolution - TEST INFRASTRUCTURE ONLY.
+
+Loads oracle/liborc.so (the C restatement in qconv_oracle.c) and, when it was built,
+oracle/_ref/libref_cpu.so (the reference's own cpu_ref.cpp, see oracle/Makefile).  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package;
+the product never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORC_PATH = HERE / "liborc.so"
+REF_PATH = HERE / "_ref" / "libref_cpu.so"
+
+_orc = None
+_ref = None
+
+_P = C.c_void_p
+_I = C.c_int32
+
+
+def build(reference_root: str = "/root/reference") -> None:
+    """make -C oracle (the reference build only happens where its sources exist)."""
+    subprocess.run(["make", "-C", str(HERE), "--no-print-directory", f"REF={reference_root}"], check=True,
+                   stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+
+
+def orc() -> C.CDLL:
+    global _orc
+    if _orc is None:
+        if not ORC_PATH.exists():
+            build()
+        h = C.CDLL(str(ORC_PATH))
+        h.orc_splitmix64.restype = C.c_uint64
+        h.orc_splitmix64.argtypes = [C.c_uint64, C.c_uint64]
+        h.orc_fill_i8_uniform.argtypes = [_P, C.c_int64, C.c_uint64, _I, _I]
+        h.orc_fill_i8_relu_half.argtypes = [_P, C.c_int64, C.c_uint64]
+        h.orc_fill_i32_uniform.argtypes = [_P, C.c_int64, C.c_uint64, _I, _I]
+        h.orc_fill_f32_uniform.argtypes = [_P, C.c_int64, C.c_uint64, C.c_float, C.c_float]
+        h.orc_conv_output_shape.argtypes = [_I] * 7 + [_P, _P, _P]
+        h.orc_conv_qi32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I, _I, _I, _P]
+        h.orc_conv_i8_acc.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
+        h.orc_requant_i8.argtypes = [_P, C.c_int64, _I, _P, _P, C.c_float, C.c_float, _I, _P]
+        h.orc_dequant_f32.argtypes = [_P, C.c_int64, _I, _P, _P, C.c_float, C.c_float, _I, _P]
+        _orc = h
+    return _orc
+
+
+def ref() -> Optional[C.CDLL]:
+    """The reference's compiled cpu_ref.cpp, or None where it was not built."""
+    global _ref
+    if _ref is None and REF_PATH.exists():
+        h = C.CDLL(str(REF_PATH))
+        h.ref_last_error.restype = C.c_char_p
+        h.ref_fprop_qi32.argtypes = [C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int,
+                                     _P, _P, _I, C.c_int, C.c_int, _P, _P]
+        h.ref_verify_tensors.argtypes = [_P, _P, C.c_size_t, C.c_float, C.c_float, _P, _P, _P, _P, _P]
+        _ref = h
+    return _ref
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data
+
+
+def _conv7(conv: Sequence[int]) -> np.ndarray:
+    a = np.ascontiguousarray(conv, dtype=np.int32)
+    assert a.shape == (7,)
+    return a
+
+
+# ---- generator -------------------------------------------------------------------------
+
+def splitmix64(seed: int, i: int) -> int:
+    return int(orc().orc_splitmix64(seed, i))
+
+
+def fill_i8_uniform(count, seed, lo, hi):
+    out = np.empty(count, np.int8)
+    orc().orc_fill_i8_uniform(_p(out), count, seed, lo, hi)
+    return out
+
+
+def fill_i8_relu_half(count, seed):
+    out = np.empty(count, np.int8)
+    orc().orc_fill_i8_relu_half(_p(out), count, seed)
+    return out
+
+
+def fill_i32_uniform(count, seed, lo, hi):
+    out = np.empty(count, np.int32)
+    orc().orc_fill_i32_uniform(_p(out), count, seed, lo, hi)
+    return out
+
+
+def fill_f32_uniform(count, seed, lo, hi):
+    out = np.empty(count, np.float32)
+    orc().orc_fill_f32_uniform(_p(out), count, seed, lo, hi)
+    return out
+
+
+# ---- convolution -----------------------------------------------------------------------
+
+def conv_output_shape(n, h, w, c, r, s, k, conv) -> Optional[Tuple[int, int]]:
+    ho, wo = C.c_int32(), C.c_int32()
+    cv = _conv7(conv)
+    if orc().orc_conv_output_shape(n, h, w, c, r, s, k, _p(cv), C.byref(ho), C.byref(wo)) != 0:
+        return None
+    return ho.value, wo.value
+
+
+def conv_qi32(x: np.ndarray, wt: np.ndarray, conv, in_zp, f_zp: int, block=(0, 0)) -> np.ndarray:
+    """int32 accumulators on float codes; x NHWC float32, wt KRSC (or K,By,Bx,R,S,C) float32."""
+    x = np.ascontiguousarray(x, np.float32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    n, h, w, c = x.shape
+    k = wt.shape[0]
+    r, s = wt.shape[-3], wt.shape[-2]
+    cv = _conv7(conv)
+    shp = conv_output_shape(n, h, w, c, r, s, k, cv)
+    if shp is None:
+        raise ValueError("rejected shape")
+    zp = np.ascontiguousarray(in_zp, np.int32)
+    assert zp.shape == (n,)
+    y = np.empty((n, shp[0], shp[1], k), np.int32)
+    by, bx = block
+    if orc().orc_conv_qi32(_p(x), n, h, w, c, _p(wt), r, s, k, _p(cv), _p(zp), int(f_zp), by, bx, _p(y)) != 0:
+        raise ValueError("rejected shape")
+    return y
+
+
+def conv_i8_acc(x: np.ndarray, wt: np.ndarray, conv, nthreads: int = 0) -> np.ndarray:
+    """int32 accumulators of int8 codes (zero points 0); x NHWC, wt KRSC."""
+    x = np.ascontiguousarray(x, np.int8)
+    wt = np.ascontiguousarray(wt, np.int8)
+    n, h, w, c = x.shape
+    k, r, s, _ = wt.shape
+    cv = _conv7(conv)
+    shp = conv_output_shape(n, h, w, c, r, s, k, cv)
+    if shp is None:
+        raise ValueError("rejected shape")
+    y = np.empty((n, shp[0], shp[1], k), np.int32)
+    if orc().orc_conv_i8_acc(_p(x), n, h, w, c, _p(wt), r, s, k, _p(cv), _p(y), nthreads) != 0:
+        raise ValueError("rejected shape")
+    return y
+
+
+def requant_i8(acc: np.ndarray, bias, w_scale, in_scale, out_scale, relu) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, np.int32)
+    k = acc.shape[-1]
+    b = None if bias is None else np.ascontiguousarray(bias, np.int32)
+    ws = np.ascontiguousarray(w_scale, np.float32)
+    y = np.empty(acc.shape, np.int8)
+    orc().orc_requant_i8(_p(acc), acc.size // k, k, _p(b), _p(ws), in_scale, out_scale, 1 if relu else 0, _p(y))
+    return y
+
+
+def dequant_f32(acc: np.ndarray, bias, w_scale, in_scale, out_scale, relu) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, np.int32)
+    k = acc.shape[-1]
+    b = None if bias is None else np.ascontiguousarray(bias, np.int32)
+    ws = np.ascontiguousarray(w_scale, np.float32)
+    y = np.empty(acc.shape, np.float32)
+    orc().orc_dequant_f32(_p(acc), acc.size // k, k, _p(b), _p(ws), in_scale, out_scale, 1 if relu else 0, _p(y))
+    return y
+
+
+# ---- the reference's own CPU path --------------------------------------------------------
+
+def ref_conv_qi32(kind: str, x, wt, conv, in_zp, f_zp, block=(0, 0)) -> Tuple[np.ndarray, float]:
+    """(int32 output, seconds) of the reference's cpu_(block_)fprop_nhwc_qi32<kind>."""
+    h = ref()
+    if h is None:
+        raise RuntimeError("oracle/_ref/libref_cpu.so was not built")
+    x = np.ascontiguousarray(x, np.float32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    n, hh, w, c = x.shape
+    k = wt.shape[0]
+    r, s = wt.shape[-3], wt.shape[-2]
+    cv = _conv7(conv)
+    shp = conv_output_shape(n, hh, w, c, r, s, k, cv)
+    if shp is None:
+        raise ValueError("rejected shape")
+    y = np.empty((n, shp[0], shp[1], k), np.int32)
+    zp = np.ascontiguousarray(in_zp, np.int32)
+    secs = C.c_double()
+    st = h.ref_fprop_qi32(0 if kind == "u8" else 1, _p(x), n, hh, w, c, _p(wt), r, s, k, _p(cv), _p(zp), int(f_zp),
+                          block[0], block[1], _p(y), C.byref(secs))
+    if st != 0:
+        raise RuntimeError(h.ref_last_error().decode())
+    return y, secs.value
+
+
+def ref_verify_tensors(refv, got, abs_eps, rel_eps) -> dict:
+    h = ref()
+    if h is None:
+        raise RuntimeError("oracle/_ref/libref_cpu.so was not built")
+    a = np.ascontiguousarray(refv, np.float32)
+    b = np.ascontiguousarray(got, np.float32)
+    ma, mr = C.c_float(), C.c_float()
+    ia, ir = C.c_size_t(), C.c_size_t()
+    ok = C.c_int()
+    if h.ref_verify_tensors(_p(a), _p(b), a.size, abs_eps, rel_eps, C.byref(ma), C.byref(mr), C.byref(ia),
+                            C.byref(ir), C.byref(ok)) != 0:
+        raise RuntimeError(h.ref_last_error().decode())
+    return {"max_abs_err": ma.value, "max_rel_err": mr.value, "max_abs_idx": ia.value, "max_rel_idx": ir.value,
+            "passed": bool(ok.value)}

@@ -1,0 +1,229 @@
+/*
+ * qconv_oracle.c - CPU restatement of the reference's quantized NHWC convolution.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker of the HIP library (see qconv_oracle.h).  Not
+ * part of the product; nothing in my_own_cnn_amd/ links or calls it.
+ *
+ * Pinning (the checks that hold this restatement to the reference, in tests/):
+ *   orc_conv_qi32        golden vectors from the reference's own cpu_ref.cpp compiled in
+ *                        this repository (oracle/_ref), the four quant_conv_test cases,
+ *                        float64 convolution, brute force and conv identities.
+ *   orc_conv_i8_acc      the same, plus C1 in full and C2-C5 hashes from oracle/_ref.
+ *   orc_requant_i8 /     no reference counterpart (the reference has no requantization):
+ *   orc_dequant_f32      hand-computed known answers and float64 bounds.
+ *   orc_fill_*           fixed known outputs of splitmix64.
+ */
+#include "qconv_oracle.h"
+
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---- synthetic data -------------------------------------------------------------- */
+
+/* splitmix64 (Steele, Lea, Flood 2014): state_i = seed + (i+1) * 0x9E3779B97F4A7C15,
+ * output = the mixing finaliser of state_i. */
+uint64_t orc_splitmix64(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1u) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+/* lo + floor(hi32(u) * (hi - lo + 1) / 2^32) */
+void orc_fill_i8_uniform(int8_t* out, int64_t count, uint64_t seed, int32_t lo, int32_t hi) {
+  const uint64_t range = (uint64_t)((int64_t)hi - lo + 1);
+  for (int64_t i = 0; i < count; ++i) {
+    const uint64_t u = orc_splitmix64(seed, (uint64_t)i);
+    out[i] = (int8_t)(lo + (int32_t)(((u >> 32) * range) >> 32));
+  }
+}
+
+/* post-ReLU activations: 0 when the top bit is clear, else 1 + floor(lo32(u) * 127 / 2^32) */
+void orc_fill_i8_relu_half(int8_t* out, int64_t count, uint64_t seed) {
+  for (int64_t i = 0; i < count; ++i) {
+    const uint64_t u = orc_splitmix64(seed, (uint64_t)i);
+    out[i] = (u >> 63) ? (int8_t)(1 + (int32_t)(((u & 0xffffffffull) * 127u) >> 32)) : (int8_t)0;
+  }
+}
+
+void orc_fill_i32_uniform(int32_t* out, int64_t count, uint64_t seed, int32_t lo, int32_t hi) {
+  const uint64_t range = (uint64_t)((int64_t)hi - lo + 1);
+  for (int64_t i = 0; i < count; ++i) {
+    const uint64_t u = orc_splitmix64(seed, (uint64_t)i);
+    out[i] = (int32_t)((int64_t)lo + (int64_t)(((u >> 32) * range) >> 32));
+  }
+}
+
+/* lo + f * (hi - lo) in single precision, f = top 24 bits of u / 2^24 (exact in fp32) */
+void orc_fill_f32_uniform(float* out, int64_t count, uint64_t seed, float lo, float hi) {
+  const float span = hi - lo;
+  for (int64_t i = 0; i < count; ++i) {
+    const uint64_t u = orc_splitmix64(seed, (uint64_t)i);
+    const float f = (float)(u >> 40) * 0x1p-24f;
+    const float t = f * span;
+    out[i] = lo + t;
+  }
+}
+
+/* ---- shape ------------------------------------------------------------------------- */
+
+/* Follows infer_conv_shape (/root/reference/src/conv_types.h:125-146). */
+int orc_conv_output_shape(int32_t n, int32_t h, int32_t w, int32_t c, int32_t r, int32_t s, int32_t k,
+                          const int32_t conv[7], int32_t* ho, int32_t* wo) {
+  (void)n;
+  const int32_t groups = conv[6];
+  if (groups <= 0 || c % groups != 0 || k % groups != 0) return -1;
+  const int64_t rows = (int64_t)h + 2 * (int64_t)conv[0] - (int64_t)conv[4] * (r - 1) - 1;
+  const int64_t cols = (int64_t)w + 2 * (int64_t)conv[1] - (int64_t)conv[5] * (s - 1) - 1;
+  if (rows < 0 || cols < 0) return -1;
+  if (conv[2] <= 0 || conv[3] <= 0) return -1;
+  *ho = (int32_t)(rows / conv[2] + 1);
+  *wo = (int32_t)(cols / conv[3] + 1);
+  if (*ho <= 0 || *wo <= 0) return -1;
+  return 0;
+}
+
+/* ---- int32 accumulation ------------------------------------------------------------ */
+
+/* Follows cpu_fprop_nhwc_qi32_impl and cpu_block_fprop_nhwc_qi32_impl
+ * (/root/reference/src/cpu_ref.cpp:36-112) with the helpers they call
+ * (centered_input_value :11-17, centered_weight_value :19-25,
+ * centered_block_weight_value :27-34, output_block_index :7-9): loop order
+ * n, ho, wo, g, ko, r, s, ci; codes truncated to int32; taps outside the input skipped;
+ * the sample's zero point subtracted from inputs and the filter's from weights;
+ * output channel g*Kg + ko.  Sums use unsigned (wrap-around) arithmetic, which equals the
+ * reference's int32 result whenever the reference's is defined. */
+int orc_conv_qi32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r,
+                  int32_t s, int32_t k, const int32_t conv[7], const int32_t* in_zp, int32_t f_zp, int32_t by,
+                  int32_t bx, int32_t* y) {
+  int32_t ho_n, wo_n;
+  if (orc_conv_output_shape(n, h, w, c, r, s, k, conv, &ho_n, &wo_n) != 0) return -1;
+  const int blocked = (by > 0 && bx > 0);
+  if (blocked && (ho_n % by != 0 || wo_n % bx != 0)) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int32_t bho = blocked ? ho_n / by : 1, bwo = blocked ? wo_n / bx : 1;
+  for (int32_t ni = 0; ni < n; ++ni) {
+    for (int32_t ho = 0; ho < ho_n; ++ho) {
+      const int32_t byi = blocked ? ho / bho : 0;
+      for (int32_t wo = 0; wo < wo_n; ++wo) {
+        const int32_t bxi = blocked ? wo / bwo : 0;
+        for (int32_t g = 0; g < g_n; ++g) {
+          for (int32_t ko = 0; ko < kg; ++ko) {
+            const int32_t kk = g * kg + ko;
+            uint32_t acc = 0;
+            for (int32_t rr = 0; rr < r; ++rr) {
+              const int32_t hi = ho * sh - ph + rr * dh;
+              if (hi < 0 || hi >= h) continue;
+              for (int32_t ss = 0; ss < s; ++ss) {
+                const int32_t wi = wo * sw - pw + ss * dw;
+                if (wi < 0 || wi >= w) continue;
+                for (int32_t ci = 0; ci < cg; ++ci) {
+                  const size_t xi = (((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg + ci;
+                  size_t wj;
+                  if (blocked) {
+                    wj = (((((size_t)kk * by + byi) * bx + bxi) * r + rr) * s + ss) * cg + ci;
+                  } else {
+                    wj = (((size_t)kk * r + rr) * s + ss) * cg + ci;
+                  }
+                  const int32_t xv = (int32_t)x[xi] - in_zp[ni];
+                  const int32_t wv = (int32_t)wt[wj] - f_zp;
+                  acc += (uint32_t)xv * (uint32_t)wv;
+                }
+              }
+            }
+            y[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + kk] = (int32_t)acc;
+          }
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* The same accumulation (cpu_ref.cpp:36-72) for int8 codes with zero points 0; output
+ * rows (n, ho) are independent and are spread over OpenMP threads. */
+int orc_conv_i8_acc(const int8_t* x, int32_t n, int32_t h, int32_t w, int32_t c, const int8_t* wt, int32_t r,
+                    int32_t s, int32_t k, const int32_t conv[7], int32_t* y, int32_t nthreads) {
+  int32_t ho_n, wo_n;
+  if (orc_conv_output_shape(n, h, w, c, r, s, k, conv, &ho_n, &wo_n) != 0) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int64_t nrows = (int64_t)n * ho_n;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t row = 0; row < nrows; ++row) {
+    const int32_t ni = (int32_t)(row / ho_n);
+    const int32_t ho = (int32_t)(row % ho_n);
+    for (int32_t wo = 0; wo < wo_n; ++wo) {
+      for (int32_t g = 0; g < g_n; ++g) {
+        for (int32_t ko = 0; ko < kg; ++ko) {
+          const int32_t kk = g * kg + ko;
+          uint32_t acc = 0;
+          for (int32_t rr = 0; rr < r; ++rr) {
+            const int32_t hi = ho * sh - ph + rr * dh;
+            if (hi < 0 || hi >= h) continue;
+            for (int32_t ss = 0; ss < s; ++ss) {
+              const int32_t wi = wo * sw - pw + ss * dw;
+              if (wi < 0 || wi >= w) continue;
+              const int8_t* xp = x + (((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg;
+              const int8_t* wp = wt + (((size_t)kk * r + rr) * s + ss) * cg;
+              int32_t dot = 0; /* |dot| <= cg * 2^14: exact for any cg < 2^17 */
+              for (int32_t ci = 0; ci < cg; ++ci) dot += (int32_t)xp[ci] * (int32_t)wp[ci];
+              acc += (uint32_t)dot;
+            }
+          }
+          y[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + kk] = (int32_t)acc;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* ---- requantization (no reference counterpart) ------------------------------------- */
+
+/* a = in_scale / out_scale; m = a * w_scale[k]; v = (float)(acc + bias[k]) * m;
+ * q = rint(v) with ties to even; q < lo (or NaN) -> lo; q > 127 -> 127. */
+void orc_requant_i8(const int32_t* acc, int64_t npix, int32_t k, const int32_t* bias, const float* w_scale,
+                    float in_scale, float out_scale, int32_t relu, int8_t* y) {
+  const float a = in_scale / out_scale;
+  const float lo = relu ? 0.0f : -128.0f;
+  for (int64_t p = 0; p < npix; ++p) {
+    for (int32_t kk = 0; kk < k; ++kk) {
+      const size_t i = (size_t)p * k + kk;
+      const float m = a * w_scale[kk];
+      const int32_t t = (int32_t)((uint32_t)acc[i] + (uint32_t)(bias ? bias[kk] : 0));
+      const float v = (float)t * m;
+      float q = rintf(v); /* default rounding mode: to nearest, ties to even */
+      q = (q >= lo) ? q : lo;
+      q = (q > 127.0f) ? 127.0f : q;
+      y[i] = (int8_t)(int32_t)q;
+    }
+  }
+}
+
+/* v = (float)(acc + bias[k]) * m; with relu, v <= 0 or NaN becomes +0. */
+void orc_dequant_f32(const int32_t* acc, int64_t npix, int32_t k, const int32_t* bias, const float* w_scale,
+                     float in_scale, float out_scale, int32_t relu, float* y) {
+  const float a = in_scale / out_scale;
+  for (int64_t p = 0; p < npix; ++p) {
+    for (int32_t kk = 0; kk < k; ++kk) {
+      const size_t i = (size_t)p * k + kk;
+      const float m = a * w_scale[kk];
+      const int32_t t = (int32_t)((uint32_t)acc[i] + (uint32_t)(bias ? bias[kk] : 0));
+      float v = (float)t * m;
+      if (relu) v = (v > 0.0f) ? v : 0.0f;
+      y[i] = v;
+    }
+  }
+}

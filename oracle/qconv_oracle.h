@@ -1,0 +1,53 @@
+/*
+ * qconv_oracle.h - CPU restatement of the reference's quantized NHWC convolution.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the HIP library is compared against;
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The product (libmiq_qconv) never links, calls or falls back to it.
+ */
+#ifndef QCONV_ORACLE_H_
+#define QCONV_ORACLE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* conv[7] = {pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, groups} */
+
+/* Deterministic synthetic data: splitmix64 output number i of the stream `seed`. */
+uint64_t orc_splitmix64(uint64_t seed, uint64_t i);
+void orc_fill_i8_uniform(int8_t* out, int64_t count, uint64_t seed, int32_t lo, int32_t hi);
+void orc_fill_i8_relu_half(int8_t* out, int64_t count, uint64_t seed);
+void orc_fill_i32_uniform(int32_t* out, int64_t count, uint64_t seed, int32_t lo, int32_t hi);
+void orc_fill_f32_uniform(float* out, int64_t count, uint64_t seed, float lo, float hi);
+
+/* Output size with the rules of infer_conv_shape; 0 on success, -1 on a rejected shape. */
+int orc_conv_output_shape(int32_t n, int32_t h, int32_t w, int32_t c, int32_t r, int32_t s, int32_t k,
+                          const int32_t conv[7], int32_t* ho, int32_t* wo);
+
+/* int32 accumulators on float codes with per-sample input zero points in_zp[n] and one
+ * filter zero point; by = bx = 0 selects the plain KRSC filter, by, bx > 0 the blocked
+ * [K, By, Bx, R, S, C/groups] filter.  Returns 0, or -1 on a rejected shape. */
+int orc_conv_qi32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r,
+                  int32_t s, int32_t k, const int32_t conv[7], const int32_t* in_zp, int32_t f_zp, int32_t by,
+                  int32_t bx, int32_t* y);
+
+/* int32 accumulators of int8 codes (zero points 0), on `nthreads` OpenMP threads
+ * (<= 0: the OpenMP default). */
+int orc_conv_i8_acc(const int8_t* x, int32_t n, int32_t h, int32_t w, int32_t c, const int8_t* wt, int32_t r,
+                    int32_t s, int32_t k, const int32_t conv[7], int32_t* y, int32_t nthreads);
+
+/* Requantization / dequantization of `npix` pixels x k channels of accumulators, with the
+ * arithmetic defined in include/miq_qconv.h. bias may be NULL. */
+void orc_requant_i8(const int32_t* acc, int64_t npix, int32_t k, const int32_t* bias, const float* w_scale,
+                    float in_scale, float out_scale, int32_t relu, int8_t* y);
+void orc_dequant_f32(const int32_t* acc, int64_t npix, int32_t k, const int32_t* bias, const float* w_scale,
+                     float in_scale, float out_scale, int32_t relu, float* y);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QCONV_ORACLE_H_ */

@@ -1,0 +1,136 @@
+// ref_shim.cpp - extern "C" access to the reference's own CPU path, compiled from the
+// reference's sources where they lie (see oracle/Makefile; output in oracle/_ref/).
+//
+// TEST INFRASTRUCTURE ONLY: used by tests/ (golden vectors, oracle pinning) and by
+// bench.py's cpu_baseline leg.  Builds the reference's TensorNHWC / FilterKRSC /
+// BlockFilterKByBxRSC from flat arrays, calls cpu_fprop_nhwc_qi32<Tin> /
+// cpu_block_fprop_nhwc_qi32<Tin> (/root/reference/src/conv_types.h:255-285 ->
+// cpu_ref.cpp:36-112, :371-401) and verify_tensors (src/verify.cpp:7-36).
+
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <string>
+#include <vector>
+
+#include "conv_types.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+using nnalgebra::DataType;
+template <DataType T>
+using QP = nnalgebra::QuantizationParameters<T>;
+
+Conv2DParams to_params(const int32_t conv[7]) {
+  Conv2DParams p;
+  p.pad_h = conv[0]; p.pad_w = conv[1];
+  p.stride_h = conv[2]; p.stride_w = conv[3];
+  p.dilation_h = conv[4]; p.dilation_w = conv[5];
+  p.groups = conv[6];
+  return p;
+}
+
+template <DataType T>
+std::vector<QP<T>> input_qparams(int n, const int32_t* zp) {
+  std::vector<QP<T>> qp(static_cast<size_t>(n));
+  for (int i = 0; i < n; ++i) qp[static_cast<size_t>(i)].zero_point = static_cast<decltype(qp[0].zero_point)>(zp[i]);
+  return qp;
+}
+
+template <DataType T>
+int run(const float* x, int n, int h, int w, int c, const float* wt, int r, int s, int k, const int32_t conv[7],
+        const int32_t* in_zp, int32_t f_zp, int by, int bx, int32_t* y, double* seconds) {
+  try {
+    const Conv2DParams p = to_params(conv);
+    TensorNHWC xt(n, h, w, c);
+    std::memcpy(xt.ptr(), x, xt.elements() * sizeof(float));
+    const auto iq = input_qparams<T>(n, in_zp);
+    QP<T> fq;
+    fq.zero_point = static_cast<decltype(fq.zero_point)>(f_zp);
+    TensorNHWCI32 yt;
+    const int cg = (p.groups > 0) ? c / p.groups : 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    if (by > 0 && bx > 0) {
+      BlockConv2DParams bp;
+      bp.conv = p;
+      bp.block_by = by;
+      bp.block_bx = bx;
+      BlockFilterKByBxRSC ft(k, by, bx, r, s, cg);
+      std::memcpy(ft.ptr(), wt, ft.elements() * sizeof(float));
+      const auto t1 = std::chrono::steady_clock::now();
+      cpu_block_fprop_nhwc_qi32<T>(xt, ft, bp, yt, iq.data(), &fq);
+      if (seconds) *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+    } else {
+      FilterKRSC ft(r, s, cg, k);
+      std::memcpy(ft.ptr(), wt, ft.elements() * sizeof(float));
+      const auto t1 = std::chrono::steady_clock::now();
+      cpu_fprop_nhwc_qi32<T>(xt, ft, p, yt, iq.data(), &fq);
+      if (seconds) *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+    }
+    (void)t0;
+    std::memcpy(y, yt.ptr(), yt.elements() * sizeof(int32_t));
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error(void) { return g_err.c_str(); }
+
+// kind 0: LinQuantU8, 1: LinQuantS5.  by = bx = 0: regular filter.  `seconds` (nullable)
+// receives the wall time of the reference call alone.
+int ref_fprop_qi32(int kind, const float* x, int n, int h, int w, int c, const float* wt, int r, int s, int k,
+                   const int32_t conv[7], const int32_t* in_zp, int32_t f_zp, int by, int bx, int32_t* y,
+                   double* seconds) {
+  if (kind == 0) return run<DataType::LinQuantU8>(x, n, h, w, c, wt, r, s, k, conv, in_zp, f_zp, by, bx, y, seconds);
+  return run<DataType::LinQuantS5>(x, n, h, w, c, wt, r, s, k, conv, in_zp, f_zp, by, bx, y, seconds);
+}
+
+int ref_verify_tensors(const float* ref, const float* got, size_t count, float abs_eps, float rel_eps,
+                       float* max_abs, float* max_rel, size_t* abs_idx, size_t* rel_idx, int* passed) {
+  try {
+    const std::vector<float> a(ref, ref + count), b(got, got + count);
+    const VerifyResult v = verify_tensors(a, b, abs_eps, rel_eps);
+    *max_abs = v.max_abs_err; *max_rel = v.max_rel_err;
+    *abs_idx = v.max_abs_idx; *rel_idx = v.max_rel_idx;
+    *passed = v.passed ? 1 : 0;
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+}  // extern "C"
+
+extern "C" {
+
+// infer_conv_shape of the reference header (conv_types.h:125-146) on a tensor / filter of
+// the given extents: 0 and (ho, wo), or -1 and the exception text in ref_last_error().
+int ref_infer_conv_shape(int n, int h, int w, int c, int r, int s, int k, const int32_t conv[7], int* ho, int* wo) {
+  try {
+    const Conv2DParams p = to_params(conv);
+    TensorNHWC x;  // extents only: no allocation
+    x.n = n; x.h = h; x.w = w; x.c = c;
+    FilterKRSC f;
+    f.r = r; f.s = s; f.k = k;
+    f.cin_per_group = (p.groups > 0) ? c / p.groups : 0;
+    const ConvShape sh = infer_conv_shape(x, f, p);
+    *ho = sh.ho;
+    *wo = sh.wo;
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+}  // extern "C"

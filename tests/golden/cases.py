@@ -1,0 +1,60 @@
+"""Loaders of the committed golden fixtures (inputs regenerated where the fixture stores
+only outputs).  Shared by the CPU and GPU tests."""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+
+from tests.golden.make_golden import (FILTER_ZP, INT8_SHAPES, input_zero_points, int8_case_inputs,
+                                      quant_codes)
+
+HERE = Path(__file__).resolve().parent
+
+
+def quant_conv_test_cases():
+    """name -> dict(kind, x, w, conv, zp, fzp, block, y) of the reference's four cases."""
+    exp = np.load(HERE / "quant_conv_test.npz")
+    out = {}
+    for kind in ("u8", "s5"):
+        out[f"regular_{kind}"] = dict(
+            kind=kind, x=quant_codes(kind, 240, 1).reshape(2, 5, 6, 4), w=quant_codes(kind, 72, 7).reshape(6, 3, 2, 2),
+            conv=(1, 0, 1, 1, 1, 1, 2), zp=input_zero_points(kind, 2), fzp=FILTER_ZP[kind], block=(0, 0),
+            y=exp[f"regular_{kind}"])
+        out[f"blocked_{kind}"] = dict(
+            kind=kind, x=quant_codes(kind, 288, 3).reshape(2, 6, 6, 4),
+            w=quant_codes(kind, 1080, 9).reshape(5, 2, 3, 3, 3, 4), conv=(1, 1, 1, 1, 1, 1, 1),
+            zp=input_zero_points(kind, 2), fzp=FILTER_ZP[kind], block=(2, 3), y=exp[f"blocked_{kind}"])
+    return out
+
+
+def qi32_cases():
+    z = np.load(HERE / "qi32_cases.npz")
+    names = sorted({k.split("/")[0] for k in z.files})
+    out = {}
+    for nm in names:
+        d = {k.split("/")[1]: z[k] for k in z.files if k.split("/")[0] == nm}
+        out[nm] = dict(kind=str(d["kind"]), x=d["x"], w=d["w"], conv=tuple(int(v) for v in d["conv"]),
+                       zp=d["zp"], fzp=int(d["fzp"]), block=tuple(int(v) for v in d["block"]), y=d["y"])
+    return out
+
+
+def int8_cases():
+    z = np.load(HERE / "int8_cases.npz")
+    out = {}
+    for idx, (name, xshape, wshape3, conv) in enumerate(INT8_SHAPES):
+        k, r, s = wshape3
+        wshape = (k, r, s, xshape[3] // conv[6])
+        x, w = int8_case_inputs(idx, name, xshape, wshape)
+        out[name] = dict(x=x, w=w, conv=tuple(conv), y=z[f"{name}/y"])
+    return out
+
+
+def config_goldens():
+    with open(HERE / "configs.json") as f:
+        return json.load(f)
+
+
+def c1_acc():
+    return np.load(HERE / "c1_tiny.npz")["acc"]

@@ -1,0 +1,223 @@
+"""The C-ABI library without a GPU: it loads, exports every declared symbol (C and the
+C++ drop-in ABI), and validates arguments on the host exactly like the reference."""
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+import my_own_cnn_amd as M
+from my_own_cnn_amd import _capi
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def exported():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(M.LIB_PATH)], check=True, capture_output=True,
+                         text=True).stdout
+    return {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+
+
+def declared_c_functions():
+    text = (ROOT / "include" / "miq_qconv.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(miq_[a-z0-9_]+)\s*\(", text))
+
+
+def test_every_declared_c_symbol_is_exported_and_bound():
+    decl = declared_c_functions()
+    assert len(decl) >= 13
+    assert decl <= exported()
+    assert decl == set(_capi.SIGNATURES)
+    lib = M.lib()
+    for name in decl:
+        assert getattr(lib, name) is not None
+    assert lib.miq_version() == 100
+
+
+def test_cpp_dropin_abi_is_exported():
+    # mangled names a caller compiled against the reference's own conv_types.h needs
+    need = set((GOLDEN / "dropin_symbols.txt").read_text().split())
+    assert len(need) == 6
+    assert need <= exported()
+
+
+def test_cpp_additions_are_exported():
+    demangled = subprocess.run(["c++filt"], input="\n".join(sorted(exported())), capture_output=True,
+                               text=True).stdout
+    for fn in ["launch_fprop_nhwc_qi8(", "launch_fprop_nhwc_qi8_acc32(", "launch_fprop_nhwc_qi8_dequant(",
+               "HipEventTimer::start()", "HipEventTimer::stop_ms()"]:
+        assert fn in demangled, fn
+
+
+def test_no_cpu_convolution_in_the_product():
+    syms = exported()
+    assert not any("cpu_fprop" in s or "orc_" in s for s in syms)
+
+
+def test_status_strings():
+    lib = M.lib()
+    assert lib.miq_status_string(0) == b"success"
+    assert lib.miq_status_string(3) == b"unsupported by the requested algorithm"
+    assert lib.miq_status_string(99) == b"unknown status"
+
+
+SHAPES = [
+    # n, h, w, c, r, s, k, conv7
+    (1, 5, 5, 4, 3, 3, 4, (1, 1, 1, 1, 1, 1, 0)),
+    (1, 5, 5, 4, 3, 3, 4, (1, 1, 1, 1, 1, 1, 3)),
+    (1, 5, 5, 6, 3, 3, 4, (1, 1, 1, 1, 1, 1, 3)),
+    (1, 2, 2, 4, 5, 5, 4, (0, 0, 1, 1, 1, 1, 1)),
+    (1, 5, 5, 4, 3, 3, 4, (1, 1, 0, 1, 1, 1, 1)),
+    (1, 5, 5, 4, 3, 3, 4, (1, 1, 1, -2, 1, 1, 1)),
+    (2, 9, 7, 8, 3, 2, 6, (1, 0, 2, 1, 2, 1, 2)),
+    (1, 1, 1, 1, 1, 1, 1, (0, 0, 1, 1, 1, 1, 1)),
+    (1, 3, 3, 2, 7, 7, 2, (3, 3, 2, 2, 1, 1, 1)),
+    (1, 0, 4, 2, 1, 1, 2, (1, 0, 1, 1, 1, 1, 1)),
+    (1, 4, 4, 2, 3, 3, 2, (-1, 0, 1, 1, 1, 1, 1)),
+]
+
+
+def reference_shape(n, h, w, c, r, s, k, conv):
+    lib = oracle.ref()
+    lib.ref_infer_conv_shape.argtypes = [C.c_int] * 7 + [C.c_void_p, C.c_void_p, C.c_void_p]
+    cv = np.array(conv, np.int32)
+    ho, wo = C.c_int(), C.c_int()
+    if lib.ref_infer_conv_shape(n, h, w, c, r, s, k, cv.ctypes.data, C.byref(ho), C.byref(wo)) != 0:
+        return lib.ref_last_error().decode()
+    return (ho.value, wo.value)
+
+
+def ours_shape(n, h, w, c, r, s, k, conv):
+    try:
+        return M.infer_conv_shape(n, h, w, c, r, s, k, M.Conv2DParams(*conv))
+    except M.MiqError as e:
+        assert e.status == _capi.MIQ_ERR_INVALID_ARGUMENT
+        return str(e).split(": ", 1)[1].rsplit(" (status", 1)[0]
+
+
+@pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref (the reference's own headers) not built here")
+@pytest.mark.parametrize("shape", SHAPES)
+def test_shape_validation_matches_reference(shape):
+    assert ours_shape(*shape) == reference_shape(*shape)
+
+
+def test_shape_validation_messages():
+    assert ours_shape(*SHAPES[0]) == "groups must be > 0"
+    assert ours_shape(*SHAPES[1]) == "input channels must be divisible by groups"
+    assert ours_shape(*SHAPES[2]) == "output channels must be divisible by groups"
+    assert ours_shape(*SHAPES[3]) == "invalid output size (negative numerator)"
+    assert ours_shape(*SHAPES[4]) == "stride must be > 0"
+    assert ours_shape(*SHAPES[6]) == (4, 6)  # (9 + 2 - 2*2 - 1) // 2 + 1, (7 - 1 - 1) + 1
+
+
+def test_block_shape_validation():
+    bp = M.BlockConv2DParams(M.Conv2DParams(1, 1, 1, 1, 1, 1, 1), 2, 3)
+    assert M.infer_block_conv_shape(2, 6, 6, 4, 3, 3, 5, bp) == (6, 6, 3, 2)
+    with pytest.raises(M.MiqError, match="Ho/Wo divisible by block grid"):
+        M.infer_block_conv_shape(2, 6, 6, 4, 3, 3, 5, M.BlockConv2DParams(M.Conv2DParams(), 4, 3))
+    with pytest.raises(M.MiqError, match="block_by and block_bx must be > 0"):
+        M.infer_block_conv_shape(2, 6, 6, 4, 3, 3, 5, M.BlockConv2DParams(M.Conv2DParams(), 0, 3))
+
+
+def test_entry_points_reject_before_touching_the_gpu():
+    lib = M.lib()
+    p = M.Conv2DParams()
+    fake = 0x1000  # never dereferenced: validation fails first
+    st = lib.miq_fprop_nhwc_qi32_u8(fake, fake, fake, 1, 5, 5, 4, 3, 3, 4, C.byref(M.Conv2DParams(groups=0)),
+                                    fake, fake, None)
+    assert st == _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert lib.miq_last_error_message() == b"groups must be > 0"
+    st = lib.miq_fprop_nhwc_qi32_s5(fake, fake, fake, 1, 5, 5, 4, 3, 3, 4, C.byref(p), None, fake, None)
+    assert st == _capi.MIQ_ERR_NULL_POINTER
+    st = lib.miq_fprop_nhwc_qi32_s5(fake, fake, None, 1, 5, 5, 4, 3, 3, 4, C.byref(p), fake, fake, None)
+    assert st == _capi.MIQ_ERR_NULL_POINTER
+    assert lib.miq_qconv2d_nhwc_i8(None, fake, fake, None, fake, fake, None) == _capi.MIQ_ERR_NULL_POINTER
+    d = M.make_desc((1, 8, 8, 3), (4, 3, 3, 3), padding=1, algo="igemm")
+    assert lib.miq_qconv2d_nhwc_i8(C.byref(d), fake, fake, None, fake, fake, None) == _capi.MIQ_ERR_UNSUPPORTED
+    assert b"% 16" in lib.miq_last_error_message()
+    d = M.make_desc((1, 8, 8, 32), (4, 3, 3, 32), padding=1, algo="stem")
+    assert lib.miq_qconv2d_nhwc_i8(C.byref(d), fake, fake, None, fake, fake, None) == _capi.MIQ_ERR_UNSUPPORTED
+    d = M.make_desc((1, 8, 8, 32), (4, 3, 3, 32), padding=1)
+    assert lib.miq_qconv2d_nhwc_i8(C.byref(d), fake, fake, None, None, fake, None) == _capi.MIQ_ERR_NULL_POINTER
+    d = M.make_desc((1, 8, 8, 32), (4, 3, 3, 32), padding=1, out_scale=0.0)
+    assert lib.miq_qconv2d_nhwc_i8(C.byref(d), fake, fake, None, fake, fake, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    d = M.make_desc((1, 8, 8, 32), (4, 3, 3, 32), padding=1, algo=9)
+    assert lib.miq_qconv2d_nhwc_i8_acc32(C.byref(d), fake, fake, fake, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    d = M.make_desc((-1, 8, 8, 32), (4, 3, 3, 32), padding=1)
+    assert lib.miq_qconv2d_nhwc_i8_acc32(C.byref(d), fake, fake, fake, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+
+
+def test_empty_batch_is_a_no_op():
+    # n == 0: valid, nothing to compute, nothing enqueued (no GPU needed)
+    lib = M.lib()
+    d = M.make_desc((0, 8, 8, 32), (4, 3, 3, 32), padding=1)
+    assert lib.miq_qconv2d_nhwc_i8_acc32(C.byref(d), None, None, None, None) == _capi.MIQ_ERR_NULL_POINTER
+    fake = 0x1000
+    assert lib.miq_qconv2d_nhwc_i8_acc32(C.byref(d), None, fake, None, None) == _capi.MIQ_OK
+
+
+def test_python_mirror_errors():
+    with pytest.raises(RuntimeError, match="requires non-null quantization parameters"):
+        M.launch_fprop_nhwc_qi32(M.DataType.LinQuantU8, 1, 1, 1, 1, 5, 5, 4, 3, 3, 4, None, None, 1)
+    with pytest.raises(TypeError, match="supports only LinQuantU8 and LinQuantS5"):
+        M.launch_fprop_nhwc_qi32(M.DataType.LinQuantI8, 1, 1, 1, 1, 5, 5, 4, 3, 3, 4, None, 1, 1)
+
+
+@pytest.mark.parametrize("name,algo", [("tiny", "igemm"), ("r50_3x3", "igemm"), ("r50_1x1", "igemm"),
+                                       ("down_s2", "igemm"), ("stem", "stem")])
+def test_plan_of_the_workloads(name, algo):
+    wl = M.WORKLOADS[name]
+    d = M.make_desc((wl.n, wl.h, wl.w, wl.c), (wl.k, wl.r, wl.s, wl.c), stride=wl.stride, padding=wl.pad,
+                    relu=wl.relu, in_scale=wl.in_scale)
+    assert M.plan(d) == algo
+
+
+def test_qparams_byte_layout():
+    a = M.qparams_array(M.DataType.LinQuantU8, [37, 66], [0.25, 0.35])
+    raw = a.tobytes()
+    assert len(raw) == 24 and raw[0] == 37 and raw[12] == 66
+    assert np.frombuffer(raw[4:8], np.float32)[0] == np.float32(0.25)
+    b = M.qparams_array(M.DataType.LinQuantS5, [-5, 2], n_bins=31)
+    raw = b.tobytes()
+    assert len(raw) == 16 and raw[0] == 0xFB and raw[1] == 31 and raw[8] == 2
+
+
+HARNESS_CASES = {
+    "exact_equal": ([1, -2, 3.5], [1, -2, 3.5], 0, 0),
+    "one_off": ([100, 200, 300], [100, 201, 300], 0, 0),
+    "within_abs": ([1, 2], [1.00005, 2], 1e-4, 0),
+    "within_rel": ([1000, 2], [1000.5, 2], 1e-4, 1e-3),
+    "zero_ref": ([0, 0], [1e-7, 3e-3], 1e-4, 1e-3),
+    "tiny_ref": ([1e-7, 5], [2e-7, 5], 0, 0),
+    "negative": ([-4, -8], [-4.004, -8], 1e-4, 1e-3),
+    "empty": ([], [], 0, 0),
+}
+
+
+def test_cpp_harness_verify_tensors():
+    exe = ROOT / "tests" / "cpp" / "bin" / "harness_test"
+    assert exe.exists(), "build with __graft_entry__.build()"
+    lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines()
+    got = {ln.split()[0]: ln.split()[1:] for ln in lines if ln.split()[0] in HARNESS_CASES}
+    assert set(got) == set(HARNESS_CASES)
+    expect_pass = {"exact_equal": 1, "one_off": 0, "within_abs": 1, "within_rel": 1, "zero_ref": 0, "tiny_ref": 0,
+                   "negative": 0, "empty": 1}
+    for name, (a, b, ae, re_) in HARNESS_CASES.items():
+        g = got[name]
+        assert int(g[4]) == expect_pass[name], name
+        if oracle.ref() is not None:  # the reference's own verify_tensors on the same vectors
+            r = oracle.ref_verify_tensors(np.array(a, np.float32), np.array(b, np.float32), ae, re_)
+            assert int(r["passed"]) == int(g[4]), name
+            assert np.float32(r["max_abs_err"]) == np.float32(float(g[0])), name
+            assert np.float32(r["max_rel_err"]) == np.float32(float(g[1])), name
+            assert (r["max_abs_idx"], r["max_rel_idx"]) == (int(g[2]), int(g[3])), name
+    assert "size_mismatch_throws 1" in lines
+    assert [ln for ln in lines if ln.startswith("shape")] == [
+        "shape error: groups must be > 0", "shape error: input channels must be divisible by groups",
+        "shape error: output channels must be divisible by groups",
+        "shape error: invalid output size (negative numerator)", "shape error: stride must be > 0"]
