@@ -24,75 +24,149 @@ __device__ __forceinline__ v4i lds_load16_unaligned(const unsigned char* base, i
   return r;
 }
 
-// Bias and requantization multipliers of channels kabs .. kabs+15 (valid below kc0 < Kg).
+// Writes one lane's 16 accumulators (channel kc0 + 4*j + r held in acc[j][r]) of one
+// output pixel at y + obase.  `ep_bias` / `ep_mult` point at the LDS copies of the bias and
+// requantization multiplier of channel kc0 (16 consecutive entries, 16-byte aligned); they
+// are read four channels at a time to keep few registers live.  `full`: all 16 channels
+// exist and the destination is 16-byte aligned, so vector stores are used; otherwise
+// channels at or beyond Kg are skipped.
 template <int EPI>
-__device__ __forceinline__ void load_requant16(const Requant& rq, int kc0, int Kg, int kabs, int32_t (&bv)[16],
-                                               float (&mv)[16]) {
-  if constexpr (EPI != kEpiAcc32) {
+__device__ __forceinline__ void store16(void* y, size_t obase, const v4i (&acc)[4], int kc0, int Kg, bool full,
+                                        const int32_t* ep_bias, const float* ep_mult, int relu) {
+  if constexpr (EPI == kEpiI8) {
+    const float lo = relu ? 0.0f : -128.0f;
+    int8_t* yp = static_cast<int8_t*>(y) + obase;
+    v4i pk;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const bool ok = kc0 + c < Kg;
-      bv[c] = (ok && rq.bias) ? rq.bias[kabs + c] : 0;
-      mv[c] = ok ? requant_multiplier(rq.act_scale, rq.wscale[kabs + c]) : 0.0f;
+    for (int j = 0; j < 4; ++j) {
+      const v4i bb = reinterpret_cast<const v4i*>(ep_bias)[j];
+      const v4f mm = reinterpret_cast<const v4f*>(ep_mult)[j];
+      unsigned u = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int q = requant_i8(acc[j][r], bb[r], mm[r], lo);
+        u |= (static_cast<unsigned>(q) & 0xffu) << (8 * r);
+        if (!full && kc0 + 4 * j + r < Kg) yp[4 * j + r] = static_cast<int8_t>(q);
+      }
+      pk[j] = static_cast<int>(u);
+    }
+    if (full) *reinterpret_cast<v4i*>(yp) = pk;
+  } else if constexpr (EPI == kEpiAcc32) {
+    (void)ep_bias;
+    (void)ep_mult;
+    (void)relu;
+    int32_t* yp = static_cast<int32_t*>(y) + obase;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (full) {
+        reinterpret_cast<v4i*>(yp)[j] = acc[j];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = acc[j][r];
+      }
+    }
+  } else {
+    float* yp = static_cast<float*>(y) + obase;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4i bb = reinterpret_cast<const v4i*>(ep_bias)[j];
+      const v4f mm = reinterpret_cast<const v4f*>(ep_mult)[j];
+      v4f f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) f[r] = dequant_f32(acc[j][r], bb[r], mm[r], relu);
+      if (full) {
+        reinterpret_cast<v4f*>(yp)[j] = f;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = f[r];
+      }
     }
   }
 }
 
-// Writes one lane's 16 accumulators (channel kc0 + 4*j + r held in acc[j][r]) of one
-// output pixel at y + obase.  `full`: all 16 channels exist and the destination is 16-byte
-// aligned, so vector stores are used; otherwise channels at or beyond Kg are skipped.
-template <int EPI>
-__device__ __forceinline__ void store16(void* y, size_t obase, const v4i (&acc)[4], int kc0, int Kg, bool full,
-                                        const int32_t (&bv)[16], const float (&mv)[16], int relu) {
-  int32_t v[16];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[4 * j + r] = acc[j][r];
+// Exact round-to-nearest-even of a float already clamped to [lo, 127] with lo >= -128:
+// adding 1.5 * 2^23 lands every such value in [2^23, 2^24), where the float grid is the
+// integers, so the IEEE addition itself rounds (ties to even); the result's bit pattern is
+// 0x4B400000 + q, whose low byte is q in two's complement.
+__device__ __forceinline__ unsigned rne_byte(float clamped) {
+  return __float_as_uint(clamped + 12582912.0f) & 0xffu;
+}
 
+// As store16, for accumulators that already include the bias (they were initialised with
+// it): requantizes with the per-channel multipliers at `ep_mult` (LDS).  For int8 output,
+// rint then clamp equals clamp then rint because the bounds are integers, and
+// fmaxf(NaN, lo) = lo gives the NaN rule.
+template <int EPI>
+__device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i (&acc)[4], int kc0, int Kg, bool full,
+                                               const float* ep_mult, int relu) {
   if constexpr (EPI == kEpiI8) {
     const float lo = relu ? 0.0f : -128.0f;
-    int q[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c) q[c] = requant_i8(v[c], bv[c], mv[c], lo);
     int8_t* yp = static_cast<int8_t*>(y) + obase;
-    if (full) {
-      v4i pk;
+    v4i pk;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const unsigned u = (static_cast<unsigned>(q[4 * d]) & 0xffu) | ((static_cast<unsigned>(q[4 * d + 1]) & 0xffu) << 8) |
-                           ((static_cast<unsigned>(q[4 * d + 2]) & 0xffu) << 16) |
-                           ((static_cast<unsigned>(q[4 * d + 3]) & 0xffu) << 24);
-        pk[d] = static_cast<int>(u);
+    for (int j = 0; j < 4; ++j) {
+      const v4f mm = reinterpret_cast<const v4f*>(ep_mult)[j];
+      unsigned u = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = static_cast<float>(acc[j][r]) * mm[r];
+        const float c = fminf(fmaxf(v, lo), 127.0f);
+        const unsigned byte = rne_byte(c);
+        u |= byte << (8 * r);
+        if (!full && kc0 + 4 * j + r < Kg) yp[4 * j + r] = static_cast<int8_t>(byte);
       }
-      *reinterpret_cast<v4i*>(yp) = pk;
-    } else {
-#pragma unroll
-      for (int c = 0; c < 16; ++c)
-        if (kc0 + c < Kg) yp[c] = static_cast<int8_t>(q[c]);
+      pk[j] = static_cast<int>(u);
     }
+    if (full) *reinterpret_cast<v4i*>(yp) = pk;
   } else if constexpr (EPI == kEpiAcc32) {
+    (void)ep_mult;
+    (void)relu;
     int32_t* yp = static_cast<int32_t*>(y) + obase;
-    if (full) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) reinterpret_cast<v4i*>(yp)[d] = v4i{v[4 * d], v[4 * d + 1], v[4 * d + 2], v[4 * d + 3]};
-    } else {
+    for (int j = 0; j < 4; ++j) {
+      if (full) {
+        reinterpret_cast<v4i*>(yp)[j] = acc[j];
+      } else {
 #pragma unroll
-      for (int c = 0; c < 16; ++c)
-        if (kc0 + c < Kg) yp[c] = v[c];
+        for (int r = 0; r < 4; ++r)
+          if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = acc[j][r];
+      }
     }
   } else {
-    float f[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c) f[c] = dequant_f32(v[c], bv[c], mv[c], relu);
     float* yp = static_cast<float*>(y) + obase;
-    if (full) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) reinterpret_cast<v4f*>(yp)[d] = v4f{f[4 * d], f[4 * d + 1], f[4 * d + 2], f[4 * d + 3]};
-    } else {
+    for (int j = 0; j < 4; ++j) {
+      const v4f mm = reinterpret_cast<const v4f*>(ep_mult)[j];
+      v4f f;
 #pragma unroll
-      for (int c = 0; c < 16; ++c)
-        if (kc0 + c < Kg) yp[c] = f[c];
+      for (int r = 0; r < 4; ++r) {
+        float v = static_cast<float>(acc[j][r]) * mm[r];
+        if (relu) v = (v > 0.0f) ? v : 0.0f;
+        f[r] = v;
+      }
+      if (full) {
+        reinterpret_cast<v4f*>(yp)[j] = f;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = f[r];
+      }
+    }
+  }
+}
+
+// Bias and requantization multiplier of `count` channels starting at kabs (entries at or
+// beyond `valid` are 0) into LDS, one channel per thread of the workgroup.
+template <int EPI>
+__device__ __forceinline__ void stage_requant(const Requant& rq, int kabs, int valid, int count, int32_t* ep_bias,
+                                              float* ep_mult) {
+  if constexpr (EPI != kEpiAcc32) {
+    for (int c = threadIdx.x; c < count; c += blockDim.x) {
+      const bool ok = c < valid;
+      ep_bias[c] = (ok && rq.bias) ? rq.bias[kabs + c] : 0;
+      ep_mult[c] = ok ? requant_multiplier(rq.act_scale, rq.wscale[kabs + c]) : 0.0f;
     }
   }
 }

@@ -13,12 +13,28 @@
 // int8 store (or four 16-byte int32/fp32 stores): a wave writes 16 pixels x 64 channels.
 //
 // Work decomposition: a workgroup (4 waves) owns one tile of RB output rows x CB output
-// columns of one image and 64*NKT*WAVES_K output channels of one group.  The input
-// patch the tile needs (its "halo": rows*stride + dilated taps, all Cg channels) is
-// staged once into LDS with coalesced 16-byte loads, zero-filled where the convolution
-// pads; every tap then reads shifted windows of it.  16-byte chunks are XOR-swizzled
-// within a pixel so that the 16 lanes of a group reading 16 neighbouring pixels hit
-// distinct LDS banks.
+// columns of one image (at most one pass of every wave: WAVES_P*NSEG*16 pixels) and
+// KT_WG = 64*NKT*WAVES_K output channels of one group.  Each wave computes NKT 64-channel
+// tiles x NSEG 16-pixel segments; per K-block it reads 4*NKT filter fragments and NSEG
+// input fragments (1 KB each) from LDS for 4*NKT*NSEG MFMAs.
+//
+// LDS holds, per workgroup: the bias and requantization multiplier of its channels; the
+// filter, in fragment order (one 1 KB block per (K-block, 64-channel tile, j), lane l's 16
+// bytes at l*16), staged in chunks of K-blocks; and the input patch of the tile (its
+// "halo": rows*stride + dilated taps, all Cg channels, zero where the convolution pads),
+// stored planar as [chunk c16][column parity hc % sw][row][hc / sw] x 16 bytes.  In that
+// layout the 16 lanes of an MFMA lane group, which read one chunk of 16 consecutive output
+// pixels, read 256 contiguous bytes for any stride: no bank conflicts, and the address of
+// a fragment is a per-lane constant plus a per-K-block constant.  Every runtime division
+// is a multiply-high by a host-computed magic number.  Filter and halo arrive with direct global->LDS loads
+// (global_load_lds_dwordx4): no registers, all in flight at once.  When the filter does
+// not fit, the chunk after the current one streams in while the current one computes.
+//
+// The K-loop is software-pipelined: the fragments of K-block b+1 are read from LDS while
+// the MFMAs of K-block b run.  Accumulators start at the bias, so the epilogue is
+// convert, scale, clamp, round: round-to-nearest-even comes from adding 1.5*2^23 to the
+// clamped value (exact IEEE rounding of a value in [-128, 127]), whose low byte is then
+// the two's-complement int8 result.
 
 #include "qconv_device.h"
 
@@ -28,7 +44,8 @@ namespace miq {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLdsBudget = 64 * 1024;  // bytes of dynamic LDS per workgroup
+constexpr int kLdsBudget = 160 * 1024;   // LDS bytes per workgroup on gfx950
+constexpr int kLdsPreferred = 76 * 1024; // two workgroups per CU
 
 struct IgemmArgs {
   const int8_t* x;
@@ -40,158 +57,251 @@ struct IgemmArgs {
   int ph, pw, sh, sw, dh, dw;
   int Cg, Kg, Cg16;  // channels per group, output channels per group, Cg / 16
   int NQ, KB, Kdim;  // chunks per filter row, MFMA K-blocks, R*S*Cg
+  int KBC, nchunks;  // K-blocks per staged filter chunk, number of chunks
   int RB, CB;        // output tile extent
   int tiles_h, tiles_w;
-  int kt_per_group;  // channel tiles (of 64*NKT*WAVES_K) per group
-  int swz_shift, swz_mask;
+  int kt_per_group;  // channel tiles (of KT_WG) per group
+  int HCs, PS, nslot;  // halo: columns per parity plane, plane size and total size (16-byte slots)
+  int w_off, h_off;  // LDS byte offsets of the filter buffers and of the halo
+  int w_buf_bytes;   // bytes of one filter chunk buffer
   float act_scale;
   int relu;
+  FastDiv fd_ps, fd_hcs, fd_sw, fd_cb, fd_cg16, fd_s, fd_tiles_img, fd_tiles_w, fd_ktpg, fd_gx;
 };
 
-__device__ __forceinline__ int swz(int hp, int shift, int mask) {
-  return ((hp >> shift) ^ (hp >> (shift + 3))) & mask;
+// Workgroups are dispatched round-robin over the 8 XCDs (id % 8).  Give each XCD a
+// contiguous range of tile ids so neighbouring tiles, which share halo rows, meet in the
+// same L2.
+__device__ __forceinline__ int xcd_tile(int bid, int total) {
+  const int q = total >> 3;
+  const int r = total & 7;
+  const int xcd = bid & 7;
+  const int pos = bid >> 3;
+  return xcd * q + min(xcd, r) + pos;
 }
 
-template <int NKT, int NSEG, int WAVES_K, int EPI>
-__global__ void __launch_bounds__(kThreads)
+// 16 bytes global -> LDS without registers; `lds_wave_base` is the wave's 1 KB block, lane l
+// lands at lds_wave_base + 16*l.
+__device__ __forceinline__ void load_lds16(const void* src, v4i* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
+}
+
+// Filter fragments of K-blocks [b0, b0 + nb) of the workgroup's channels into `dst`
+// (fragment order).  Fragment f = (bl * CT + ct) * 4 + j goes to dst + f * 64 (v4i units).
+template <int CT>
+__device__ __forceinline__ void stage_filter(const IgemmArgs& a, const int8_t* wg, int kwg0, int b0, int nb, v4i* dst,
+                                             int wave, int lane) {
+  const int nfrag = nb * CT * 4;
+  const int row_l = lane & 15;
+  const int grp_l = lane >> 4;
+  for (int f = wave; f < nfrag; f += 4) {
+    const int j = f & 3;
+    const int ct = (f >> 2) % CT;
+    const int bl = (f >> 2) / CT;
+    const int kc = kwg0 + ct * 64 + 16 * (row_l >> 2) + 4 * j + (row_l & 3);
+    const int q = 4 * (b0 + bl) + grp_l;
+    v4i* blk = dst + f * 64;
+    if (kc < a.Kg && q < a.NQ) {
+      load_lds16(wg + static_cast<size_t>(kc) * a.Kdim + q * 16, blk);
+    } else {
+      blk[lane] = v4i{0, 0, 0, 0};
+    }
+  }
+}
+
+template <int NKT, int NSEG, int WAVES_K, int EPI, bool TAPU>
+__global__ void __launch_bounds__(kThreads, NKT == 1 ? 2 : 1)  // two waves per SIMD where it does not spill
 i8_igemm_kernel(IgemmArgs a) {
   constexpr int WAVES_P = 4 / WAVES_K;
-  constexpr int KTILE = 64 * NKT;  // output channels per wave
-  extern __shared__ v4i halo[];
+  constexpr int KTILE = 64 * NKT;          // output channels per wave
+  constexpr int KT_WG = KTILE * WAVES_K;   // output channels per workgroup
+  constexpr int CT = KT_WG / 64;           // 64-channel tiles per workgroup
+  extern __shared__ v4i smem[];
+  int32_t* ep_bias = reinterpret_cast<int32_t*>(smem);
+  float* ep_mult = reinterpret_cast<float*>(smem) + KT_WG;
+  v4i* wbuf0 = smem + a.w_off / 16;
+  v4i* wbuf1 = wbuf0 + a.w_buf_bytes / 16;
+  v4i* halo = smem + a.h_off / 16;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wk = wave % WAVES_K;
   const int wp = wave / WAVES_K;
+  const int row_l = lane & 15;  // MFMA row (A) / column (B) of this lane
+  const int grp_l = lane >> 4;  // chunk slot of this lane inside a K-block
 
-  const int tiles_img = a.tiles_h * a.tiles_w;
-  const int n = blockIdx.x / tiles_img;
-  const int trem = blockIdx.x - n * tiles_img;
-  const int th = trem / a.tiles_w;
+  const int nblk = gridDim.x * gridDim.y;
+  const int lin = xcd_tile(blockIdx.x + blockIdx.y * gridDim.x, nblk);
+  const int ctile = fdiv(lin, a.fd_gx);
+  const int tile = lin - ctile * static_cast<int>(gridDim.x);
+  const int n = fdiv(tile, a.fd_tiles_img);
+  const int trem = tile - n * a.tiles_h * a.tiles_w;
+  const int th = fdiv(trem, a.fd_tiles_w);
   const int tw = trem - th * a.tiles_w;
-  const int gi = blockIdx.y / a.kt_per_group;
-  const int kt = blockIdx.y - gi * a.kt_per_group;
+  const int gi = fdiv(ctile, a.fd_ktpg);
+  const int kt = ctile - gi * a.kt_per_group;
+  const int kwg0 = kt * KT_WG;             // first channel of the workgroup within the group
+  const int kwave0 = kwg0 + wk * KTILE;    // first channel of this wave within the group
+  const int8_t* wg = a.w + static_cast<size_t>(gi) * a.Kg * a.Kdim;
 
   const int ho0 = th * a.RB;
   const int wo0 = tw * a.CB;
   const int rows = min(a.RB, a.Ho - ho0);
   const int cols = min(a.CB, a.Wo - wo0);
-  const int HR = (rows - 1) * a.sh + (a.R - 1) * a.dh + 1;
-  const int HC = (cols - 1) * a.sw + (a.S - 1) * a.dw + 1;
-  const int hi0 = ho0 * a.sh - a.ph;
-  const int wi0 = wo0 * a.sw - a.pw;
 
-  // ---- stage the input halo of this tile (this group's channels) into LDS ----
-  const int8_t* xg = a.x + static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg;
-  const int nchunk = HR * HC * a.Cg16;
-  for (int i = tid; i < nchunk; i += kThreads) {
-    const int hp = i / a.Cg16;
-    const int c16 = i - hp * a.Cg16;
-    const int hr = hp / HC;
-    const int hc = hp - hr * HC;
-    const int hi = hi0 + hr;
-    const int wi = wi0 + hc;
-    v4i v = {0, 0, 0, 0};
-    if (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) && static_cast<unsigned>(wi) < static_cast<unsigned>(a.W)) {
-      v = *reinterpret_cast<const v4i*>(xg + (static_cast<size_t>(hi) * a.W + wi) * a.C + c16 * 16);
+  // ---- staging: filter chunk 0 and the halo (direct loads), epilogue parameters ----
+  stage_filter<CT>(a, wg, kwg0, 0, min(a.KBC, a.KB), wbuf0, wave, lane);
+  {
+    const int hi0 = ho0 * a.sh - a.ph;
+    const int wi0 = wo0 * a.sw - a.pw;
+    const int8_t* xg = a.x + static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg;
+    for (int u = wave; u * 64 < a.nslot; u += 4) {
+      const int L = u * 64 + lane;  // LDS slot this lane fills
+      if (L < a.nslot) {
+        const int plane = fdiv(L, a.fd_ps);
+        const int rem = L - plane * a.PS;
+        const int hr = fdiv(rem, a.fd_hcs);
+        const int hcs = rem - hr * a.HCs;
+        const int c16 = fdiv(plane, a.fd_sw);
+        const int par = plane - c16 * a.sw;
+        const int hi = hi0 + hr;
+        const int wi = wi0 + hcs * a.sw + par;
+        if (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) && static_cast<unsigned>(wi) < static_cast<unsigned>(a.W)) {
+          load_lds16(xg + (static_cast<size_t>(hi) * a.W + wi) * a.C + c16 * 16, halo + u * 64);
+        } else {
+          halo[L] = v4i{0, 0, 0, 0};
+        }
+      }
     }
-    halo[hp * a.Cg16 + (c16 ^ swz(hp, a.swz_shift, a.swz_mask))] = v;
   }
+  if constexpr (EPI != kEpiAcc32) {
+    stage_requant<EPI>(Requant{a.bias, a.wscale, a.act_scale, a.relu}, gi * a.Kg + kwg0, a.Kg - kwg0, KT_WG, ep_bias,
+                       ep_mult);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  const int kwave0 = kt * (KTILE * WAVES_K) + wk * KTILE;  // first channel of this wave within the group
-  if (kwave0 >= a.Kg) return;                               // no barrier follows
+  const bool wave_active = kwave0 < a.Kg;  // waves past the last channel still join every barrier
 
-  const int npix = rows * cols;
-  const int nseg = (npix + 15) >> 4;
-  const int row_l = lane & 15;  // MFMA row (A) / column (B) of this lane
-  const int grp_l = lane >> 4;  // chunk slot of this lane inside a K-block
-  const int8_t* wg = a.w + static_cast<size_t>(gi) * a.Kg * a.Kdim;
-
-  // Filter rows this lane feeds to the A operand of MFMA (t, j).
-  int kc[NKT][4];
+  // per segment: halo slot of tap (0,0) / chunk 0 for this lane's pixel, output pixel index
+  int pix_off[NSEG], opix[NSEG];
+  bool pv[NSEG];
 #pragma unroll
-  for (int t = 0; t < NKT; ++t)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) kc[t][j] = kwave0 + t * 64 + 16 * (row_l >> 2) + 4 * j + (row_l & 3);
+  for (int i = 0; i < NSEG; ++i) {
+    const int p = (wp * NSEG + i) * 16 + row_l;
+    const int lho = fdiv(p, a.fd_cb);
+    const int lwo = p - lho * a.CB;
+    pv[i] = lho < rows && lwo < cols;
+    pix_off[i] = lho * a.sh * a.HCs + lwo;
+    opix[i] = (n * a.Ho + ho0 + lho) * a.Wo + wo0 + lwo;
+  }
+  const int grp_plane_off = grp_l * a.sw * a.PS;  // lane group g reads chunk c16 + g (TAPU)
 
-  for (int sg0 = wp * NSEG; sg0 < nseg; sg0 += WAVES_P * NSEG) {
-    int pb[NSEG];
-    bool pv[NSEG];
+  // accumulators start at the bias (int8 / fp32 outputs) or at 0 (raw accumulators)
+  v4i acc[NKT][4][NSEG];
+#pragma unroll
+  for (int t = 0; t < NKT; ++t) {
+    const int lc = wk * KTILE + t * 64 + 16 * grp_l;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v4i init = {0, 0, 0, 0};
+      if constexpr (EPI != kEpiAcc32) init = reinterpret_cast<const v4i*>(ep_bias + lc)[j];
+#pragma unroll
+      for (int i = 0; i < NSEG; ++i) acc[t][j][i] = init;
+    }
+  }
+
+  // fragment loaders for one K-block
+  auto load_b = [&](int b, v4i (&B)[NSEG]) {
+    int off;
+    bool qv;
+    if constexpr (TAPU) {  // Cg16 % 4 == 0: the 4 chunks of a K-block belong to one tap
+      const int q0 = 4 * b;
+      const int tap = fdiv(q0, a.fd_cg16);
+      const int cb = q0 - tap * a.Cg16;
+      const int rr = fdiv(tap, a.fd_s);
+      const int sdw = (tap - rr * a.S) * a.dw;
+      const int hq = fdiv(sdw, a.fd_sw);
+      off = (cb * a.sw + (sdw - hq * a.sw)) * a.PS + rr * a.dh * a.HCs + hq + grp_plane_off;
+      qv = true;
+    } else {
+      const int q = 4 * b + grp_l;
+      const int tap = fdiv(q, a.fd_cg16);
+      const int c16 = q - tap * a.Cg16;
+      const int rr = fdiv(tap, a.fd_s);
+      const int sdw = (tap - rr * a.S) * a.dw;
+      const int hq = fdiv(sdw, a.fd_sw);
+      off = (c16 * a.sw + (sdw - hq * a.sw)) * a.PS + rr * a.dh * a.HCs + hq;
+      qv = q < a.NQ;
+    }
 #pragma unroll
     for (int i = 0; i < NSEG; ++i) {
-      const int p = (sg0 + i) * 16 + row_l;
-      pv[i] = p < npix;
-      const int lho = p / cols;
-      const int lwo = p - lho * cols;
-      pb[i] = pv[i] ? (lho * a.sh) * HC + lwo * a.sw : 0;
+      v4i v = {0, 0, 0, 0};
+      if (qv && pv[i]) v = halo[pix_off[i] + off];
+      B[i] = v;
     }
-
-    v4i acc[NKT][4][NSEG];
+  };
+  auto load_a = [&](const v4i* wb, int bl, v4i (&A)[NKT][4]) {
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) A[t][j] = wb[((bl * CT + wk * NKT + t) * 4 + j) * 64 + lane];
+  };
+  auto mma = [&](const v4i (&A)[NKT][4], const v4i (&B)[NSEG]) {
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int i = 0; i < NSEG; ++i) acc[t][j][i] = v4i{0, 0, 0, 0};
+        for (int i = 0; i < NSEG; ++i)
+          acc[t][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[t][j], B[i], acc[t][j][i], 0, 0, 0);
+  };
 
-    for (int b = 0; b < a.KB; ++b) {
-      const int q = 4 * b + grp_l;
-      const bool qv = q < a.NQ;
-      const int tap = q / a.Cg16;
-      const int c16 = q - tap * a.Cg16;
-      const int rr = tap / a.S;
-      const int ss = tap - rr * a.S;
-      const int toff = rr * a.dh * HC + ss * a.dw;
-
-      v4i A[NKT][4];
-#pragma unroll
-      for (int t = 0; t < NKT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v4i v = {0, 0, 0, 0};
-          if (qv && kc[t][j] < a.Kg) v = *reinterpret_cast<const v4i*>(wg + static_cast<size_t>(kc[t][j]) * a.Kdim + q * 16);
-          A[t][j] = v;
-        }
-      v4i B[NSEG];
-#pragma unroll
-      for (int i = 0; i < NSEG; ++i) {
-        const int hp = pb[i] + toff;
-        v4i v = {0, 0, 0, 0};
-        if (qv && pv[i]) v = halo[hp * a.Cg16 + (c16 ^ swz(hp, a.swz_shift, a.swz_mask))];
-        B[i] = v;
-      }
-#pragma unroll
-      for (int t = 0; t < NKT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int i = 0; i < NSEG; ++i)
-            acc[t][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[t][j], B[i], acc[t][j][i], 0, 0, 0);
+  for (int c = 0; c < a.nchunks; ++c) {
+    const int b0 = c * a.KBC;
+    const int nb = min(a.KBC, a.KB - b0);
+    const v4i* wb = (c & 1) ? wbuf1 : wbuf0;
+    if (c + 1 < a.nchunks) {  // next chunk streams in behind this one
+      stage_filter<CT>(a, wg, kwg0, b0 + a.KBC, min(a.KBC, a.KB - b0 - a.KBC), (c & 1) ? wbuf0 : wbuf1, wave, lane);
     }
-
-    // ---- epilogue: lane holds channels kc0 .. kc0+15 of pixel p for each (t, i) ----
-    const Requant rq{a.bias, a.wscale, a.act_scale, a.relu};
-#pragma unroll
-    for (int t = 0; t < NKT; ++t) {
-      const int kc0 = kwave0 + t * 64 + 16 * grp_l;
-      if (kc0 >= a.Kg) continue;
-      const int kabs = gi * a.Kg + kc0;
-      const bool full = (kc0 + 16 <= a.Kg) && ((a.Kg & 15) == 0);
-      int32_t bv[16];
-      float mv[16];
-      load_requant16<EPI>(rq, kc0, a.Kg, kabs, bv, mv);
-#pragma unroll
-      for (int i = 0; i < NSEG; ++i) {
-        if (!pv[i]) continue;
-        const int p = (sg0 + i) * 16 + row_l;
-        const int lho = p / cols;
-        const int lwo = p - lho * cols;
-        const size_t opix = (static_cast<size_t>(n) * a.Ho + (ho0 + lho)) * a.Wo + (wo0 + lwo);
-        const v4i frag[4] = {acc[t][0][i], acc[t][1][i], acc[t][2][i], acc[t][3][i]};
-        store16<EPI>(a.y, opix * a.K + kabs, frag, kc0, a.Kg, full, bv, mv, a.relu);
+    if (wave_active) {
+      v4i A0[NKT][4], A1[NKT][4], B0[NSEG], B1[NSEG];
+      load_a(wb, 0, A0);
+      load_b(b0, B0);
+      int bl = 0;
+      for (; bl + 2 <= nb; bl += 2) {
+        load_a(wb, bl + 1, A1);
+        load_b(b0 + bl + 1, B1);
+        mma(A0, B0);
+        if (bl + 2 < nb) {
+          load_a(wb, bl + 2, A0);
+          load_b(b0 + bl + 2, B0);
+        }
+        mma(A1, B1);
       }
+      if (bl < nb) mma(A0, B0);
+    }
+    if (c + 1 < a.nchunks) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+  if (!wave_active) return;
+
+  // ---- epilogue: lane holds channels kc0 .. kc0+15 of pixel p for each (t, i) ----
+#pragma unroll
+  for (int t = 0; t < NKT; ++t) {
+    const int kc0 = kwave0 + t * 64 + 16 * grp_l;
+    if (kc0 >= a.Kg) continue;
+    const int kabs = gi * a.Kg + kc0;
+    const bool full = (kc0 + 16 <= a.Kg) && ((a.Kg & 15) == 0);
+    const int lc = kc0 - kwg0;
+#pragma unroll
+    for (int i = 0; i < NSEG; ++i) {
+      if (!pv[i]) continue;
+      const v4i frag[4] = {acc[t][0][i], acc[t][1][i], acc[t][2][i], acc[t][3][i]};
+      store16_biased<EPI>(a.y, static_cast<size_t>(opix[i]) * a.K + kabs, frag, kc0, a.Kg, full, ep_mult + lc, a.relu);
     }
   }
 }
@@ -199,18 +309,38 @@ i8_igemm_kernel(IgemmArgs a) {
 // Host-side tiling decision for one problem.
 struct IgemmPlan {
   int nkt, waves_k, nseg;
+  int KBC, nchunks;
   int RB, CB, tiles_h, tiles_w, kt_per_group;
+  int w_off, h_off, w_buf_bytes;
   size_t lds_bytes;
 };
 
-size_t halo_bytes(const Geom& g, int RB, int CB) {
-  const size_t HR = static_cast<size_t>(RB - 1) * g.sh + static_cast<size_t>(g.R - 1) * g.dh + 1;
-  const size_t HC = static_cast<size_t>(CB - 1) * g.sw + static_cast<size_t>(g.S - 1) * g.dw + 1;
-  return HR * HC * static_cast<size_t>(g.Cg);
+// Planar halo of a full RB x CB tile: Cg16 chunks x sw parity planes x HR rows x HCs columns.
+struct HaloDims {
+  int HR, HCs, PS, nslot;
+};
+
+HaloDims halo_dims(const Geom& g, int RB, int CB) {
+  HaloDims h;
+  h.HR = (RB - 1) * g.sh + (g.R - 1) * g.dh + 1;
+  const int HC = (CB - 1) * g.sw + (g.S - 1) * g.dw + 1;
+  h.HCs = (HC + g.sw - 1) / g.sw;
+  h.PS = h.HR * h.HCs;
+  h.nslot = (g.Cg / 16) * g.sw * h.PS;
+  return h;
 }
 
+size_t halo_bytes(const Geom& g, int RB, int CB) {
+  const long long HR = static_cast<long long>(RB - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
+  const long long HC = static_cast<long long>(CB - 1) * g.sw + static_cast<long long>(g.S - 1) * g.dw + 1;
+  const long long HCs = (HC + g.sw - 1) / g.sw;
+  return static_cast<size_t>(HR * HCs * g.sw * g.Cg);
+}
+
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
 bool make_plan(const Geom& g, IgemmPlan* pl) {
-  // Channel tiling: one wave covers 64*nkt channels; waves_k waves split the channels.
+  // Channel tiling: a wave covers 64*nkt channels, waves_k waves split the channels.
   if (g.Kg <= 64) {
     pl->nkt = 1; pl->waves_k = 1;
   } else if (g.Kg <= 128) {
@@ -220,42 +350,99 @@ bool make_plan(const Geom& g, IgemmPlan* pl) {
   } else {
     pl->nkt = 2; pl->waves_k = 4;
   }
-  pl->nseg = 4;
+  pl->nseg = pl->nkt == 2 ? 2 : 4;  // keeps two waves per SIMD (registers)
+  const int kt_wg = 64 * pl->nkt * pl->waves_k;
   const int waves_p = 4 / pl->waves_k;
-  const int tp = waves_p * pl->nseg * 16;  // pixels per tile
-  pl->kt_per_group = (g.Kg + 64 * pl->nkt * pl->waves_k - 1) / (64 * pl->nkt * pl->waves_k);
+  const int tile_px = waves_p * pl->nseg * 16;
+  pl->kt_per_group = (g.Kg + kt_wg - 1) / kt_wg;
+  const int kb = (g.R * g.S * (g.Cg / 16) + 3) / 4;
+  const size_t kblock_bytes = static_cast<size_t>(kt_wg) * 64;  // filter bytes of one K-block
+  const size_t ep_bytes = round_up(static_cast<size_t>(kt_wg) * 8, 1024);
 
-  // Spatial tiling: whole output rows when they are short, otherwise row segments.
-  int CB = std::min(g.Wo, tp);
-  int RB = std::max(1, tp / CB);
-  RB = std::min(RB, g.Ho);
-  while (RB > 1 && halo_bytes(g, RB, CB) > static_cast<size_t>(kLdsBudget)) --RB;
-  while (CB > 16 && halo_bytes(g, RB, CB) > static_cast<size_t>(kLdsBudget)) CB -= 16;
-  if (halo_bytes(g, RB, CB) > static_cast<size_t>(kLdsBudget)) return false;
+  // Spatial tiling: whole output rows if they are short, else row segments; one pass of
+  // every wave.  Prefer the row count that leaves the fewest idle lanes (ties: taller).
+  int CB = std::min(g.Wo, tile_px);
+  int RB = std::max(1, std::min(g.Ho, tile_px / CB));
+  auto lds_total = [&](int rb, int cb, int kbc, int nbuf) {
+    return ep_bytes + nbuf * kbc * kblock_bytes + round_up(halo_bytes(g, rb, cb), 1024);
+  };
+  // Filter staging: the whole filter in one buffer when that keeps two workgroups per CU;
+  // else the largest double-buffered chunk that does; else the whole filter or chunks within
+  // the full LDS of one workgroup.
+  auto fit = [&](int rb, int cb, int* kbc, int* nbuf) {
+    const size_t limits[2] = {static_cast<size_t>(kLdsPreferred), static_cast<size_t>(kLdsBudget)};
+    for (size_t lim : limits) {
+      if (lds_total(rb, cb, kb, 1) <= lim) {
+        *kbc = kb;
+        *nbuf = 1;
+        return true;
+      }
+      for (int c = kb - 1; c >= 1; --c) {
+        if (lds_total(rb, cb, c, 2) <= lim) {
+          *kbc = c;
+          *nbuf = 2;
+          return true;
+        }
+      }
+    }
+    return false;
+  };
+  int kbc = 0, nbuf = 0;
+  while (RB > 1 && !fit(RB, CB, &kbc, &nbuf)) --RB;
+  while (CB > 16 && !fit(RB, CB, &kbc, &nbuf)) CB -= 16;
+  if (!fit(RB, CB, &kbc, &nbuf)) return false;
   pl->RB = RB;
   pl->CB = CB;
+  pl->KBC = kbc;
+  pl->nchunks = (kb + kbc - 1) / kbc;
   pl->tiles_h = (g.Ho + RB - 1) / RB;
   pl->tiles_w = (g.Wo + CB - 1) / CB;
-  pl->lds_bytes = halo_bytes(g, RB, CB);
+  pl->w_off = static_cast<int>(ep_bytes);
+  pl->w_buf_bytes = static_cast<int>(kbc * kblock_bytes);
+  pl->h_off = static_cast<int>(ep_bytes + nbuf * kbc * kblock_bytes);
+  pl->lds_bytes = lds_total(RB, CB, kbc, nbuf);
   return true;
 }
 
-template <int NKT, int WAVES_K, int EPI>
+template <int NKT, int NSEG, int WAVES_K, int EPI, bool TAPU>
 void launch_cfg(const IgemmArgs& a, const IgemmPlan& pl, int N, int G, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(N * pl.tiles_h * pl.tiles_w), static_cast<unsigned>(G * pl.kt_per_group));
-  hipLaunchKernelGGL((i8_igemm_kernel<NKT, 4, WAVES_K, EPI>), grid, dim3(kThreads), pl.lds_bytes, stream, a);
+  auto kern = i8_igemm_kernel<NKT, NSEG, WAVES_K, EPI, TAPU>;
+  if (pl.lds_bytes > 64 * 1024) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(pl.lds_bytes));
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.lds_bytes, stream, a);
+}
+
+template <int NKT, int WAVES_K, int EPI, bool TAPU>
+void launch_nseg(const IgemmArgs& a, const IgemmPlan& pl, int N, int G, hipStream_t stream) {
+  if constexpr (NKT == 2) {
+    launch_cfg<NKT, 2, WAVES_K, EPI, TAPU>(a, pl, N, G, stream);
+  } else {
+    launch_cfg<NKT, 4, WAVES_K, EPI, TAPU>(a, pl, N, G, stream);
+  }
+}
+
+template <int EPI, bool TAPU>
+void launch_shape(const IgemmArgs& a, const IgemmPlan& pl, int N, int G, hipStream_t stream) {
+  if (pl.nkt == 2) {
+    launch_nseg<2, 4, EPI, TAPU>(a, pl, N, G, stream);
+  } else if (pl.waves_k == 4) {
+    launch_nseg<1, 4, EPI, TAPU>(a, pl, N, G, stream);
+  } else if (pl.waves_k == 2) {
+    launch_nseg<1, 2, EPI, TAPU>(a, pl, N, G, stream);
+  } else {
+    launch_nseg<1, 1, EPI, TAPU>(a, pl, N, G, stream);
+  }
 }
 
 template <int EPI>
 void launch_epi(const IgemmArgs& a, const IgemmPlan& pl, int N, int G, hipStream_t stream) {
-  if (pl.nkt == 2) {
-    launch_cfg<2, 4, EPI>(a, pl, N, G, stream);
-  } else if (pl.waves_k == 4) {
-    launch_cfg<1, 4, EPI>(a, pl, N, G, stream);
-  } else if (pl.waves_k == 2) {
-    launch_cfg<1, 2, EPI>(a, pl, N, G, stream);
+  if (a.Cg16 % 4 == 0) {
+    launch_shape<EPI, true>(a, pl, N, G, stream);
   } else {
-    launch_cfg<1, 1, EPI>(a, pl, N, G, stream);
+    launch_shape<EPI, false>(a, pl, N, G, stream);
   }
 }
 
@@ -288,8 +475,8 @@ bool igemm_eligible(const Geom& g0, const void* x, const void* w, const void* y,
   if (!aligned16(x) || !aligned16(w) || !aligned16(y)) return no("implicit GEMM needs 16-byte aligned tensors");
   IgemmPlan pl;
   if (!make_plan(g, &pl)) return no("implicit GEMM input tile does not fit in LDS");
-  const long long grid_x = static_cast<long long>(g.N) * pl.tiles_h * pl.tiles_w;
-  if (grid_x > 0x7fffffffLL || static_cast<long long>(g.G) * pl.kt_per_group > 65535) return no("grid too large");
+  const long long blocks = static_cast<long long>(g.N) * pl.tiles_h * pl.tiles_w * g.G * pl.kt_per_group;
+  if (blocks > 0x7fffffffLL || static_cast<long long>(g.G) * pl.kt_per_group > 65535) return no("grid too large");
   return true;
 }
 
@@ -308,17 +495,22 @@ hipError_t launch_i8_igemm(const Geom& g0, Epi epi, const int8_t* x, const int8_
   a.NQ = g.R * g.S * a.Cg16;
   a.KB = (a.NQ + 3) / 4;
   a.Kdim = g.R * g.S * g.Cg;
+  a.KBC = pl.KBC; a.nchunks = pl.nchunks;
   a.RB = pl.RB; a.CB = pl.CB; a.tiles_h = pl.tiles_h; a.tiles_w = pl.tiles_w;
   a.kt_per_group = pl.kt_per_group;
-  if (a.Cg16 % 8 == 0) {
-    a.swz_shift = 0; a.swz_mask = 7;
-  } else if (a.Cg16 % 4 == 0) {
-    a.swz_shift = 1; a.swz_mask = 3;
-  } else if (a.Cg16 % 2 == 0) {
-    a.swz_shift = 2; a.swz_mask = 1;
-  } else {
-    a.swz_shift = 0; a.swz_mask = 0;
-  }
+  const HaloDims hd = halo_dims(g, pl.RB, pl.CB);
+  a.HCs = hd.HCs; a.PS = hd.PS; a.nslot = hd.nslot;
+  a.fd_ps = make_fastdiv(hd.PS);
+  a.fd_hcs = make_fastdiv(hd.HCs);
+  a.fd_sw = make_fastdiv(g.sw);
+  a.fd_cb = make_fastdiv(pl.CB);
+  a.fd_cg16 = make_fastdiv(a.Cg16);
+  a.fd_s = make_fastdiv(g.S);
+  a.fd_tiles_img = make_fastdiv(pl.tiles_h * pl.tiles_w);
+  a.fd_tiles_w = make_fastdiv(pl.tiles_w);
+  a.fd_ktpg = make_fastdiv(pl.kt_per_group);
+  a.fd_gx = make_fastdiv(g.N * pl.tiles_h * pl.tiles_w);
+  a.w_off = pl.w_off; a.h_off = pl.h_off; a.w_buf_bytes = pl.w_buf_bytes;
   a.act_scale = rq.act_scale;
   a.relu = rq.relu;
 

@@ -43,6 +43,26 @@ struct BlockGeom {
 
 enum QpKind : int { kQpU8 = 0, kQpS5 = 1 };
 
+// Division by a launch-constant divisor d >= 1 for numerators 0 <= n < 2^31, as one
+// multiply-high, one add and one shift (Granlund & Montgomery, "Division by invariant
+// integers using multiplication", 1994): s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1,
+// n / d = (mulhi(n, m) + n) >> s.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((uint64_t{1} << s) < d) ++s;
+  const uint64_t m = ((uint64_t{1} << 32) * ((uint64_t{1} << s) - d)) / d + 1;
+  return FastDiv{d, static_cast<uint32_t>(m), s};
+}
+
+inline uint32_t fastdiv_host(uint32_t n, const FastDiv& f) {
+  const uint32_t t = static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> 32);
+  return (t + n) >> f.s;
+}
+
 // int32 accumulators on float codes with per-sample input zero points (compat surface).
 hipError_t launch_qi32_direct(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w,
                               int32_t* y, const void* in_qp, const void* f_qp, hipStream_t stream);
@@ -62,6 +82,11 @@ hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t*
                           hipStream_t stream);
 
 #if defined(__HIPCC__)
+__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
+  const uint32_t un = static_cast<uint32_t>(n);
+  return static_cast<int>((__umulhi(un, f.m) + un) >> f.s);
+}
+
 // ---- epilogue arithmetic shared by every int8 kernel --------------------------------
 // Each step is one IEEE-754 single operation with round-to-nearest-even, in this order,
 // so the GPU result equals the host restatement bit for bit (no contraction: the

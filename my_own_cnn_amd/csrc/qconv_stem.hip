@@ -25,6 +25,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kNseg = 4;
+constexpr int kStageBatch = 8;  // dword loads in flight per thread while staging
 constexpr int kLdsBudget = 64 * 1024;
 
 struct StemArgs {
@@ -41,6 +42,7 @@ struct StemArgs {
   int PL, P;        // left zero pad and pitch (bytes) of one staged input row
   int w_off;        // LDS byte offset of the staged filter slice
   int w_bytes;      // LDS bytes reserved for it
+  int ep_off;       // LDS byte offset of the 64 biases and 64 multipliers
   int row_dw;       // input rows are dword aligned (W*C % 4 == 0)
   float act_scale;
   int relu;
@@ -61,50 +63,66 @@ i8_stem_kernel(StemArgs a) {
   const int HR = (rows - 1) * a.sh + (a.R - 1) * a.dh + 1;
   const int hi0 = ho0 * a.sh - a.ph;
 
-  // ---- filter slice [k0, k0+kn): contiguous bytes of the KRSC filter ----
+  // ---- filter slice [k0, k0+kn) (contiguous bytes of the KRSC filter) and the input rows
+  // hi0 .. hi0+HR-1 (full width, zero columns left and right) -> LDS; every load of both is
+  // issued before the first LDS write waits on it ----
   unsigned char* wl = smem + a.w_off;
   {
     const int kn = min(64, a.K - k0);
     const int L = kn * a.RSC;  // 4-aligned start: k0 * RSC is a multiple of 64
-    const unsigned char* src = reinterpret_cast<const unsigned char*>(a.w) + static_cast<size_t>(k0) * a.RSC;
-    const int ndw = a.w_bytes >> 2;
-    for (int i = tid; i < ndw; i += kThreads) {
-      const int b = i * 4;
-      unsigned v = 0;
-      if (b + 4 <= L) {
-        v = *reinterpret_cast<const unsigned*>(src + b);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (b + e < L) v |= static_cast<unsigned>(src[b + e]) << (8 * e);
-      }
-      reinterpret_cast<unsigned*>(wl)[i] = v;
-    }
-  }
-
-  // ---- input rows hi0 .. hi0+HR-1, full width, zero columns left/right ----
-  {
+    const unsigned char* wsrc = reinterpret_cast<const unsigned char*>(a.w) + static_cast<size_t>(k0) * a.RSC;
+    const int ndw_w = a.w_bytes >> 2;
     const int dw_per_row = a.P >> 2;
+    const int ndw_x = HR * dw_per_row;
     const int rowb = a.W * a.C;
     const unsigned char* ximg = reinterpret_cast<const unsigned char*>(a.x) + static_cast<size_t>(n) * a.H * rowb;
-    for (int i = tid; i < HR * dw_per_row; i += kThreads) {
-      const int hr = i / dw_per_row;
-      const int b = (i - hr * dw_per_row) * 4 - a.PL;  // byte index in the input row
-      const int hi = hi0 + hr;
-      unsigned v = 0;
-      if (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) && b + 4 > 0 && b < rowb) {
-        const unsigned char* src = ximg + static_cast<size_t>(hi) * rowb;
-        if (a.row_dw && b >= 0 && b + 4 <= rowb) {
-          v = *reinterpret_cast<const unsigned*>(src + b);
-        } else {
+    const int total = ndw_x + ndw_w;
+    for (int base = tid; base < total; base += kThreads * kStageBatch) {
+      unsigned tmp[kStageBatch];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (b + e >= 0 && b + e < rowb) v |= static_cast<unsigned>(src[b + e]) << (8 * e);
+      for (int u = 0; u < kStageBatch; ++u) {
+        const int i = base + u * kThreads;
+        unsigned v = 0;
+        if (i < ndw_x) {
+          const int hr = i / dw_per_row;
+          const int b = (i - hr * dw_per_row) * 4 - a.PL;  // byte index in the input row
+          const int hi = hi0 + hr;
+          if (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) && b + 4 > 0 && b < rowb) {
+            const unsigned char* src = ximg + static_cast<size_t>(hi) * rowb;
+            if (a.row_dw && b >= 0 && b + 4 <= rowb) {
+              v = *reinterpret_cast<const unsigned*>(src + b);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (b + e >= 0 && b + e < rowb) v |= static_cast<unsigned>(src[b + e]) << (8 * e);
+            }
+          }
+        } else if (i < total) {
+          const int b = (i - ndw_x) * 4;
+          if (b + 4 <= L) {
+            v = *reinterpret_cast<const unsigned*>(wsrc + b);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (b + e < L) v |= static_cast<unsigned>(wsrc[b + e]) << (8 * e);
+          }
+        }
+        tmp[u] = v;
+      }
+#pragma unroll
+      for (int u = 0; u < kStageBatch; ++u) {
+        const int i = base + u * kThreads;
+        if (i < ndw_x) {
+          reinterpret_cast<unsigned*>(smem)[i] = tmp[u];
+        } else if (i < total) {
+          reinterpret_cast<unsigned*>(wl)[i - ndw_x] = tmp[u];
         }
       }
-      reinterpret_cast<unsigned*>(smem)[i] = v;
     }
   }
+  int32_t* ep_bias = reinterpret_cast<int32_t*>(smem + a.ep_off);
+  float* ep_mult = reinterpret_cast<float*>(smem + a.ep_off) + 64;
+  stage_requant<EPI>(Requant{a.bias, a.wscale, a.act_scale, a.relu}, k0, a.K - k0, 64, ep_bias, ep_mult);
   __syncthreads();
 
   const int row_l = lane & 15;
@@ -138,13 +156,9 @@ i8_stem_kernel(StemArgs a) {
 
   const int npix = rows * a.Wo;
   const int nseg = (npix + 15) >> 4;
-  const Requant rq{a.bias, a.wscale, a.act_scale, a.relu};
   const int kc0 = 16 * grp_l;  // first of this lane's 16 output channels (relative to k0)
   const bool kvalid = k0 + kc0 < a.K;
   const bool full = (k0 + kc0 + 16 <= a.K) && ((a.K & 15) == 0);
-  int32_t bv[16];
-  float mv[16];
-  load_requant16<EPI>(rq, k0 + kc0, a.K, k0 + kc0, bv, mv);
 
   for (int sg0 = wave * kNseg; sg0 < nseg; sg0 += 4 * kNseg) {
     int ob[kNseg];
@@ -193,7 +207,7 @@ i8_stem_kernel(StemArgs a) {
       const int lwo = p - lho * a.Wo;
       const size_t opix = (static_cast<size_t>(n) * a.Ho + (ho0 + lho)) * a.Wo + lwo;
       const v4i frag[4] = {acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
-      store16<EPI>(a.y, opix * a.K + k0 + kc0, frag, k0 + kc0, a.K, full, bv, mv, a.relu);
+      store16<EPI>(a.y, opix * a.K + k0 + kc0, frag, k0 + kc0, a.K, full, ep_bias + kc0, ep_mult + kc0, a.relu);
     }
   }
 }
@@ -201,7 +215,7 @@ i8_stem_kernel(StemArgs a) {
 struct StemPlan {
   int RowB, CPR, NQ, KB;
   int RB, tiles_h;
-  int PL, P, w_off, w_bytes;
+  int PL, P, w_off, w_bytes, ep_off;
   size_t lds;
 };
 
@@ -228,7 +242,7 @@ bool make_plan(const Geom& g, StemPlan* pl) {
   int RB = std::max(1, std::min(g.Ho, 256 / std::max(1, g.Wo)));
   auto lds_for = [&](int rb) {
     const long long HR = static_cast<long long>(rb - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
-    return HR * pl->P + pl->w_bytes;
+    return HR * pl->P + pl->w_bytes + 512;
   };
   while (RB > 1 && lds_for(RB) > kLdsBudget) --RB;
   if (lds_for(RB) > kLdsBudget) return false;
@@ -236,6 +250,7 @@ bool make_plan(const Geom& g, StemPlan* pl) {
   pl->tiles_h = (g.Ho + RB - 1) / RB;
   const long long HR = static_cast<long long>(RB - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
   pl->w_off = static_cast<int>(HR * pl->P);
+  pl->ep_off = pl->w_off + pl->w_bytes;
   pl->lds = static_cast<size_t>(lds_for(RB));
   return true;
 }
@@ -284,7 +299,7 @@ hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t*
   a.SC = g.S * g.C; a.RSC = g.R * a.SC;
   a.CPR = pl.CPR; a.NQ = pl.NQ;
   a.RB = pl.RB; a.tiles_h = pl.tiles_h;
-  a.PL = pl.PL; a.P = pl.P; a.w_off = pl.w_off; a.w_bytes = pl.w_bytes;
+  a.PL = pl.PL; a.P = pl.P; a.w_off = pl.w_off; a.w_bytes = pl.w_bytes; a.ep_off = pl.ep_off;
   a.row_dw = ((g.W * g.C) % 4 == 0) ? 1 : 0;
   a.act_scale = rq.act_scale;
   a.relu = rq.relu;
