@@ -47,7 +47,25 @@ def parse():
     ap.add_argument("--algo", default="auto")
     ap.add_argument("--all", action="store_true", help="also print a per-config table on stderr")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many MiB (counter calibration)")
     return ap.parse_args()
+
+
+def copy_calibration(mib: int) -> None:
+    """A plain copy kernel of known size: the reference point that scales the FETCH_SIZE /
+    WRITE_SIZE counters of rocprofv3 into bytes."""
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    for _ in range(3):
+        flush.fill_(1)  # evicts src/dst from L2 and MALL between copies
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "launches": 3}), flush=True)
 
 
 def cpu_model() -> str:
@@ -89,6 +107,9 @@ def cpu_baseline(wl):
 
 def main():
     args = parse()
+    if args.copy_mb:
+        copy_calibration(args.copy_mb)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding of the convolution is described in DESIGN.md, not benchmarked", file=sys.stderr)

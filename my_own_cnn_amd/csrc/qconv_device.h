@@ -86,21 +86,18 @@ __device__ __forceinline__ void store16(void* y, size_t obase, const v4i (&acc)[
   }
 }
 
-// Exact round-to-nearest-even of a float already clamped to [lo, 127] with lo >= -128:
-// adding 1.5 * 2^23 lands every such value in [2^23, 2^24), where the float grid is the
-// integers, so the IEEE addition itself rounds (ties to even); the result's bit pattern is
-// 0x4B400000 + q, whose low byte is q in two's complement.
-__device__ __forceinline__ unsigned rne_byte(float clamped) {
-  return __float_as_uint(clamped + 12582912.0f) & 0xffu;
-}
-
 // As store16, for accumulators that already include the bias (they were initialised with
-// it): requantizes with the per-channel multipliers at `ep_mult` (LDS).  For int8 output,
-// rint then clamp equals clamp then rint because the bounds are integers, and
-// fmaxf(NaN, lo) = lo gives the NaN rule.
+// it): requantizes with the per-channel multipliers at `ep_mult` (LDS).
+//
+// int8: q = clamp(rint(v), lo, 127) computed as rint(med3(v, lo, 127)) - equal because
+// the bounds are integers - in four instructions per value: convert, multiply,
+// v_med3_f32 (which returns its lower bound, lo, for a NaN input: the NaN rule), and the
+// 1.5 * 2^23 addition that rounds; v_perm_b32 gathers the four low bytes.
 template <int EPI>
-__device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i (&acc)[4], int kc0, int Kg, bool full,
-                                               const float* ep_mult, int relu) {
+__device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i& a0, const v4i& a1, const v4i& a2,
+                                               const v4i& a3, int kc0, int Kg, bool full, const float* ep_mult,
+                                               int relu) {
+  const v4i* acc[4] = {&a0, &a1, &a2, &a3};
   if constexpr (EPI == kEpiI8) {
     const float lo = relu ? 0.0f : -128.0f;
     int8_t* yp = static_cast<int8_t*>(y) + obase;
@@ -108,16 +105,19 @@ __device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const v4f mm = reinterpret_cast<const v4f*>(ep_mult)[j];
-      unsigned u = 0;
+      unsigned u[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float v = static_cast<float>(acc[j][r]) * mm[r];
-        const float c = fminf(fmaxf(v, lo), 127.0f);
-        const unsigned byte = rne_byte(c);
-        u |= byte << (8 * r);
-        if (!full && kc0 + 4 * j + r < Kg) yp[4 * j + r] = static_cast<int8_t>(byte);
+        const float v = static_cast<float>((*acc[j])[r]) * mm[r];
+        u[r] = __float_as_uint(__builtin_amdgcn_fmed3f(v, lo, 127.0f) + 12582912.0f);
       }
-      pk[j] = static_cast<int>(u);
+      pk[j] = static_cast<int>(__builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u) |
+                               __builtin_amdgcn_perm(u[3], u[2], 0x04000c0cu));
+      if (!full) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = static_cast<int8_t>(u[r] & 0xffu);
+      }
     }
     if (full) *reinterpret_cast<v4i*>(yp) = pk;
   } else if constexpr (EPI == kEpiAcc32) {
@@ -127,11 +127,11 @@ __device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (full) {
-        reinterpret_cast<v4i*>(yp)[j] = acc[j];
+        reinterpret_cast<v4i*>(yp)[j] = *acc[j];
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = acc[j][r];
+          if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = (*acc[j])[r];
       }
     }
   } else {
@@ -142,7 +142,7 @@ __device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i 
       v4f f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float v = static_cast<float>(acc[j][r]) * mm[r];
+        float v = static_cast<float>((*acc[j])[r]) * mm[r];
         if (relu) v = (v > 0.0f) ? v : 0.0f;
         f[r] = v;
       }

@@ -33,8 +33,9 @@
 // The K-loop is software-pipelined: the fragments of K-block b+1 are read from LDS while
 // the MFMAs of K-block b run.  Accumulators start at the bias, so the epilogue is
 // convert, scale, clamp, round: round-to-nearest-even comes from adding 1.5*2^23 to the
-// clamped value (exact IEEE rounding of a value in [-128, 127]), whose low byte is then
-// the two's-complement int8 result.
+// clamped value (exact IEEE rounding of a value in [-128, 127]: the sum lands in
+// [2^23, 2^24), where the float grid is the integers), whose low byte is then the
+// two's-complement int8 result.
 
 #include "qconv_device.h"
 
@@ -300,8 +301,8 @@ i8_igemm_kernel(IgemmArgs a) {
 #pragma unroll
     for (int i = 0; i < NSEG; ++i) {
       if (!pv[i]) continue;
-      const v4i frag[4] = {acc[t][0][i], acc[t][1][i], acc[t][2][i], acc[t][3][i]};
-      store16_biased<EPI>(a.y, static_cast<size_t>(opix[i]) * a.K + kabs, frag, kc0, a.Kg, full, ep_mult + lc, a.relu);
+      store16_biased<EPI>(a.y, static_cast<size_t>(opix[i]) * a.K + kabs, acc[t][0][i], acc[t][1][i], acc[t][2][i],
+                          acc[t][3][i], kc0, a.Kg, full, ep_mult + lc, a.relu);
     }
   }
 }

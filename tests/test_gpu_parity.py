@@ -216,3 +216,20 @@ def test_empty_batch(device):
     y = M.qconv2d_nhwc_i8_acc32(x, w, padding=1)
     torch.cuda.synchronize()
     assert tuple(y.shape) == (0, 8, 8, 16)
+
+
+def test_non_finite_scales_follow_the_definition(device):
+    # NaN -> lo, +inf -> 127 (acc > 0) / lo (acc < 0), 0 * inf -> NaN -> lo; every kernel family
+    c = cases.int8_cases()["c16_k32_3x3"]
+    k = c["w"].shape[0]
+    ws = np.full(k, 5e-3, np.float32)
+    ws[0], ws[1], ws[2], ws[3] = np.nan, np.inf, -np.inf, 0.0
+    bias = np.zeros(k, np.int32)
+    bias[4] = -c["y"][..., 4].max() - 1   # pushes every value of channel 4 below lo
+    xd, wd, bd, sd = dev(c["x"], device), dev(c["w"], device), dev(bias, device), dev(ws, device)
+    for relu in (False, True):
+        want = oracle.requant_i8(c["y"], bias, ws, 0.02, 1.0, relu)
+        for algo in algos_for(c["x"], c["w"], c["conv"]):
+            q = M.qconv2d_nhwc_i8(xd, wd, bd, sd, relu=relu, in_scale=0.02, algo=algo, **conv_kwargs(c["conv"]))
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(q.cpu().numpy(), want, err_msg=f"{algo} relu={relu}")
