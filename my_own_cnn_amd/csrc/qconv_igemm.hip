@@ -12,11 +12,13 @@
 // channels of one pixel (4 rows x 4 MFMAs), which the epilogue writes as one 16-byte
 // int8 store (or four 16-byte int32/fp32 stores): a wave writes 16 pixels x 64 channels.
 //
-// Work decomposition: a workgroup (4 waves) owns one tile of RB output rows x CB output
-// columns of one image (at most one pass of every wave: WAVES_P*NSEG*16 pixels) and
-// KT_WG = 64*NKT*WAVES_K output channels of one group.  Each wave computes NKT 64-channel
-// tiles x NSEG 16-pixel segments; per K-block it reads 4*NKT filter fragments and NSEG
-// input fragments (1 KB each) from LDS for 4*NKT*NSEG MFMAs.
+// Work decomposition: a workgroup (WAVES = 4 or 8 waves) owns one tile of RB output rows x
+// CB output columns of one image (one pass of every wave: at most WAVES_P*NSEG 16-pixel
+// segments, interleaved over the waves) and KT_WG = 64*NKT*WAVES_K output channels of one
+// group.  Each wave computes NKT 64-channel tiles x up to NSEG segments; per K-block it
+// reads 4*NKT filter fragments and one input fragment per segment (1 KB each) from LDS.
+// The host picks the tile so that every SIMD gets as even a share of segments as the
+// problem allows (8-wave workgroups let one filter copy in LDS serve a whole CU).
 //
 // LDS holds, per workgroup: the bias and requantization multiplier of its channels; the
 // filter, in fragment order (one 1 KB block per (K-block, 64-channel tile, j), lane l's 16
@@ -40,11 +42,11 @@
 #include "qconv_device.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace miq {
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int kLdsBudget = 160 * 1024;   // LDS bytes per workgroup on gfx950
 constexpr int kLdsPreferred = 76 * 1024; // two workgroups per CU
 
@@ -89,13 +91,13 @@ __device__ __forceinline__ void load_lds16(const void* src, v4i* lds_wave_base) 
 
 // Filter fragments of K-blocks [b0, b0 + nb) of the workgroup's channels into `dst`
 // (fragment order).  Fragment f = (bl * CT + ct) * 4 + j goes to dst + f * 64 (v4i units).
-template <int CT>
+template <int CT, int WAVES>
 __device__ __forceinline__ void stage_filter(const IgemmArgs& a, const int8_t* wg, int kwg0, int b0, int nb, v4i* dst,
                                              int wave, int lane) {
   const int nfrag = nb * CT * 4;
   const int row_l = lane & 15;
   const int grp_l = lane >> 4;
-  for (int f = wave; f < nfrag; f += 4) {
+  for (int f = wave; f < nfrag; f += WAVES) {
     const int j = f & 3;
     const int ct = (f >> 2) % CT;
     const int bl = (f >> 2) / CT;
@@ -110,10 +112,10 @@ __device__ __forceinline__ void stage_filter(const IgemmArgs& a, const int8_t* w
   }
 }
 
-template <int NKT, int NSEG, int WAVES_K, int EPI, bool TAPU>
-__global__ void __launch_bounds__(kThreads, NKT == 1 ? 2 : 1)  // two waves per SIMD where it does not spill
+template <int NKT, int NSEG, int WAVES_K, int EPI, bool TAPU, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES, (NKT == 1 && WAVES == 4) ? 2 : 1)  // two waves per SIMD
 i8_igemm_kernel(IgemmArgs a) {
-  constexpr int WAVES_P = 4 / WAVES_K;
+  constexpr int WAVES_P = WAVES / WAVES_K;
   constexpr int KTILE = 64 * NKT;          // output channels per wave
   constexpr int KT_WG = KTILE * WAVES_K;   // output channels per workgroup
   constexpr int CT = KT_WG / 64;           // 64-channel tiles per workgroup
@@ -152,12 +154,12 @@ i8_igemm_kernel(IgemmArgs a) {
   const int cols = min(a.CB, a.Wo - wo0);
 
   // ---- staging: filter chunk 0 and the halo (direct loads), epilogue parameters ----
-  stage_filter<CT>(a, wg, kwg0, 0, min(a.KBC, a.KB), wbuf0, wave, lane);
+  stage_filter<CT, WAVES>(a, wg, kwg0, 0, min(a.KBC, a.KB), wbuf0, wave, lane);
   {
     const int hi0 = ho0 * a.sh - a.ph;
     const int wi0 = wo0 * a.sw - a.pw;
     const int8_t* xg = a.x + static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg;
-    for (int u = wave; u * 64 < a.nslot; u += 4) {
+    for (int u = wave; u * 64 < a.nslot; u += WAVES) {
       const int L = u * 64 + lane;  // LDS slot this lane fills
       if (L < a.nslot) {
         const int plane = fdiv(L, a.fd_ps);
@@ -185,12 +187,15 @@ i8_igemm_kernel(IgemmArgs a) {
 
   const bool wave_active = kwave0 < a.Kg;  // waves past the last channel still join every barrier
 
-  // per segment: halo slot of tap (0,0) / chunk 0 for this lane's pixel, output pixel index
+  // per segment: halo slot of tap (0,0) / chunk 0 for this lane's pixel, output pixel index.
+  // Segments are interleaved over the waves; sv[i] (wave-uniform) marks the ones that exist.
+  const int nseg_tile = (rows * a.CB + 15) >> 4;
   int pix_off[NSEG], opix[NSEG];
-  bool pv[NSEG];
+  bool pv[NSEG], sv[NSEG];
 #pragma unroll
   for (int i = 0; i < NSEG; ++i) {
-    const int p = (wp * NSEG + i) * 16 + row_l;
+    sv[i] = wp + i * WAVES_P < nseg_tile;
+    const int p = (wp + i * WAVES_P) * 16 + row_l;
     const int lho = fdiv(p, a.fd_cb);
     const int lwo = p - lho * a.CB;
     pv[i] = lho < rows && lwo < cols;
@@ -251,12 +256,14 @@ i8_igemm_kernel(IgemmArgs a) {
   };
   auto mma = [&](const v4i (&A)[NKT][4], const v4i (&B)[NSEG]) {
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+    for (int i = 0; i < NSEG; ++i) {
+      if (!sv[i]) continue;  // wave-uniform
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int t = 0; t < NKT; ++t)
 #pragma unroll
-        for (int i = 0; i < NSEG; ++i)
+        for (int j = 0; j < 4; ++j)
           acc[t][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[t][j], B[i], acc[t][j][i], 0, 0, 0);
+    }
   };
 
   for (int c = 0; c < a.nchunks; ++c) {
@@ -264,7 +271,8 @@ i8_igemm_kernel(IgemmArgs a) {
     const int nb = min(a.KBC, a.KB - b0);
     const v4i* wb = (c & 1) ? wbuf1 : wbuf0;
     if (c + 1 < a.nchunks) {  // next chunk streams in behind this one
-      stage_filter<CT>(a, wg, kwg0, b0 + a.KBC, min(a.KBC, a.KB - b0 - a.KBC), (c & 1) ? wbuf0 : wbuf1, wave, lane);
+      stage_filter<CT, WAVES>(a, wg, kwg0, b0 + a.KBC, min(a.KBC, a.KB - b0 - a.KBC), (c & 1) ? wbuf0 : wbuf1, wave,
+                               lane);
     }
     if (wave_active) {
       v4i A0[NKT][4], A1[NKT][4], B0[NSEG], B1[NSEG];
@@ -309,7 +317,7 @@ i8_igemm_kernel(IgemmArgs a) {
 
 // Host-side tiling decision for one problem.
 struct IgemmPlan {
-  int nkt, waves_k, nseg;
+  int nkt, waves_k, nseg, waves;
   int KBC, nchunks;
   int RB, CB, tiles_h, tiles_w, kt_per_group;
   int w_off, h_off, w_buf_bytes;
@@ -340,8 +348,25 @@ size_t halo_bytes(const Geom& g, int RB, int CB) {
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
+// Compute units of the current device (one query per device; 256 when no device answers).
+int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Chooses the channel split, the workgroup size (4 or 8 waves) and the tile.  The cost of a
+// candidate is, per round of resident workgroups, the largest number of 16-pixel segments
+// one SIMD works through, plus a share for the segments of the whole CU (LDS and L1
+// bandwidth are per CU) and a fixed per-round cost for staging and the epilogue; the
+// cheapest candidate wins (ties: taller tiles, which re-read less halo).
 bool make_plan(const Geom& g, IgemmPlan* pl) {
-  // Channel tiling: a wave covers 64*nkt channels, waves_k waves split the channels.
   if (g.Kg <= 64) {
     pl->nkt = 1; pl->waves_k = 1;
   } else if (g.Kg <= 128) {
@@ -353,75 +378,110 @@ bool make_plan(const Geom& g, IgemmPlan* pl) {
   }
   pl->nseg = pl->nkt == 2 ? 2 : 4;  // keeps two waves per SIMD (registers)
   const int kt_wg = 64 * pl->nkt * pl->waves_k;
-  const int waves_p = 4 / pl->waves_k;
-  const int tile_px = waves_p * pl->nseg * 16;
   pl->kt_per_group = (g.Kg + kt_wg - 1) / kt_wg;
   const int kb = (g.R * g.S * (g.Cg / 16) + 3) / 4;
   const size_t kblock_bytes = static_cast<size_t>(kt_wg) * 64;  // filter bytes of one K-block
   const size_t ep_bytes = round_up(static_cast<size_t>(kt_wg) * 8, 1024);
-
-  // Spatial tiling: whole output rows if they are short, else row segments; one pass of
-  // every wave.  Prefer the row count that leaves the fewest idle lanes (ties: taller).
-  int CB = std::min(g.Wo, tile_px);
-  int RB = std::max(1, std::min(g.Ho, tile_px / CB));
+  const int cus = device_cu_count();
   auto lds_total = [&](int rb, int cb, int kbc, int nbuf) {
     return ep_bytes + nbuf * kbc * kblock_bytes + round_up(halo_bytes(g, rb, cb), 1024);
   };
-  // Filter staging: the whole filter in one buffer when that keeps two workgroups per CU;
-  // else the largest double-buffered chunk that does; else the whole filter or chunks within
-  // the full LDS of one workgroup.
-  auto fit = [&](int rb, int cb, int* kbc, int* nbuf) {
-    const size_t limits[2] = {static_cast<size_t>(kLdsPreferred), static_cast<size_t>(kLdsBudget)};
-    for (size_t lim : limits) {
-      if (lds_total(rb, cb, kb, 1) <= lim) {
-        *kbc = kb;
-        *nbuf = 1;
-        return true;
-      }
-      for (int c = kb - 1; c >= 1; --c) {
-        if (lds_total(rb, cb, c, 2) <= lim) {
-          *kbc = c;
-          *nbuf = 2;
+
+  bool found = false;
+  double best = 0.0;
+  for (int waves : {4, 8}) {
+    if (waves == 8 && pl->nkt != 1) continue;
+    const int waves_p = waves / pl->waves_k;
+    const int pass_segs = waves_p * pl->nseg;
+    // Filter staging: whole when that keeps two workgroups per CU (4-wave) / fits (8-wave);
+    // else the largest double-buffered chunk that does; else anything within the full LDS.
+    const size_t preferred = waves == 4 ? 76 * 1024 : static_cast<size_t>(kLdsBudget);
+    auto fit = [&](int rb, int cb, int* kbc, int* nbuf) {
+      const size_t limits[2] = {preferred, static_cast<size_t>(kLdsBudget)};
+      for (size_t lim : limits) {
+        if (lds_total(rb, cb, kb, 1) <= lim) {
+          *kbc = kb;
+          *nbuf = 1;
           return true;
         }
+        for (int c = kb - 1; c >= 1; --c) {
+          if (lds_total(rb, cb, c, 2) <= lim) {
+            *kbc = c;
+            *nbuf = 2;
+            return true;
+          }
+        }
+      }
+      return false;
+    };
+    int CB = std::min(g.Wo, pass_segs * 16);
+    int kbc = 0, nbuf = 0;
+    while (CB > 16 && !fit(1, CB, &kbc, &nbuf)) CB -= 16;
+    if (!fit(1, CB, &kbc, &nbuf)) continue;
+    const int tiles_w = (g.Wo + CB - 1) / CB;
+    for (int rb = 1; rb <= g.Ho; ++rb) {
+      const int segs = (rb * CB + 15) / 16;
+      if (segs > pass_segs) break;
+      if (!fit(rb, CB, &kbc, &nbuf)) break;
+      const size_t lds = lds_total(rb, CB, kbc, nbuf);
+      const long long tiles = static_cast<long long>(g.N) * ((g.Ho + rb - 1) / rb) * tiles_w * g.G * pl->kt_per_group;
+      const int wg_per_cu = (waves == 8 || lds > 76 * 1024) ? 1 : 2;
+      const long long rounds = (tiles + static_cast<long long>(cus) * wg_per_cu - 1) / (static_cast<long long>(cus) * wg_per_cu);
+      // segments of the busiest SIMD in one round: SIMD s runs waves s, s+4 of the resident workgroups
+      auto segs_of = [&](int wp) { return wp < segs % waves_p ? segs / waves_p + 1 : segs / waves_p; };
+      int per_simd = 0;
+      const int per_cu = (waves == 8 ? 1 : wg_per_cu) * segs;  // shares LDS / L1 bandwidth of one CU
+      for (int sm = 0; sm < 4; ++sm) {
+        int load = 0;
+        if (waves == 8) {
+          load = segs_of(sm / pl->waves_k) + segs_of((sm + 4) / pl->waves_k);
+        } else {
+          load = wg_per_cu * segs_of(sm / pl->waves_k);
+        }
+        per_simd = std::max(per_simd, load);
+      }
+      const double cost = static_cast<double>(rounds) * (per_simd + 0.125 * per_cu + 3.0 * wg_per_cu);
+      if (!found || cost < best - 1e-9 || (cost <= best + 1e-9 && rb >= pl->RB && waves == pl->waves)) {
+        found = true;
+        best = cost;
+        pl->waves = waves;
+        pl->RB = rb;
+        pl->CB = CB;
+        pl->KBC = kbc;
+        pl->nchunks = (kb + kbc - 1) / kbc;
+        pl->tiles_h = (g.Ho + rb - 1) / rb;
+        pl->tiles_w = tiles_w;
+        pl->w_off = static_cast<int>(ep_bytes);
+        pl->w_buf_bytes = static_cast<int>(kbc * kblock_bytes);
+        pl->h_off = static_cast<int>(ep_bytes + nbuf * kbc * kblock_bytes);
+        pl->lds_bytes = lds;
       }
     }
-    return false;
-  };
-  int kbc = 0, nbuf = 0;
-  while (RB > 1 && !fit(RB, CB, &kbc, &nbuf)) --RB;
-  while (CB > 16 && !fit(RB, CB, &kbc, &nbuf)) CB -= 16;
-  if (!fit(RB, CB, &kbc, &nbuf)) return false;
-  pl->RB = RB;
-  pl->CB = CB;
-  pl->KBC = kbc;
-  pl->nchunks = (kb + kbc - 1) / kbc;
-  pl->tiles_h = (g.Ho + RB - 1) / RB;
-  pl->tiles_w = (g.Wo + CB - 1) / CB;
-  pl->w_off = static_cast<int>(ep_bytes);
-  pl->w_buf_bytes = static_cast<int>(kbc * kblock_bytes);
-  pl->h_off = static_cast<int>(ep_bytes + nbuf * kbc * kblock_bytes);
-  pl->lds_bytes = lds_total(RB, CB, kbc, nbuf);
-  return true;
+  }
+  return found;
 }
 
-template <int NKT, int NSEG, int WAVES_K, int EPI, bool TAPU>
+template <int NKT, int NSEG, int WAVES_K, int EPI, bool TAPU, int WAVES>
 void launch_cfg(const IgemmArgs& a, const IgemmPlan& pl, int N, int G, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(N * pl.tiles_h * pl.tiles_w), static_cast<unsigned>(G * pl.kt_per_group));
-  auto kern = i8_igemm_kernel<NKT, NSEG, WAVES_K, EPI, TAPU>;
+  auto kern = i8_igemm_kernel<NKT, NSEG, WAVES_K, EPI, TAPU, WAVES>;
   if (pl.lds_bytes > 64 * 1024) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>(pl.lds_bytes));
   }
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.lds_bytes, stream, a);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * WAVES), pl.lds_bytes, stream, a);
 }
 
 template <int NKT, int WAVES_K, int EPI, bool TAPU>
 void launch_nseg(const IgemmArgs& a, const IgemmPlan& pl, int N, int G, hipStream_t stream) {
   if constexpr (NKT == 2) {
-    launch_cfg<NKT, 2, WAVES_K, EPI, TAPU>(a, pl, N, G, stream);
+    launch_cfg<NKT, 2, WAVES_K, EPI, TAPU, 4>(a, pl, N, G, stream);
   } else {
-    launch_cfg<NKT, 4, WAVES_K, EPI, TAPU>(a, pl, N, G, stream);
+    if (pl.waves == 8) {
+      launch_cfg<NKT, 4, WAVES_K, EPI, TAPU, 8>(a, pl, N, G, stream);
+    } else {
+      launch_cfg<NKT, 4, WAVES_K, EPI, TAPU, 4>(a, pl, N, G, stream);
+    }
   }
 }
 
