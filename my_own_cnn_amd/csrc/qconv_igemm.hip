@@ -43,6 +43,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 namespace miq {
 namespace {
@@ -112,6 +113,34 @@ __device__ __forceinline__ void stage_filter(const IgemmArgs& a, const int8_t* w
   }
 }
 
+// Scheduling groups for one K-block step: MFMA, LDS read, MFMA, LDS read, ... then the
+// remaining MFMAs (or reads).
+template <int NMFMA, int NREAD>
+__device__ __forceinline__ void interleave_mfma_ds() {
+  if constexpr (NMFMA > 0 && NREAD > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+    interleave_mfma_ds<NMFMA - 1, NREAD - 1>();
+  } else if constexpr (NMFMA > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);
+  } else if constexpr (NREAD > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
+  }
+}
+
+// Calls f(std::integral_constant<int, n>) for a wave-uniform 1 <= n <= NMAX (nothing for n
+// == 0): one branch-free instantiation of the callee per count.
+template <int NMAX, typename F>
+__device__ __forceinline__ void dispatch_count(int n, F&& f) {
+  if constexpr (NMAX > 0) {
+    if (n == NMAX) {
+      f(std::integral_constant<int, NMAX>{});
+    } else {
+      dispatch_count<NMAX - 1>(n, f);
+    }
+  }
+}
+
 template <int NKT, int NSEG, int WAVES_K, int EPI, bool TAPU, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES, (NKT == 1 && WAVES == 4) ? 2 : 1)  // two waves per SIMD
 i8_igemm_kernel(IgemmArgs a) {
@@ -128,7 +157,7 @@ i8_igemm_kernel(IgemmArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: wave-level branches stay scalar
   const int wk = wave % WAVES_K;
   const int wp = wave / WAVES_K;
   const int row_l = lane & 15;  // MFMA row (A) / column (B) of this lane
@@ -188,18 +217,20 @@ i8_igemm_kernel(IgemmArgs a) {
   const bool wave_active = kwave0 < a.Kg;  // waves past the last channel still join every barrier
 
   // per segment: halo slot of tap (0,0) / chunk 0 for this lane's pixel, output pixel index.
-  // Segments are interleaved over the waves; sv[i] (wave-uniform) marks the ones that exist.
+  // Segments are interleaved over the waves: segment i of this wave is tile segment
+  // wp + i * WAVES_P, and the first nsv of them exist (wave-uniform).
   const int nseg_tile = (rows * a.CB + 15) >> 4;
+  const int nsv = wave_active ? min(NSEG, max(0, (nseg_tile - wp + WAVES_P - 1) / WAVES_P)) : 0;
   int pix_off[NSEG], opix[NSEG];
-  bool pv[NSEG], sv[NSEG];
+  bool pv[NSEG];
 #pragma unroll
   for (int i = 0; i < NSEG; ++i) {
-    sv[i] = wp + i * WAVES_P < nseg_tile;
     const int p = (wp + i * WAVES_P) * 16 + row_l;
     const int lho = fdiv(p, a.fd_cb);
     const int lwo = p - lho * a.CB;
     pv[i] = lho < rows && lwo < cols;
-    pix_off[i] = lho * a.sh * a.HCs + lwo;
+    // pixels outside the tile read slot 0 (finite data, never stored): no predication in the K-loop
+    pix_off[i] = pv[i] ? lho * a.sh * a.HCs + lwo : 0;
     opix[i] = (n * a.Ho + ho0 + lho) * a.Wo + wo0 + lwo;
   }
   const int grp_plane_off = grp_l * a.sw * a.PS;  // lane group g reads chunk c16 + g (TAPU)
@@ -218,10 +249,10 @@ i8_igemm_kernel(IgemmArgs a) {
     }
   }
 
-  // fragment loaders for one K-block
-  auto load_b = [&](int b, v4i (&B)[NSEG]) {
+  // fragment loaders for one K-block; `b` is clamped by the callers to [0, KB)
+  auto load_b = [&](int b, auto& B) {
+    constexpr int NS = std::extent<std::remove_reference_t<decltype(B)>>::value;
     int off;
-    bool qv;
     if constexpr (TAPU) {  // Cg16 % 4 == 0: the 4 chunks of a K-block belong to one tap
       const int q0 = 4 * b;
       const int tap = fdiv(q0, a.fd_cg16);
@@ -230,23 +261,17 @@ i8_igemm_kernel(IgemmArgs a) {
       const int sdw = (tap - rr * a.S) * a.dw;
       const int hq = fdiv(sdw, a.fd_sw);
       off = (cb * a.sw + (sdw - hq * a.sw)) * a.PS + rr * a.dh * a.HCs + hq + grp_plane_off;
-      qv = true;
     } else {
-      const int q = 4 * b + grp_l;
+      const int q = min(4 * b + grp_l, a.NQ - 1);  // past the last chunk the filter fragment is zero
       const int tap = fdiv(q, a.fd_cg16);
       const int c16 = q - tap * a.Cg16;
       const int rr = fdiv(tap, a.fd_s);
       const int sdw = (tap - rr * a.S) * a.dw;
       const int hq = fdiv(sdw, a.fd_sw);
       off = (c16 * a.sw + (sdw - hq * a.sw)) * a.PS + rr * a.dh * a.HCs + hq;
-      qv = q < a.NQ;
     }
 #pragma unroll
-    for (int i = 0; i < NSEG; ++i) {
-      v4i v = {0, 0, 0, 0};
-      if (qv && pv[i]) v = halo[pix_off[i] + off];
-      B[i] = v;
-    }
+    for (int i = 0; i < NS; ++i) B[i] = halo[pix_off[i] + off];
   };
   auto load_a = [&](const v4i* wb, int bl, v4i (&A)[NKT][4]) {
 #pragma unroll
@@ -254,16 +279,39 @@ i8_igemm_kernel(IgemmArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) A[t][j] = wb[((bl * CT + wk * NKT + t) * 4 + j) * 64 + lane];
   };
-  auto mma = [&](const v4i (&A)[NKT][4], const v4i (&B)[NSEG]) {
+  auto mma = [&](const v4i (&A)[NKT][4], const auto& B) {
+    constexpr int NS = std::extent<std::remove_reference_t<decltype(B)>>::value;
 #pragma unroll
-    for (int i = 0; i < NSEG; ++i) {
-      if (!sv[i]) continue;  // wave-uniform
+    for (int i = 0; i < NS; ++i)
 #pragma unroll
       for (int t = 0; t < NKT; ++t)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[t][j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[t][j], B[i], acc[t][j][i], 0, 0, 0);
+  };
+  // K-blocks [b0, b0 + nb) of the staged chunk `wb` for the first NS segments; branch-free
+  // inside, so LDS reads of K-block b+1 stay in flight under the MFMAs of K-block b.
+  auto kloop = [&](auto ns_tag, const v4i* wb, int b0, int nb) {
+    constexpr int NS = decltype(ns_tag)::value;
+    v4i A0[NKT][4], A1[NKT][4], B0[NS], B1[NS];
+    load_a(wb, 0, A0);
+    load_b(b0, B0);
+    int bl = 0;
+    // The reads of the next K-block are interleaved one by one with the first MFMAs of
+    // this one, so they complete under the remaining MFMAs.
+    constexpr int NMMA = NKT * 4 * NS, NRD = NKT * 4 + NS;
+    for (; bl + 2 <= nb; bl += 2) {
+      mma(A0, B0);
+      load_a(wb, bl + 1, A1);
+      load_b(b0 + bl + 1, B1);
+      interleave_mfma_ds<NMMA, NRD>();
+      const int bn = min(bl + 2, nb - 1);  // the last pass re-reads a valid K-block, unused
+      mma(A1, B1);
+      load_a(wb, bn, A0);
+      load_b(b0 + bn, B0);
+      interleave_mfma_ds<NMMA, NRD>();
     }
+    if (bl < nb) mma(A0, B0);
   };
 
   for (int c = 0; c < a.nchunks; ++c) {
@@ -274,23 +322,7 @@ i8_igemm_kernel(IgemmArgs a) {
       stage_filter<CT, WAVES>(a, wg, kwg0, b0 + a.KBC, min(a.KBC, a.KB - b0 - a.KBC), (c & 1) ? wbuf0 : wbuf1, wave,
                                lane);
     }
-    if (wave_active) {
-      v4i A0[NKT][4], A1[NKT][4], B0[NSEG], B1[NSEG];
-      load_a(wb, 0, A0);
-      load_b(b0, B0);
-      int bl = 0;
-      for (; bl + 2 <= nb; bl += 2) {
-        load_a(wb, bl + 1, A1);
-        load_b(b0 + bl + 1, B1);
-        mma(A0, B0);
-        if (bl + 2 < nb) {
-          load_a(wb, bl + 2, A0);
-          load_b(b0 + bl + 2, B0);
-        }
-        mma(A1, B1);
-      }
-      if (bl < nb) mma(A0, B0);
-    }
+    dispatch_count<NSEG>(nsv, [&](auto ns_tag) { kloop(ns_tag, wb, b0, nb); });
     if (c + 1 < a.nchunks) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
