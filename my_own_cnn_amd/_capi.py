@@ -28,7 +28,9 @@ MIQ_ALGO_AUTO = 0
 MIQ_ALGO_DIRECT = 1
 MIQ_ALGO_IGEMM = 2
 MIQ_ALGO_STEM = 3
-ALGOS = {"auto": MIQ_ALGO_AUTO, "direct": MIQ_ALGO_DIRECT, "igemm": MIQ_ALGO_IGEMM, "stem": MIQ_ALGO_STEM}
+MIQ_ALGO_BAND = 4
+ALGOS = {"auto": MIQ_ALGO_AUTO, "direct": MIQ_ALGO_DIRECT, "igemm": MIQ_ALGO_IGEMM, "stem": MIQ_ALGO_STEM,
+         "band": MIQ_ALGO_BAND}
 ALGO_NAMES = {v: k for k, v in ALGOS.items()}
 
 

@@ -28,6 +28,7 @@ SOURCES = [
     "qconv_direct.hip",
     "qconv_igemm.hip",
     "qconv_stem.hip",
+    "qconv_band.hip",
     "conv_quant_host.cpp",
     "verify.cpp",
     "bench.cpp",

@@ -1,0 +1,555 @@
+// int8 convolution for narrow feature maps (Wo <= 64) with small filters: row bands,
+// filter-stationary MFMA (v_mfma_i32_16x16x64_i8), the band's input rows staged in LDS.
+//
+// Work decomposition.  A workgroup of 8 waves (two per SIMD) owns a band of BH consecutive
+// output rows of one image and one 64-channel tile of one group.  Output rows are cut into
+// 16-pixel segments (segment column sc covers wo = 16*sc .. 16*sc + 15; the last one may
+// be partly outside the image).  Wave w owns segment column w % SEGR of the rows
+// t = w / SEGR (mod RPAR) of the band, one row per phase.  A SIMD runs two waves so that
+// one wave's LDS reads and epilogue overlap the other's MFMAs: one wave cannot overlap
+// them with its own matrix instructions.
+//
+// Filter-stationary.  Each wave keeps the whole 64-channel filter of the workgroup in
+// registers: KB = R*S*Cg/64 K-blocks x 4 MFMA row blocks of 16 bytes per lane.  The only
+// LDS traffic of the main loop is then the input fragments: 1 KB per K-block per segment,
+// shared by the 64 output channels of the 4 MFMAs that consume it.
+//
+// Input rows.  The band's input rows (its "halo": (BH-1)*sh + (R-1)*dh + 1 rows) go to
+// LDS as [row][chunk quad][16-column block][chunk in quad][column in block] x 16 bytes,
+// halo column c holding input column c - pw (a chunk is 16 channels, a quad 4 chunks).
+// One buffer_load_dwordx4 ... lds (global -> LDS without registers) fills one (row, quad,
+// block): its 64 lanes read 16 pixels x 64 channel bytes, one contiguous kilobyte of NHWC
+// input when the group has 64 channels.  The buffer range check turns every padding
+// position into zeros (an out-of-image row or column gets an offset past num_records), so
+// no lane is predicated.  The 16 lanes of an MFMA lane group
+// read 16 consecutive columns of one chunk: their 16-byte slots are distinct modulo 16,
+// so the read is free of bank conflicts for any column shift.
+//
+// Loads.  Every load of the workgroup (filter, epilogue parameters, the band's input rows)
+// is issued at the start, spread over the 8 waves, with one buffer resource per tensor and
+// a few scalar instructions per load: scalar work is shared by the waves of a SIMD and a
+// long scalar loop delays everything behind it.  Kernel arguments are preloaded in one
+// s_load batch.  A wave waits (vmcnt) for its own loads and the barrier publishes all of
+// them; after the last barrier the phases run without synchronisation.
+//
+// Skew.  The two waves of a SIMD (w and w + 4) are offset by one epilogue: the leading
+// wave runs MFMA(p) then epilogue(p), the trailing one epilogue(p - 1) then MFMA(p), so one
+// wave's VALU work runs beside the other's matrix instructions.
+//
+// Epilogue.  Accumulators start at the bias; the output is convert, scale, clamp, round
+// (the 1.5*2^23 addition) and one 16-byte store of 16 consecutive channels per lane, the
+// arithmetic of the other int8 kernels.
+
+#include "qconv_device.h"
+
+#include <atomic>
+#include <cstdlib>
+
+namespace miq {
+namespace {
+
+constexpr int kBandWaves = 8;  // two per SIMD: one wave's LDS reads and epilogue overlap the other's MFMAs
+constexpr int kBandMaxKB = 9;  // filter registers per lane: 16 * KB
+constexpr int kBandLds = 160 * 1024;
+// Output stores are non-temporal (nt): the next kernel then does not have to write back
+// this one's output from L2 before its own loads (measured: ~5% per launch).
+constexpr int kStoreAux = 2;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// FastDiv without its divisor (the device only needs the multiplier and the shift).
+struct FastDivM {
+  uint32_t m, s;
+};
+FastDivM fastdiv_m(uint32_t d) {
+  const FastDiv f = make_fastdiv(d);
+  return FastDivM{f.m, f.s};
+}
+__device__ __forceinline__ int fdiv(int n, const FastDivM& f) {
+  const uint32_t un = static_cast<uint32_t>(n);
+  return static_cast<int>((__umulhi(un, f.m) + un) >> f.s);
+}
+
+struct BandArgs {
+  const int8_t* x;
+  const int8_t* w;
+  const int32_t* bias;
+  const float* wscale;
+  void* y;
+  int H, W, C, K, Ho, Wo;
+  int ph, pw, sh;
+  int Cg, Kg, Kdim;
+  int BH;             // output rows per band
+  int bands_per_img;  // ceil(Ho / BH)
+  int nbands;         // N * bands_per_img
+  int kt_per_group;   // 64-channel tiles per group
+  int nblocks;        // workgroups of the launch (gridDim would be one more kernarg round trip)
+  int NQ, NPB;        // chunk quads (Cg / 64) and 16-column blocks per input row
+  int SEGR, RPAR;     // segment columns per output row, row phases per wave
+  int nphase;         // ceil(BH / RPAR)
+  int ni;             // input load instructions per workgroup = HR * NQ * NPB
+  int filt_lds, ep_lds, halo_lds;  // LDS byte offsets
+  float act_scale;
+  int relu;
+  // per K-block: LDS slot offset of its (filter row, chunk quad) << 8 | halo column shift
+  // (filter column * dilation, < 256); the struct stays within 64 words, one s_load batch
+  int tap[kBandMaxKB];
+  FastDivM fd_nbands, fd_bpi, fd_ktpg, fd_rowi, fd_npb;
+};
+
+static_assert(sizeof(BandArgs) <= 256, "kernel arguments fit one s_load batch");
+
+__device__ __forceinline__ int xcd_tile(int bid, int total) {
+  const int q = total >> 3;
+  const int r = total & 7;
+  const int xcd = bid & 7;
+  const int pos = bid >> 3;
+  return xcd * q + min(xcd, r) + pos;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n; counts above 15 wait for 15 (waiting for more
+// completions than needed is always correct).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n <= 0 ? 0 : (n >= 15 ? 15 : n)) {
+    case 0: __builtin_amdgcn_s_waitcnt(0xF70 | 0); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0xF70 | 1); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0xF70 | 2); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0xF70 | 3); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0xF70 | 4); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0xF70 | 5); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0xF70 | 6); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0xF70 | 7); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0xF70 | 8); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0xF70 | 9); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0xF70 | 10); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0xF70 | 11); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0xF70 | 12); break;
+    case 13: __builtin_amdgcn_s_waitcnt(0xF70 | 13); break;
+    case 14: __builtin_amdgcn_s_waitcnt(0xF70 | 14); break;
+    default: __builtin_amdgcn_s_waitcnt(0xF70 | 15); break;
+  }
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which would wait for this
+// wave's pending stores); the clobber keeps LDS accesses on their side of it.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), num_records, 0x00020000);
+}
+
+// 16 bytes per lane, global -> LDS at lds + 16 * lane; out-of-range lanes write zeros.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, v4i* lds, unsigned voff, unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
+}
+
+// 16 bytes from LDS byte address `addr`.
+__device__ __forceinline__ v4i lds_read16(unsigned addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(static_cast<uintptr_t>(addr));
+}
+
+// int8 output of one lane: channels kc0 .. kc0 + 15 of one pixel, accumulators biased.
+__device__ __forceinline__ v4i pack_i8(const v4i (&acc)[4], const v4f (&mult)[4], float lo) {
+  v4i pk;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    unsigned u[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = static_cast<float>(acc[j][r]) * mult[j][r];
+      u[r] = __float_as_uint(__builtin_amdgcn_fmed3f(v, lo, 127.0f) + 12582912.0f);
+    }
+    pk[j] = static_cast<int>(__builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u) |
+                             __builtin_amdgcn_perm(u[3], u[2], 0x04000c0cu));
+  }
+  return pk;
+}
+
+// 16 consecutive channels of one pixel as int32 accumulators or dequantized fp32.
+template <int EPI>
+__device__ __forceinline__ void store_wide(void* y, size_t obase, const v4i (&acc)[4], const v4f (&mult)[4], int relu) {
+  if constexpr (EPI == kEpiAcc32) {
+    int32_t* yp = static_cast<int32_t*>(y) + obase;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) reinterpret_cast<v4i*>(yp)[j] = acc[j];
+  } else {
+    float* yp = static_cast<float*>(y) + obase;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v4f f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = static_cast<float>(acc[j][r]) * mult[j][r];
+        if (relu) v = (v > 0.0f) ? v : 0.0f;  // NaN and -0 -> +0
+        f[r] = v;
+      }
+      reinterpret_cast<v4f*>(yp)[j] = f;
+    }
+  }
+}
+
+template <int KB, int EPI>
+__global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_in) {
+  const BandArgs a = preload_args(a_in);
+  extern __shared__ v4i smem[];
+  v4i* filt = smem + a.filt_lds / 16;
+  v4i* halo = smem + a.halo_lds / 16;
+  v4i* ep = smem + a.ep_lds / 16;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row_l = lane & 15;
+  const int grp_l = lane >> 4;
+
+  const int lin = xcd_tile(blockIdx.x, a.nblocks);
+  const int ctile = fdiv(lin, a.fd_nbands);
+  const int band = lin - ctile * a.nbands;
+  const int n = fdiv(band, a.fd_bpi);
+  const int bi = band - n * a.bands_per_img;
+  const int gi = fdiv(ctile, a.fd_ktpg);
+  const int k0 = (ctile - gi * a.kt_per_group) * 64;
+  const int ho0 = bi * a.BH;
+  const int row_instr = a.NQ * a.NPB;  // input load instructions per input row
+
+  // Scalar work is shared by the waves of a SIMD (one instruction per wave per issue
+  // turn), so the loads below use one buffer resource each and keep per-load work to a
+  // few instructions.
+  //
+  // ---- filter -> LDS.  Fragment f = 4b + j (K-block b, MFMA row block j) goes to wave
+  // f % 8.  Its lane (row_l, grp_l) holds channel k0 + 16*(row_l/4) + 4j + row_l%4, bytes
+  // [16*(4b + grp_l), +16) of that channel's KRSC row; channels at or beyond Kg lie past
+  // num_records (zeros).
+  {
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + static_cast<size_t>(gi) * a.Kg * a.Kdim, a.Kg * a.Kdim);
+    const unsigned lane_row = static_cast<unsigned>((16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
+    for (int f = wave; f < 4 * KB; f += kBandWaves) {
+      load_lds16(rw, filt + f * 64, lane_row, static_cast<unsigned>((k0 + 4 * (f & 3)) * a.Kdim + 64 * (f >> 2)));
+    }
+  }
+  // ---- bias and per-channel scales of the tile's 64 channels ----
+  if (EPI != kEpiAcc32 && wave == 0) {
+    const int valid = max(0, a.Kg - k0) * 4;
+    const size_t off = static_cast<size_t>(gi) * a.Kg + min(k0, a.Kg);
+    load_lds16(make_rsrc(a.bias ? a.bias + off : nullptr, a.bias ? valid : 0), ep, 16u * lane, 0);
+    load_lds16(make_rsrc(a.wscale + off, valid), ep + 64, 16u * lane, 0);
+  }
+  // ---- every input row of the band, in row order: instruction i = (row * NQ + quad) *
+  // NPB + block goes to wave i % 8; its lane l reads column 16 * block + l % 16 - pw, chunk
+  // 4 * quad + l / 16.  One resource covers the image (group gi's channels onward); the row
+  // goes into soffset.  A column outside the image gets voffset 2^30 and a row outside it
+  // soffset 2^30: either way past num_records (< 2^30), and their sum cannot wrap.
+  int my_loads = 0;
+  {
+    const int hi0 = ho0 * a.sh - a.ph;
+    const size_t img = static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + img, a.H * a.W * a.C - gi * a.Cg);
+    const int col_lane = row_l - a.pw;
+    for (int i = wave; i < a.ni; i += kBandWaves) {
+      const int hr = fdiv(i, a.fd_rowi);
+      const int rem = i - hr * row_instr;
+      const int q = fdiv(rem, a.fd_npb);
+      const int pb = rem - q * a.NPB;
+      const int hi = hi0 + hr;
+      const unsigned soff =
+          static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) ? static_cast<unsigned>(hi * a.W * a.C + 64 * q) : 0x40000000u;
+      const int col = col_lane + 16 * pb;
+      const unsigned voff =
+          static_cast<unsigned>(col) < static_cast<unsigned>(a.W) ? static_cast<unsigned>(col * a.C + 16 * grp_l) : 0x40000000u;
+      load_lds16(rx, halo + i * 64, voff, soff);
+      ++my_loads;
+    }
+  }
+  // filter and epilogue parameters (issued before any input row) complete; the barrier
+  // publishes every wave's part
+  wait_vmcnt(my_loads);
+  barrier_only();
+
+  v4i A[KB][4];
+#pragma unroll
+  for (int b = 0; b < KB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) A[b][j] = filt[(b * 4 + j) * 64 + lane];
+  // epilogue parameters of this lane's 16 channels kc0 + 4j + r (zero past Kg)
+  const int kc0 = k0 + 16 * grp_l;
+  const bool ch_ok = kc0 < a.Kg;  // Kg % 16 == 0: a lane's 16 channels all exist or none does
+  v4i bias_v[4];
+  v4f mult_v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bias_v[j] = v4i{0, 0, 0, 0};
+    mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (EPI != kEpiAcc32) {
+      bias_v[j] = ep[4 * grp_l + j];
+      const v4i ws = ep[64 + 4 * grp_l + j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mult_v[j][r] = requant_multiplier(a.act_scale, __int_as_float(ws[r]));
+    }
+  }
+
+  const bool wave_on = wave < a.SEGR * a.RPAR;
+  const int sc = wave_on ? wave % a.SEGR : 0;
+  const int rp = wave_on ? wave / a.SEGR : 0;
+  const int wo = 16 * sc + row_l;
+  // LDS byte address of this lane's fragment of K-block b in the band's first output row:
+  // column x = wo + shift lies in block x / 16 at position x % 16, i.e. slot
+  // 64 * (x / 16) + x % 16 = x + 48 * (x / 16); plus its chunk and the K-block's row and
+  // quad.  A phase adds one uniform row offset.
+  const unsigned halo_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(halo) & 0xffffffffu);
+  unsigned baddr[KB];
+#pragma unroll
+  for (int b = 0; b < KB; ++b) {
+    const int x = row_l + (a.tap[b] & 0xff);
+    baddr[b] = halo_addr + 16u * static_cast<unsigned>((a.tap[b] >> 8) + 64 * sc + 16 * grp_l + x + 48 * (x >> 4));
+  }
+  const unsigned row_bytes = 16u * static_cast<unsigned>(a.sh * row_instr * 64);  // per output row
+  const float lo = a.relu ? 0.0f : -128.0f;
+
+  // Output through a buffer resource over the band's rows (of image n, group gi): the lane
+  // part of the offset is fixed, the row part goes into soffset.  A lane whose pixel or
+  // channels do not exist, or a row past the band, gets 2^30 and its store is dropped.
+  constexpr int kOutBytes = EPI == kEpiI8 ? 1 : 4;
+  const int band_rows = min(a.BH, a.Ho - ho0);
+  const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + static_cast<size_t>(gi) * a.Kg;
+  const __amdgpu_buffer_rsrc_t ry =
+      make_rsrc(static_cast<char*>(a.y) + out0 * kOutBytes, band_rows * a.Wo * a.K * kOutBytes);
+  const unsigned lane_out =
+      (wave_on && wo < a.Wo && ch_ok) ? static_cast<unsigned>((wo * a.K + kc0) * kOutBytes) : 0x40000000u;
+  auto row_off = [&](int q) {
+    const int t = q * a.RPAR + rp;
+    return t < band_rows ? static_cast<unsigned>(t * a.Wo * a.K * kOutBytes) : 0x40000000u;
+  };
+  auto emit = [&](const v4i (&acc)[4], int q) {
+    const unsigned soff = row_off(q);
+    if constexpr (EPI == kEpiI8) {
+      __builtin_amdgcn_raw_buffer_store_b128(pack_i8(acc, mult_v, lo), ry, lane_out, soff, kStoreAux);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v4i v = acc[j];
+        if constexpr (EPI == kEpiF32) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float f = static_cast<float>(acc[j][r]) * mult_v[j][r];
+            if (a.relu) f = (f > 0.0f) ? f : 0.0f;  // NaN and -0 -> +0
+            v[r] = __float_as_int(f);
+          }
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, lane_out + 16 * j, soff, kStoreAux);
+      }
+    }
+  };
+  auto mfma_phase = [&](int p, v4i (&acc)[4]) {
+    // rows past the band reuse its last row (their results are dropped)
+    const unsigned rb = static_cast<unsigned>(min(p * a.RPAR + rp, a.BH - 1)) * row_bytes;
+    // input fragments are read RS K-blocks ahead: each read goes out right after the
+    // MFMAs that free its register
+    constexpr int RS = KB < 4 ? KB : 4;
+    v4i B[RS];
+#pragma unroll
+    for (int r = 0; r < RS; ++r) B[r] = lds_read16(baddr[r] + rb);
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][j], B[b % RS], b == 0 ? bias_v[j] : acc[j], 0, 0, 0);
+      }
+      if (b + RS < KB) B[b % RS] = lds_read16(baddr[b + RS] + rb);
+      __builtin_amdgcn_sched_barrier(0);  // keeps each read RS K-blocks ahead of its use
+    }
+  };
+
+  // every input row is in LDS
+  wait_vmcnt(0);
+  barrier_only();
+  // The two waves of a SIMD (waves w and w + 4) are skewed by one epilogue: the "leading"
+  // wave w < 4 runs MFMA(p) then the epilogue of p; the trailing one runs the epilogue of
+  // p - 1 then MFMA(p), so one wave's VALU work runs beside the other's matrix instructions.
+  v4i acc[4];
+  if (wave < kBandWaves / 2) {
+    for (int p = 0; p < a.nphase; ++p) {
+      mfma_phase(p, acc);
+      emit(acc, p);
+    }
+  } else {
+    for (int p = 0; p < a.nphase; ++p) {
+      v4i prev[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) prev[j] = acc[j];
+      if (p > 0) emit(prev, p - 1);
+      mfma_phase(p, acc);
+    }
+    if (a.nphase > 0) emit(acc, a.nphase - 1);
+  }
+}
+
+struct BandPlan {
+  int KB, NQ, NPB, SEGR, RPAR, BH, bands_per_img, kt_per_group, HR, ni, nphase;
+  int filt_lds, ep_lds, halo_lds;
+  size_t lds_bytes;
+};
+
+int band_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+bool band_plan(const Geom& g, Epi epi, BandPlan* p, std::string* why) {
+  auto no = [&](const char* m) { if (why) *why = m; return false; };
+  if (g.Cg % 64 != 0 || g.Cg == 0) return no("band kernel needs (c/groups) % 64 == 0");
+  if (g.Kg <= 0 || g.Kg % 16 != 0) return no("band kernel needs (k/groups) % 16 == 0");
+  if (g.sw != 1) return no("band kernel needs stride_w == 1");
+  if (g.sh < 1 || g.dh < 1 || g.dw < 1 || g.ph < 0 || g.pw < 0) return no("band kernel needs positive stride/dilation");
+  if (g.Wo > 64) return no("band kernel needs output width <= 64");
+  if (g.R < 1 || g.S < 1) return no("band kernel needs a non-empty filter");
+  const long long kb = static_cast<long long>(g.R) * g.S * (g.Cg / 64);
+  if (kb > kBandMaxKB) return no("band kernel filter does not fit in registers (R*S*c/groups > 576)");
+  if (static_cast<long long>(g.H) * g.W * g.C >= (1LL << 30)) return no("band kernel needs images below 2^30 bytes");
+  if (static_cast<long long>(g.Kg) * g.R * g.S * g.Cg >= (1LL << 30)) return no("band kernel needs group filters below 2^30 bytes");
+  if (static_cast<long long>(g.Ho) * g.Wo * g.K * 4 >= (1LL << 30)) return no("band kernel needs images below 2^30 output bytes");
+  const long long hcols = static_cast<long long>(g.Wo) + static_cast<long long>(g.S - 1) * g.dw;
+  if (hcols > 128) return no("band kernel needs output width + dilated filter width <= 128");
+  p->KB = static_cast<int>(kb);
+  p->NQ = g.Cg / 64;
+  p->NPB = static_cast<int>((hcols + 15) / 16);
+  p->SEGR = (g.Wo + 15) / 16;
+  p->RPAR = p->SEGR > kBandWaves / 2 ? 1 : kBandWaves / p->SEGR;
+  p->kt_per_group = (g.Kg + 63) / 64;
+  const int cus = band_cu_count();
+  const size_t filt_bytes = static_cast<size_t>(p->KB) * 4 * 1024;
+  bool found = false;
+  double best = 0.0;
+  for (int bh = 1; bh <= g.Ho; ++bh) {
+    const long long hr = static_cast<long long>(bh - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
+    const long long ni = hr * p->NQ * p->NPB;
+    if (ni > kBandWaves * 15) break;  // at most 15 input loads per wave (exact vmcnt waits)
+    const int nphase = (bh + p->RPAR - 1) / p->RPAR;
+    const size_t lds = filt_bytes + 2048 + static_cast<size_t>(ni + 1) * 1024;
+    if (lds > static_cast<size_t>(kBandLds)) break;
+    const long long bands = (g.Ho + bh - 1) / bh;
+    const long long wgs = static_cast<long long>(g.N) * bands * g.G * p->kt_per_group;
+    const long long rounds = (wgs + cus - 1) / cus;
+    // phases of work per round plus a fixed cost for the filter and the first input rows
+    const double cost = static_cast<double>(rounds) * (nphase + 2.5);
+    if (!found || cost < best - 1e-9) {
+      found = true;
+      best = cost;
+      p->BH = bh;
+      p->bands_per_img = static_cast<int>(bands);
+      p->HR = static_cast<int>(hr);
+      p->ni = static_cast<int>(ni);
+      p->nphase = nphase;
+      p->filt_lds = 0;
+      p->ep_lds = static_cast<int>(filt_bytes);
+      p->halo_lds = static_cast<int>(filt_bytes + 2048);
+      p->lds_bytes = lds;
+    }
+  }
+  if (!found) return no("band kernel input rows do not fit in LDS");
+  const long long blocks = static_cast<long long>(g.N) * p->bands_per_img * g.G * p->kt_per_group;
+  if (blocks > 0x7fffffffLL) return no("grid too large");
+  return true;
+}
+
+template <int KB>
+void band_launch_kb(const BandArgs& a, const BandPlan& pl, Epi epi, unsigned nblocks, hipStream_t stream) {
+  const dim3 grid(nblocks);
+  switch (epi) {
+    case kEpiI8: {
+      auto kern = i8_band_kernel<KB, kEpiI8>;
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(pl.lds_bytes));
+      hipLaunchKernelGGL(kern, grid, dim3(64 * kBandWaves), pl.lds_bytes, stream, a);
+      break;
+    }
+    case kEpiAcc32: {
+      auto kern = i8_band_kernel<KB, kEpiAcc32>;
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(pl.lds_bytes));
+      hipLaunchKernelGGL(kern, grid, dim3(64 * kBandWaves), pl.lds_bytes, stream, a);
+      break;
+    }
+    default: {
+      auto kern = i8_band_kernel<KB, kEpiF32>;
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(pl.lds_bytes));
+      hipLaunchKernelGGL(kern, grid, dim3(64 * kBandWaves), pl.lds_bytes, stream, a);
+      break;
+    }
+  }
+}
+
+template <int KB>
+void band_dispatch(int kb, const BandArgs& a, const BandPlan& pl, Epi epi, unsigned nblocks, hipStream_t stream) {
+  if constexpr (KB >= 1) {
+    if (kb == KB) {
+      band_launch_kb<KB>(a, pl, epi, nblocks, stream);
+    } else {
+      band_dispatch<KB - 1>(kb, a, pl, epi, nblocks, stream);
+    }
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+bool band_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                   std::string* why) {
+  const bool params_ok = epi == kEpiAcc32 || ((rq.bias == nullptr || aligned16(rq.bias)) && aligned16(rq.wscale));
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) || !params_ok) {
+    if (why) *why = "band kernel needs 16-byte aligned tensors, bias and scales";
+    return false;
+  }
+  BandPlan pl;
+  return band_plan(g, epi, &pl, why);
+}
+
+hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                          hipStream_t stream) {
+  if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
+  BandPlan pl;
+  if (!band_plan(g, epi, &pl, nullptr)) return hipErrorInvalidConfiguration;
+  BandArgs a;
+  a.x = x; a.w = w; a.bias = rq.bias; a.wscale = rq.wscale; a.y = y;
+  a.H = g.H; a.W = g.W; a.C = g.C; a.K = g.K; a.Ho = g.Ho; a.Wo = g.Wo;
+  a.ph = g.ph; a.pw = g.pw; a.sh = g.sh;
+  a.Cg = g.Cg; a.Kg = g.Kg; a.Kdim = g.R * g.S * g.Cg;
+  a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.nbands = g.N * pl.bands_per_img;
+  a.kt_per_group = pl.kt_per_group; a.NQ = pl.NQ; a.NPB = pl.NPB; a.SEGR = pl.SEGR; a.RPAR = pl.RPAR;
+  a.nphase = pl.nphase; a.ni = pl.ni;
+  a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.halo_lds = pl.halo_lds;
+  a.act_scale = rq.act_scale; a.relu = rq.relu;
+  // K-block b = chunks 4b .. 4b+3 of the flattened (tap, 16-channel chunk) order, all of
+  // one tap because Cg16 % 4 == 0.
+  const int cg16 = g.Cg / 16;
+  for (int b = 0; b < kBandMaxKB; ++b) {
+    if (b < pl.KB) {
+      const int q0 = 4 * b;
+      const int tap = q0 / cg16;
+      const int cb = q0 % cg16;
+      const int r = tap / g.S;
+      const int s = tap % g.S;
+      a.tap[b] = ((r * g.dh * pl.NQ + cb / 4) * pl.NPB * 64) << 8 | (s * g.dw);
+    } else {
+      a.tap[b] = 0;
+    }
+  }
+  a.fd_nbands = fastdiv_m(a.nbands);
+  a.fd_bpi = fastdiv_m(pl.bands_per_img);
+  a.fd_ktpg = fastdiv_m(pl.kt_per_group);
+  a.fd_rowi = fastdiv_m(pl.NQ * pl.NPB);
+  a.fd_npb = fastdiv_m(pl.NPB);
+  const long long nblocks = static_cast<long long>(a.nbands) * g.G * pl.kt_per_group;
+  a.nblocks = static_cast<int>(nblocks);
+  band_dispatch<kBandMaxKB>(pl.KB, a, pl, epi, static_cast<unsigned>(nblocks), stream);
+  return hipGetLastError();
+}
+
+}  // namespace miq

@@ -98,15 +98,17 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
 }
 
 // Validates an int8 problem and resolves the kernel family.
-int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y, miq::Epi epi, miq::Geom* g,
-            int32_t* algo) {
+int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y, const miq::Requant& rq,
+            miq::Epi epi, miq::Geom* g, int32_t* algo) {
   if (d == nullptr) return fail(MIQ_ERR_NULL_POINTER, "descriptor pointer is NULL");
   int st = infer_geom(d->n, d->h, d->w, d->c, d->r, d->s, d->k, &d->conv, g);
   if (st != MIQ_OK) return st;
   std::string why;
   switch (d->algo) {
     case MIQ_ALGO_AUTO:
-      if (miq::igemm_eligible(*g, x, w, y, epi, nullptr)) {
+      if (miq::band_eligible(*g, x, w, y, rq, epi, nullptr)) {
+        *algo = MIQ_ALGO_BAND;
+      } else if (miq::igemm_eligible(*g, x, w, y, epi, nullptr)) {
         *algo = MIQ_ALGO_IGEMM;
       } else if (miq::stem_eligible(*g, x, w, y, epi, nullptr)) {
         *algo = MIQ_ALGO_STEM;
@@ -125,6 +127,10 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
       if (!miq::stem_eligible(*g, x, w, y, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       *algo = MIQ_ALGO_STEM;
       break;
+    case MIQ_ALGO_BAND:
+      if (!miq::band_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_BAND;
+      break;
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
   }
@@ -135,11 +141,11 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
              const float* w_scale, void* y, void* stream) {
   miq::Geom g;
   int32_t algo = 0;
-  int st = plan_i8(d, x, w, y, epi, &g, &algo);
+  miq::Requant rq{bias, w_scale, 1.0f, d != nullptr && d->relu != 0 ? 1 : 0};
+  int st = plan_i8(d, x, w, y, rq, epi, &g, &algo);
   if (st != MIQ_OK) return st;
   st = check_tensors(g, filt_elems(g), x, w, y);
   if (st != MIQ_OK) return st;
-  miq::Requant rq{bias, w_scale, 1.0f, d->relu != 0 ? 1 : 0};
   if (epi != miq::kEpiAcc32) {
     if (g.K > 0 && w_scale == nullptr) return fail(MIQ_ERR_NULL_POINTER, "per-channel scale pointer is NULL");
     if (!std::isfinite(d->in_scale) || !std::isfinite(d->out_scale) || d->out_scale == 0.0f) {
@@ -153,6 +159,7 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
   switch (algo) {
     case MIQ_ALGO_IGEMM: e = miq::launch_i8_igemm(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_STEM: e = miq::launch_i8_stem(g, epi, x, w, y, rq, s); break;
+    case MIQ_ALGO_BAND: e = miq::launch_i8_band(g, epi, x, w, y, rq, s); break;
     default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");
@@ -211,7 +218,9 @@ int miq_qconv2d_plan(const miq_qconv_desc* d, int32_t* algo) {
   miq::Geom g;
   // Alignment is judged for 256-byte aligned allocations (what hipMalloc returns).
   static const char kAligned[16] __attribute__((aligned(256))) = {0};
-  return plan_i8(d, kAligned, kAligned, kAligned, miq::kEpiI8, &g, algo);
+  const miq::Requant rq{reinterpret_cast<const int32_t*>(kAligned), reinterpret_cast<const float*>(kAligned), 1.0f,
+                        d != nullptr && d->relu != 0 ? 1 : 0};
+  return plan_i8(d, kAligned, kAligned, kAligned, rq, miq::kEpiI8, &g, algo);
 }
 
 int miq_fprop_nhwc_qi32_u8(const float* x, const float* w, int32_t* y, int32_t n, int32_t h, int32_t wdt, int32_t c,

@@ -9,6 +9,25 @@ namespace miq {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Returns a copy of a kernel-argument struct with every 32-bit word already in an SGPR.
+// The compiler otherwise fetches kernel arguments lazily, one s_load batch (and one full
+// memory round trip) per first use, and a kernel whose addressing needs many fields pays
+// several such round trips before its first global load is issued.  Consuming every word
+// in an empty asm statement makes all of them load in one batch at kernel entry.
+template <typename T>
+__device__ __forceinline__ T preload_args(const T& in) {
+  static_assert(sizeof(T) % 4 == 0, "kernel argument structs are made of 32-bit words");
+  constexpr int kWords = static_cast<int>(sizeof(T) / 4);
+  union {
+    T t;
+    int w[kWords];
+  } u;
+  u.t = in;
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) asm volatile("" : "+s"(u.w[i]));
+  return u.t;
+}
+
 // 16 bytes from an arbitrary byte offset of an LDS buffer, built from five aligned dword
 // reads and byte-funnel shifts (v_alignbyte_b32).  Reads bytes [o & ~3, (o & ~3) + 20).
 __device__ __forceinline__ v4i lds_load16_unaligned(const unsigned char* base, int o) {

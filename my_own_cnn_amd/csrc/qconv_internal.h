@@ -76,6 +76,13 @@ bool igemm_eligible(const Geom& g, const void* x, const void* w, const void* y, 
 hipError_t launch_i8_igemm(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                            hipStream_t stream);
 
+// int8 MFMA row-band kernel, filter in registers: (C/groups) % 64 == 0, (K/groups) % 16 == 0,
+// stride_w == 1, Wo <= 64, R*S*C/groups <= 576.
+bool band_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                   std::string* why);
+hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                          hipStream_t stream);
+
 // int8 MFMA thin-channel kernel for stems: groups == 1, C < 16.
 bool stem_eligible(const Geom& g, const void* x, const void* w, const void* y, Epi epi, std::string* why);
 hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,

@@ -168,7 +168,7 @@ def test_python_mirror_errors():
         M.launch_fprop_nhwc_qi32(M.DataType.LinQuantI8, 1, 1, 1, 1, 5, 5, 4, 3, 3, 4, None, 1, 1)
 
 
-@pytest.mark.parametrize("name,algo", [("tiny", "igemm"), ("r50_3x3", "igemm"), ("r50_1x1", "igemm"),
+@pytest.mark.parametrize("name,algo", [("tiny", "igemm"), ("r50_3x3", "band"), ("r50_1x1", "band"),
                                        ("down_s2", "igemm"), ("stem", "stem")])
 def test_plan_of_the_workloads(name, algo):
     wl = M.WORKLOADS[name]

@@ -69,7 +69,7 @@ def algos_for(x, w, conv):
     n, h, wd, c = x.shape
     k, r, s, _ = w.shape
     out = ["auto", "direct"]
-    for a in ("igemm", "stem"):
+    for a in ("igemm", "stem", "band"):
         d = M.make_desc(x.shape, w.shape, stride=conv[2:4], padding=conv[0:2], dilation=conv[4:6], groups=conv[6],
                         algo=a)
         try:
@@ -93,7 +93,7 @@ def test_int8_accumulators_every_algo(device):
             torch.cuda.synchronize()
             np.testing.assert_array_equal(y.cpu().numpy(), c["y"], err_msg=f"{name} {algo}")
             ran.add(algo)
-    assert ran == {"auto", "direct", "igemm", "stem"}
+    assert ran == {"auto", "direct", "igemm", "stem", "band"}
 
 
 def requant_inputs(k, seed):
