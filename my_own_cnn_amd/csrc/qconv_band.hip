@@ -42,6 +42,7 @@
 
 #include "qconv_device.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 
@@ -88,6 +89,7 @@ struct BandArgs {
   int SEGR, RPAR;     // segment columns per output row, row phases per wave
   int nphase;         // ceil(BH / RPAR)
   int ni;             // input load instructions per workgroup = HR * NQ * NPB
+  int ni0;            // those of the input rows phase 0 reads
   int filt_lds, ep_lds, halo_lds;  // LDS byte offsets
   float act_scale;
   int relu;
@@ -358,27 +360,43 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
     }
   };
 
-  // every input row is in LDS
-  wait_vmcnt(0);
-  barrier_only();
+  // Phase 0 starts as soon as its own input rows are in: a wave waits for its loads among
+  // the first ni0 (exact: no store is pending yet).  The wait for the rest comes after the
+  // phase-0 MFMAs and before the first store, so it is exact too, and after its barrier
+  // nothing synchronises any more.
+  {
+    const int mine0 = a.ni0 > wave ? (a.ni0 - wave + kBandWaves - 1) / kBandWaves : 0;
+    wait_vmcnt(my_loads - mine0);
+    barrier_only();
+  }
+  auto wait_rest = [&]() {
+    wait_vmcnt(0);
+    barrier_only();
+  };
   // The two waves of a SIMD (waves w and w + 4) are skewed by one epilogue: the "leading"
   // wave w < 4 runs MFMA(p) then the epilogue of p; the trailing one runs the epilogue of
   // p - 1 then MFMA(p), so one wave's VALU work runs beside the other's matrix instructions.
+  // Phases whose row lies past the band (or past the image) are skipped, wave-uniformly.
+  const int nph = wave_on ? min(a.nphase, (band_rows - rp + a.RPAR - 1) / a.RPAR) : 0;
   v4i acc[4];
   if (wave < kBandWaves / 2) {
-    for (int p = 0; p < a.nphase; ++p) {
+    for (int p = 0; p < nph; ++p) {
       mfma_phase(p, acc);
+      if (p == 0) wait_rest();
       emit(acc, p);
     }
+    if (nph == 0) wait_rest();
   } else {
-    for (int p = 0; p < a.nphase; ++p) {
+    for (int p = 0; p < nph; ++p) {
       v4i prev[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) prev[j] = acc[j];
+      if (p == 1) wait_rest();
       if (p > 0) emit(prev, p - 1);
       mfma_phase(p, acc);
     }
-    if (a.nphase > 0) emit(acc, a.nphase - 1);
+    if (nph <= 1) wait_rest();
+    if (nph > 0) emit(acc, nph - 1);
   }
 }
 
@@ -524,6 +542,11 @@ hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t*
   a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.nbands = g.N * pl.bands_per_img;
   a.kt_per_group = pl.kt_per_group; a.NQ = pl.NQ; a.NPB = pl.NPB; a.SEGR = pl.SEGR; a.RPAR = pl.RPAR;
   a.nphase = pl.nphase; a.ni = pl.ni;
+  {
+    const long long rows0 = std::min<long long>(pl.HR, static_cast<long long>(pl.RPAR - 1) * g.sh +
+                                                           static_cast<long long>(g.R - 1) * g.dh + 1);
+    a.ni0 = static_cast<int>(rows0) * pl.NQ * pl.NPB;
+  }
   a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.halo_lds = pl.halo_lds;
   a.act_scale = rq.act_scale; a.relu = rq.relu;
   // K-block b = chunks 4b .. 4b+3 of the flattened (tap, 16-channel chunk) order, all of
