@@ -52,24 +52,6 @@ namespace {
 constexpr int kBandWaves = 8;  // two per SIMD: one wave's LDS reads and epilogue overlap the other's MFMAs
 constexpr int kBandMaxKB = 9;  // filter registers per lane: 16 * KB
 constexpr int kBandLds = 160 * 1024;
-// Output stores are non-temporal (nt): the next kernel then does not have to write back
-// this one's output from L2 before its own loads (measured: ~5% per launch).
-constexpr int kStoreAux = 2;
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// FastDiv without its divisor (the device only needs the multiplier and the shift).
-struct FastDivM {
-  uint32_t m, s;
-};
-FastDivM fastdiv_m(uint32_t d) {
-  const FastDiv f = make_fastdiv(d);
-  return FastDivM{f.m, f.s};
-}
-__device__ __forceinline__ int fdiv(int n, const FastDivM& f) {
-  const uint32_t un = static_cast<uint32_t>(n);
-  return static_cast<int>((__umulhi(un, f.m) + un) >> f.s);
-}
 
 struct BandArgs {
   const int8_t* x;
@@ -100,95 +82,6 @@ struct BandArgs {
 };
 
 static_assert(sizeof(BandArgs) <= 256, "kernel arguments fit one s_load batch");
-
-__device__ __forceinline__ int xcd_tile(int bid, int total) {
-  const int q = total >> 3;
-  const int r = total & 7;
-  const int xcd = bid & 7;
-  const int pos = bid >> 3;
-  return xcd * q + min(xcd, r) + pos;
-}
-
-// s_waitcnt vmcnt(n) for a wave-uniform n; counts above 15 wait for 15 (waiting for more
-// completions than needed is always correct).
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  switch (n <= 0 ? 0 : (n >= 15 ? 15 : n)) {
-    case 0: __builtin_amdgcn_s_waitcnt(0xF70 | 0); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0xF70 | 1); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0xF70 | 2); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0xF70 | 3); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0xF70 | 4); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0xF70 | 5); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0xF70 | 6); break;
-    case 7: __builtin_amdgcn_s_waitcnt(0xF70 | 7); break;
-    case 8: __builtin_amdgcn_s_waitcnt(0xF70 | 8); break;
-    case 9: __builtin_amdgcn_s_waitcnt(0xF70 | 9); break;
-    case 10: __builtin_amdgcn_s_waitcnt(0xF70 | 10); break;
-    case 11: __builtin_amdgcn_s_waitcnt(0xF70 | 11); break;
-    case 12: __builtin_amdgcn_s_waitcnt(0xF70 | 12); break;
-    case 13: __builtin_amdgcn_s_waitcnt(0xF70 | 13); break;
-    case 14: __builtin_amdgcn_s_waitcnt(0xF70 | 14); break;
-    default: __builtin_amdgcn_s_waitcnt(0xF70 | 15); break;
-  }
-}
-
-// Workgroup barrier without the memory fence of __syncthreads (which would wait for this
-// wave's pending stores); the clobber keeps LDS accesses on their side of it.
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_records) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), num_records, 0x00020000);
-}
-
-// 16 bytes per lane, global -> LDS at lds + 16 * lane; out-of-range lanes write zeros.
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, v4i* lds, unsigned voff, unsigned soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
-}
-
-// 16 bytes from LDS byte address `addr`.
-__device__ __forceinline__ v4i lds_read16(unsigned addr) {
-  return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(static_cast<uintptr_t>(addr));
-}
-
-// int8 output of one lane: channels kc0 .. kc0 + 15 of one pixel, accumulators biased.
-__device__ __forceinline__ v4i pack_i8(const v4i (&acc)[4], const v4f (&mult)[4], float lo) {
-  v4i pk;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    unsigned u[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = static_cast<float>(acc[j][r]) * mult[j][r];
-      u[r] = __float_as_uint(__builtin_amdgcn_fmed3f(v, lo, 127.0f) + 12582912.0f);
-    }
-    pk[j] = static_cast<int>(__builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u) |
-                             __builtin_amdgcn_perm(u[3], u[2], 0x04000c0cu));
-  }
-  return pk;
-}
-
-// 16 consecutive channels of one pixel as int32 accumulators or dequantized fp32.
-template <int EPI>
-__device__ __forceinline__ void store_wide(void* y, size_t obase, const v4i (&acc)[4], const v4f (&mult)[4], int relu) {
-  if constexpr (EPI == kEpiAcc32) {
-    int32_t* yp = static_cast<int32_t*>(y) + obase;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) reinterpret_cast<v4i*>(yp)[j] = acc[j];
-  } else {
-    float* yp = static_cast<float*>(y) + obase;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v4f f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = static_cast<float>(acc[j][r]) * mult[j][r];
-        if (relu) v = (v > 0.0f) ? v : 0.0f;  // NaN and -0 -> +0
-        f[r] = v;
-      }
-      reinterpret_cast<v4f*>(yp)[j] = f;
-    }
-  }
-}
 
 template <int KB, int EPI>
 __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_in) {

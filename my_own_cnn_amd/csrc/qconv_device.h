@@ -9,6 +9,94 @@ namespace miq {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Cache policy of the row-band kernels' output stores: non-temporal (nt), so the next
+// kernel does not have to write this one's output back from L2 before its own loads
+// (measured: ~5% per launch).
+constexpr int kStoreAux = 2;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// FastDiv without its divisor (the device only needs the multiplier and the shift).
+struct FastDivM {
+  uint32_t m, s;
+};
+inline FastDivM fastdiv_m(uint32_t d) {
+  const FastDiv f = make_fastdiv(d);
+  return FastDivM{f.m, f.s};
+}
+__device__ __forceinline__ int fdiv(int n, const FastDivM& f) {
+  const uint32_t un = static_cast<uint32_t>(n);
+  return static_cast<int>((__umulhi(un, f.m) + un) >> f.s);
+}
+
+// Workgroup id -> tile index such that each of the 8 XCDs (workgroups are dealt to them
+// round-robin) gets one contiguous range of tiles: neighbouring tiles share an L2.
+__device__ __forceinline__ int xcd_tile(int bid, int total) {
+  const int q = total >> 3;
+  const int r = total & 7;
+  const int xcd = bid & 7;
+  const int pos = bid >> 3;
+  return xcd * q + min(xcd, r) + pos;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n; counts above 15 wait for 15 (waiting for more
+// completions than needed is always correct).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n <= 0 ? 0 : (n >= 15 ? 15 : n)) {
+    case 0: __builtin_amdgcn_s_waitcnt(0xF70 | 0); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0xF70 | 1); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0xF70 | 2); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0xF70 | 3); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0xF70 | 4); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0xF70 | 5); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0xF70 | 6); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0xF70 | 7); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0xF70 | 8); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0xF70 | 9); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0xF70 | 10); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0xF70 | 11); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0xF70 | 12); break;
+    case 13: __builtin_amdgcn_s_waitcnt(0xF70 | 13); break;
+    case 14: __builtin_amdgcn_s_waitcnt(0xF70 | 14); break;
+    default: __builtin_amdgcn_s_waitcnt(0xF70 | 15); break;
+  }
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which would wait for this
+// wave's pending stores); the clobber keeps LDS accesses on their side of it.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), num_records, 0x00020000);
+}
+
+// 16 bytes per lane, global -> LDS at lds + 16 * lane; out-of-range lanes write zeros.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, v4i* lds, unsigned voff, unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
+}
+
+// 16 bytes from LDS byte address `addr`.
+__device__ __forceinline__ v4i lds_read16(unsigned addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(static_cast<uintptr_t>(addr));
+}
+
+// int8 output of one lane: channels kc0 .. kc0 + 15 of one pixel, accumulators biased.
+__device__ __forceinline__ v4i pack_i8(const v4i (&acc)[4], const v4f (&mult)[4], float lo) {
+  v4i pk;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    unsigned u[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = static_cast<float>(acc[j][r]) * mult[j][r];
+      u[r] = __float_as_uint(__builtin_amdgcn_fmed3f(v, lo, 127.0f) + 12582912.0f);
+    }
+    pk[j] = static_cast<int>(__builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u) |
+                             __builtin_amdgcn_perm(u[3], u[2], 0x04000c0cu));
+  }
+  return pk;
+}
+
 // Returns a copy of a kernel-argument struct with every 32-bit word already in an SGPR.
 // The compiler otherwise fetches kernel arguments lazily, one s_load batch (and one full
 // memory round trip) per first use, and a kernel whose addressing needs many fields pays

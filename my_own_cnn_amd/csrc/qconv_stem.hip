@@ -15,10 +15,22 @@
 // columns for the padding) into LDS; every lane then assembles its 16-byte operands from
 // arbitrary byte offsets with aligned dword reads and v_alignbyte_b32.  The filter
 // fragments stay in registers for the whole tile.
+//
+// Row-band variant (i8_stem_band_kernel, used when the shape allows it).  A workgroup of
+// 8 waves owns a band of BH output rows of one image and 64 channels, about one band per
+// CU.  Its loads are buffer_load_dwordx4 ... lds (global -> LDS, no registers): the
+// filter slice as contiguous kilobytes, and every input row as P/1024 kilobyte
+// instructions whose lane l carries row bytes [1024m + 16l - PLB, +16).  A lane whose
+// bytes lie left or right of the row, or a row outside the image, gets an offset past
+// num_records and writes zeros, so the padding costs nothing.  Then each wave takes
+// 16-pixel segments of the band in turn: its four K-blocks' operands come from the staged
+// rows at arbitrary byte offsets, and the int8 result of 16 channels per lane leaves in
+// one 16-byte buffer store.
 
 #include "qconv_device.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace miq {
 namespace {
@@ -212,14 +224,296 @@ i8_stem_kernel(StemArgs a) {
   }
 }
 
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// ---------------------------------------------------------------------------------------
+// Row-band variant
+
+constexpr int kSbWaves = 8;
+constexpr int kSbLds = 160 * 1024;
+
+struct StemBandArgs {
+  const int8_t* x;
+  const int8_t* w;
+  const int32_t* bias;
+  const float* wscale;
+  void* y;
+  int H, W, C, K, Ho, Wo;
+  int ph, pw, sh, sw, dh;
+  int SC, RSC, CPR, NQ;  // filter row bytes, filter bytes per channel, chunks per row slot, R * CPR
+  int BH, bands_per_img, nbands, nblocks;
+  int SEGR;              // 16-pixel segments per output row
+  int P, PLB, rows_ld;   // staged row pitch (bytes, multiple of 1024), its left pad, loads per row
+  int HR;                // staged input rows per band
+  int nfilt;             // filter load instructions
+  int filt_lds, ep_lds, halo_lds;  // LDS byte offsets
+  float act_scale;
+  int relu;
+  FastDivM fd_nbands, fd_bpi, fd_segr, fd_rowsld;
+};
+
+static_assert(sizeof(StemBandArgs) <= 256, "kernel arguments fit one s_load batch");
+
+template <int KB, int EPI>
+__global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBandArgs a_in) {
+  const StemBandArgs a = preload_args(a_in);
+  extern __shared__ v4i sb_lds[];
+  const unsigned char* bytes = reinterpret_cast<const unsigned char*>(sb_lds);
+  v4i* filt = sb_lds + a.filt_lds / 16;
+  v4i* halo = sb_lds + a.halo_lds / 16;
+  v4i* ep = sb_lds + a.ep_lds / 16;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row_l = lane & 15;
+  const int grp_l = lane >> 4;
+
+  const int lin = xcd_tile(blockIdx.x, a.nblocks);
+  const int ctile = fdiv(lin, a.fd_nbands);
+  const int band = lin - ctile * a.nbands;
+  const int n = fdiv(band, a.fd_bpi);
+  const int bi = band - n * a.bands_per_img;
+  const int k0 = ctile * 64;
+  const int ho0 = bi * a.BH;
+  const int band_rows = min(a.BH, a.Ho - ho0);
+
+  // ---- loads.  Filter instruction f (lane l: bytes [1024f + 16l, +16) of the tile's
+  // 64 * RSC filter bytes, contiguous in KRSC) and input instruction i = row * rows_ld + m
+  // go to wave f % 8 and i % 8; bias and scales to wave 0.
+  {
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + static_cast<size_t>(k0) * a.RSC, 64 * a.RSC);
+    for (int f = wave; f < a.nfilt; f += kSbWaves) load_lds16(rw, filt + f * 64, 16u * lane, 1024u * f);
+  }
+  if (EPI != kEpiAcc32 && wave == 0) {
+    load_lds16(make_rsrc(a.bias ? a.bias + k0 : nullptr, a.bias ? 256 : 0), ep, 16u * lane, 0);
+    load_lds16(make_rsrc(a.wscale + k0, 256), ep + 64, 16u * lane, 0);
+  }
+  {
+    const int rowb = a.W * a.C;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + static_cast<size_t>(n) * a.H * rowb, a.H * rowb);
+    const int hi0 = ho0 * a.sh - a.ph;
+    const int ni = a.HR * a.rows_ld;
+    for (int i = wave; i < ni; i += kSbWaves) {
+      const int hr = fdiv(i, a.fd_rowsld);
+      const int m = i - hr * a.rows_ld;
+      const int hi = hi0 + hr;
+      const int b = 1024 * m + 16 * lane - a.PLB;  // this lane's first byte in the input row
+      const unsigned soff =
+          static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) ? static_cast<unsigned>(hi * rowb) : 0x40000000u;
+      const unsigned voff = (b >= 0 && b + 16 <= rowb) ? static_cast<unsigned>(b) : 0x40000000u;
+      load_lds16(rx, halo + i * 64, voff, soff);
+    }
+  }
+  wait_vmcnt(0);
+  barrier_only();
+
+  // ---- filter fragments: lane (row_l, grp_l) of fragment (b, j) holds channel
+  // 16*(row_l/4) + 4j + row_l%4 of the tile, chunk q = 4b + grp_l (filter row q / CPR,
+  // bytes 16 * (q % CPR) .. of its SC-byte slot; bytes past SC and chunks past NQ are 0).
+  v4i A[KB][4];
+  const unsigned char* fbytes = bytes + a.filt_lds;
+#pragma unroll
+  for (int b = 0; b < KB; ++b) {
+    const int q = 4 * b + grp_l;
+    const int r = a.CPR == 2 ? (q >> 1) : q;
+    const int h = q - r * a.CPR;
+    const int nvalid = q < a.NQ ? min(16, a.SC - 16 * h) : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kl = 16 * (row_l >> 2) + 4 * j + (row_l & 3);
+      v4i v = lds_load16_unaligned(fbytes, kl * a.RSC + (nvalid > 0 ? r * a.SC + 16 * h : 0));
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int keep = min(4, max(0, nvalid - 4 * d));
+        const unsigned msk = keep >= 4 ? 0xffffffffu : ((1u << (8 * keep)) - 1u);
+        v[d] = static_cast<int>(static_cast<unsigned>(v[d]) & msk);
+      }
+      A[b][j] = v;
+    }
+  }
+  // epilogue parameters of this lane's 16 channels k0 + 16 * grp_l + 4j + r
+  v4i bias_v[4];
+  v4f mult_v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bias_v[j] = v4i{0, 0, 0, 0};
+    mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (EPI != kEpiAcc32) {
+      bias_v[j] = ep[4 * grp_l + j];
+      const v4i ws = ep[64 + 4 * grp_l + j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mult_v[j][r] = requant_multiplier(a.act_scale, __int_as_float(ws[r]));
+    }
+  }
+  // per K-block: byte offset of this lane's chunk within a staged band row window
+  int qoff[KB];
+#pragma unroll
+  for (int b = 0; b < KB; ++b) {
+    const int q = min(4 * b + grp_l, a.NQ - 1);  // chunks past NQ meet zero filter bytes
+    const int r = a.CPR == 2 ? (q >> 1) : q;
+    qoff[b] = r * a.dh * a.P + 16 * (q - r * a.CPR);
+  }
+  const float lo = a.relu ? 0.0f : -128.0f;
+  constexpr int kOutBytes = EPI == kEpiI8 ? 1 : 4;
+  const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + k0;
+  const __amdgpu_buffer_rsrc_t ry =
+      make_rsrc(static_cast<char*>(a.y) + out0 * kOutBytes, band_rows * a.Wo * a.K * kOutBytes);
+  const unsigned char* hbytes = bytes + a.halo_lds;
+
+  const int nseg = band_rows * a.SEGR;
+  for (int sg = wave; sg < nseg; sg += kSbWaves) {
+    const int t = fdiv(sg, a.fd_segr);
+    const int wo = 16 * (sg - t * a.SEGR) + row_l;
+    const bool pix = wo < a.Wo;
+    const int base = t * a.sh * a.P + a.PLB + ((pix ? wo : a.Wo - 1) * a.sw - a.pw) * a.C;
+    v4i acc[4];
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      const v4i B = lds_load16_unaligned(hbytes, base + qoff[b]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][j], B, b == 0 ? bias_v[j] : acc[j], 0, 0, 0);
+    }
+    const unsigned voff = pix ? static_cast<unsigned>(((t * a.Wo + wo) * a.K + 16 * grp_l) * kOutBytes) : 0x40000000u;
+    if constexpr (EPI == kEpiI8) {
+      __builtin_amdgcn_raw_buffer_store_b128(pack_i8(acc, mult_v, lo), ry, voff, 0, kStoreAux);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v4i v = acc[j];
+        if constexpr (EPI == kEpiF32) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float f = static_cast<float>(acc[j][r]) * mult_v[j][r];
+            if (a.relu) f = (f > 0.0f) ? f : 0.0f;  // NaN and -0 -> +0
+            v[r] = __float_as_int(f);
+          }
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, voff + 16 * j, 0, kStoreAux);
+      }
+    }
+  }
+}
+
+struct StemBandPlan {
+  int CPR, NQ, KB, BH, bands_per_img, HR, P, PLB, rows_ld, nfilt;
+  int filt_lds, ep_lds, halo_lds;
+  size_t lds;
+};
+
+int sb_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The band variant needs what the general stem kernel needs plus: whole 16-byte chunks
+// per input row (W*C % 16 == 0, so no load straddles a row end), whole 64-channel tiles
+// (K % 64 == 0: filter slice, bias and scales in whole loads) and its rows in LDS.
+bool make_band_plan(const Geom& g, StemBandPlan* pl) {
+  const int SC = g.S * g.C;
+  pl->CPR = SC <= 16 ? 1 : 2;
+  pl->NQ = g.R * pl->CPR;
+  pl->KB = (pl->NQ + 3) / 4;
+  if (pl->KB > 4 || g.dw != 1) return false;
+  const long long rowb = static_cast<long long>(g.W) * g.C;
+  if (rowb % 16 != 0 || g.K % 64 != 0) return false;
+  if (static_cast<long long>(g.H) * rowb >= (1LL << 30)) return false;
+  if (static_cast<long long>(g.Ho) * g.Wo * g.K * 4 >= (1LL << 30)) return false;
+  pl->PLB = round_up(std::max(0, g.pw) * g.C, 16);
+  // last byte any lane reads in a staged row: window of the last output column, its
+  // row slot and the 4-byte over-read of the unaligned LDS loader
+  const long long last = pl->PLB + (static_cast<long long>(g.Wo - 1) * g.sw - g.pw) * g.C + 16LL * pl->CPR + 4;
+  const long long need = std::max<long long>(pl->PLB + rowb, last);
+  pl->P = static_cast<int>((need + 1023) / 1024 * 1024);
+  pl->rows_ld = pl->P / 1024;
+  const long long RSC = static_cast<long long>(g.R) * SC;
+  pl->nfilt = static_cast<int>((64 * RSC + 20 + 1023) / 1024);  // + the loader's over-read
+  const int segr = (g.Wo + 15) / 16;
+  const int cus = sb_cu_count();
+  // filter, then 2 KB for bias and scales (each of their two loads writes all 64 lanes)
+  const size_t fixed = static_cast<size_t>(pl->nfilt) * 1024 + 2048;
+  bool found = false;
+  double best = 0.0;
+  for (int bh = 1; bh <= g.Ho; ++bh) {
+    const long long hr = static_cast<long long>(bh - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
+    const size_t lds = fixed + static_cast<size_t>(hr) * pl->P;
+    if (lds > static_cast<size_t>(kSbLds)) break;
+    const long long bands = (g.Ho + bh - 1) / bh;
+    const long long wgs = static_cast<long long>(g.N) * bands * (g.K / 64);
+    const long long rounds = (wgs + cus - 1) / cus;
+    // segments per wave plus a fixed cost for the loads
+    const double cost = static_cast<double>(rounds) * ((bh * segr + kSbWaves - 1) / kSbWaves + 3);
+    if (!found || cost < best - 1e-9) {
+      found = true;
+      best = cost;
+      pl->BH = bh;
+      pl->bands_per_img = static_cast<int>(bands);
+      pl->HR = static_cast<int>(hr);
+      pl->filt_lds = 0;
+      pl->ep_lds = pl->nfilt * 1024;
+      pl->halo_lds = pl->ep_lds + 2048;
+      pl->lds = lds;
+    }
+  }
+  if (!found) return false;
+  const long long blocks = static_cast<long long>(g.N) * pl->bands_per_img * (g.K / 64);
+  return blocks <= 0x7fffffffLL;
+}
+
+template <int EPI>
+void launch_band(const StemBandArgs& a, const StemBandPlan& pl, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(a.nblocks));
+  auto go = [&](auto kern) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(pl.lds));
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kSbWaves), pl.lds, stream, a);
+  };
+  switch (pl.KB) {
+    case 1: go(i8_stem_band_kernel<1, EPI>); break;
+    case 2: go(i8_stem_band_kernel<2, EPI>); break;
+    case 3: go(i8_stem_band_kernel<3, EPI>); break;
+    default: go(i8_stem_band_kernel<4, EPI>); break;
+  }
+}
+
+hipError_t launch_stem_band(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                            const StemBandPlan& pl, hipStream_t stream) {
+  StemBandArgs a;
+  a.x = x; a.w = w; a.bias = rq.bias; a.wscale = rq.wscale; a.y = y;
+  a.H = g.H; a.W = g.W; a.C = g.C; a.K = g.K; a.Ho = g.Ho; a.Wo = g.Wo;
+  a.ph = g.ph; a.pw = g.pw; a.sh = g.sh; a.sw = g.sw; a.dh = g.dh;
+  a.SC = g.S * g.C; a.RSC = g.R * a.SC; a.CPR = pl.CPR; a.NQ = pl.NQ;
+  a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.nbands = g.N * pl.bands_per_img;
+  a.nblocks = a.nbands * (g.K / 64);
+  a.SEGR = (g.Wo + 15) / 16;
+  a.P = pl.P; a.PLB = pl.PLB; a.rows_ld = pl.rows_ld; a.HR = pl.HR; a.nfilt = pl.nfilt;
+  a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.halo_lds = pl.halo_lds;
+  a.act_scale = rq.act_scale; a.relu = rq.relu;
+  a.fd_nbands = fastdiv_m(a.nbands);
+  a.fd_bpi = fastdiv_m(pl.bands_per_img);
+  a.fd_segr = fastdiv_m(a.SEGR);
+  a.fd_rowsld = fastdiv_m(pl.rows_ld);
+  switch (epi) {
+    case kEpiI8: launch_band<kEpiI8>(a, pl, stream); break;
+    case kEpiAcc32: launch_band<kEpiAcc32>(a, pl, stream); break;
+    default: launch_band<kEpiF32>(a, pl, stream); break;
+  }
+  return hipGetLastError();
+}
+
 struct StemPlan {
   int RowB, CPR, NQ, KB;
   int RB, tiles_h;
   int PL, P, w_off, w_bytes, ep_off;
   size_t lds;
 };
-
-int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 bool make_plan(const Geom& g, StemPlan* pl) {
   const int SC = g.S * g.C;
@@ -290,6 +584,10 @@ bool stem_eligible(const Geom& g, const void* x, const void* w, const void* y, E
 hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream) {
   if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
+  {
+    StemBandPlan bp;
+    if (make_band_plan(g, &bp)) return launch_stem_band(g, epi, x, w, y, rq, bp, stream);
+  }
   StemPlan pl;
   if (!make_plan(g, &pl)) return hipErrorInvalidConfiguration;
   StemArgs a;
