@@ -216,7 +216,8 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   auto emit = [&](const v4i (&acc)[4], int q) {
     const unsigned soff = row_off(q);
     if constexpr (EPI == kEpiI8) {
-      __builtin_amdgcn_raw_buffer_store_b128(pack_i8(acc, mult_v, lo), ry, lane_out, soff, kStoreAux);
+      const v4i pk = a.relu ? pack_u8_relu(acc, mult_v) : pack_i8(acc, mult_v, lo);
+      __builtin_amdgcn_raw_buffer_store_b128(pk, ry, lane_out, soff, kStoreAux);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {

@@ -97,6 +97,25 @@ __device__ __forceinline__ v4i pack_i8(const v4i (&acc)[4], const v4f (&mult)[4]
   return pk;
 }
 
+// With ReLU the int8 result is clamp(rint(v), 0, 127) (NaN -> 0), so v_cvt_pk_u8_f32 --
+// round to nearest even, saturate to [0, 255], NaN -> 0 (checked on the device against
+// rint for ties, near-ties, NaN and infinities) -- rounds and packs each value of
+// med3(v, 0, 127) in one instruction.
+__device__ __forceinline__ v4i pack_u8_relu(const v4i (&acc)[4], const v4f (&mult)[4]) {
+  v4i pk;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    unsigned u = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = __builtin_amdgcn_fmed3f(static_cast<float>(acc[j][r]) * mult[j][r], 0.0f, 127.0f);
+      u = __builtin_amdgcn_cvt_pk_u8_f32(v, static_cast<unsigned>(r), u);
+    }
+    pk[j] = static_cast<int>(u);
+  }
+  return pk;
+}
+
 // Returns a copy of a kernel-argument struct with every 32-bit word already in an SGPR.
 // The compiler otherwise fetches kernel arguments lazily, one s_load batch (and one full
 // memory round trip) per first use, and a kernel whose addressing needs many fields pays

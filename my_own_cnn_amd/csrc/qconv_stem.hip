@@ -23,9 +23,9 @@
 // instructions whose lane l carries row bytes [1024m + 16l - PLB, +16).  A lane whose
 // bytes lie left or right of the row, or a row outside the image, gets an offset past
 // num_records and writes zeros, so the padding costs nothing.  Then each wave takes
-// 16-pixel segments of the band in turn: its four K-blocks' operands come from the staged
-// rows at arbitrary byte offsets, and the int8 result of 16 channels per lane leaves in
-// one 16-byte buffer store.
+// 16-pixel segments of the band in turn: its K-blocks' operands come from the staged rows
+// at arbitrary byte offsets (read one segment ahead), and the int8 result of 16 channels
+// per lane leaves in one 16-byte buffer store.
 
 #include "qconv_device.h"
 
@@ -360,23 +360,55 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
       make_rsrc(static_cast<char*>(a.y) + out0 * kOutBytes, band_rows * a.Wo * a.K * kOutBytes);
   const unsigned char* hbytes = bytes + a.halo_lds;
 
+  // A segment's operands: this lane's window starts at byte `base` of the band's staged
+  // rows; K-block b's chunk lies qoff[b] further (a multiple of 16), so all of a segment's
+  // reads share one dword alignment.  The five dwords of every chunk are read one segment
+  // ahead, into `raw`, and funnel-shifted when the segment starts.
   const int nseg = band_rows * a.SEGR;
+  auto window = [&](int sg, int& t, int& wo) {
+    t = fdiv(sg, a.fd_segr);
+    wo = 16 * (sg - t * a.SEGR) + row_l;
+    return t * a.sh * a.P + a.PLB + ((wo < a.Wo ? wo : a.Wo - 1) * a.sw - a.pw) * a.C;
+  };
+  unsigned raw[KB][5];
+  auto fetch = [&](int base) {
+    const unsigned* p = reinterpret_cast<const unsigned*>(hbytes + (base & ~3));
+#pragma unroll
+    for (int b = 0; b < KB; ++b)
+#pragma unroll
+      for (int i = 0; i < 5; ++i) raw[b][i] = p[qoff[b] / 4 + i];
+  };
+  int t = 0, wo = 0, base = 0;
+  if (wave < nseg) {
+    base = window(wave, t, wo);
+    fetch(base);
+  }
   for (int sg = wave; sg < nseg; sg += kSbWaves) {
-    const int t = fdiv(sg, a.fd_segr);
-    const int wo = 16 * (sg - t * a.SEGR) + row_l;
-    const bool pix = wo < a.Wo;
-    const int base = t * a.sh * a.P + a.PLB + ((pix ? wo : a.Wo - 1) * a.sw - a.pw) * a.C;
+    const unsigned sh = static_cast<unsigned>(base & 3);
+    v4i B[KB];
+#pragma unroll
+    for (int b = 0; b < KB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) B[b][i] = static_cast<int>(__builtin_amdgcn_alignbyte(raw[b][i + 1], raw[b][i], sh));
+    const int t_cur = t, wo_cur = wo;
+    // the next segment's reads may not move above the shifts that consume `raw`
+    __builtin_amdgcn_sched_barrier(0);
+    // (the last segment re-reads its own window: unconditional reads keep `raw` in place)
+    base = window(sg + kSbWaves < nseg ? sg + kSbWaves : sg, t, wo);
+    fetch(base);
+    // a pixel past the row's end gets an offset 2^30 higher: past num_records, dropped
+    const unsigned voff = static_cast<unsigned>(((t_cur * a.Wo + wo_cur) * a.K + 16 * grp_l) * kOutBytes) +
+                          (static_cast<unsigned>(wo_cur >= a.Wo) << 30);
     v4i acc[4];
 #pragma unroll
     for (int b = 0; b < KB; ++b) {
-      const v4i B = lds_load16_unaligned(hbytes, base + qoff[b]);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][j], B, b == 0 ? bias_v[j] : acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][j], B[b], b == 0 ? bias_v[j] : acc[j], 0, 0, 0);
     }
-    const unsigned voff = pix ? static_cast<unsigned>(((t * a.Wo + wo) * a.K + 16 * grp_l) * kOutBytes) : 0x40000000u;
     if constexpr (EPI == kEpiI8) {
-      __builtin_amdgcn_raw_buffer_store_b128(pack_i8(acc, mult_v, lo), ry, voff, 0, kStoreAux);
+      const v4i pk = a.relu ? pack_u8_relu(acc, mult_v) : pack_i8(acc, mult_v, lo);
+      __builtin_amdgcn_raw_buffer_store_b128(pk, ry, voff, 0, kStoreAux);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
