@@ -78,7 +78,8 @@ struct BandArgs {
   // per K-block: LDS slot offset of its (filter row, chunk quad) << 8 | halo column shift
   // (filter column * dilation, < 256); the struct stays within 64 words, one s_load batch
   int tap[kBandMaxKB];
-  FastDivM fd_nbands, fd_bpi, fd_ktpg, fd_rowi, fd_npb;
+  int ntiles;         // channel tiles per band: groups * kt_per_group
+  FastDivM fd_ntiles, fd_bpi, fd_ktpg, fd_rowi, fd_npb;
 };
 
 static_assert(sizeof(BandArgs) <= 256, "kernel arguments fit one s_load batch");
@@ -97,8 +98,10 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   const int grp_l = lane >> 4;
 
   const int lin = xcd_tile(blockIdx.x, a.nblocks);
-  const int ctile = fdiv(lin, a.fd_nbands);
-  const int band = lin - ctile * a.nbands;
+  // channel tile fastest: the tiles of one band (which read the same input rows) get
+  // neighbouring indices and so one XCD's L2
+  const int band = fdiv(lin, a.fd_ntiles);
+  const int ctile = lin - band * a.ntiles;
   const int n = fdiv(band, a.fd_bpi);
   const int bi = band - n * a.bands_per_img;
   const int gi = fdiv(ctile, a.fd_ktpg);
@@ -458,7 +461,8 @@ hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t*
       a.tap[b] = 0;
     }
   }
-  a.fd_nbands = fastdiv_m(a.nbands);
+  a.ntiles = g.G * pl.kt_per_group;
+  a.fd_ntiles = fastdiv_m(a.ntiles);
   a.fd_bpi = fastdiv_m(pl.bands_per_img);
   a.fd_ktpg = fastdiv_m(pl.kt_per_group);
   a.fd_rowi = fastdiv_m(pl.NQ * pl.NPB);
