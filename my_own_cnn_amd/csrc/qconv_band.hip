@@ -64,12 +64,15 @@ struct BandArgs {
   int Cg, Kg, Kdim;
   int BH;             // output rows per band
   int bands_per_img;  // ceil(Ho / BH)
-  int nbands;         // N * bands_per_img
-  int kt_per_group;   // 64-channel tiles per group
+  int NT, WPT;        // 64-channel tiles per workgroup, waves per tile (8 / NT)
+  int kt_per_group;   // workgroup channel tiles (NT * 64 channels) per group
   int nblocks;        // workgroups of the launch (gridDim would be one more kernarg round trip)
   int NQ, NPB;        // chunk quads (Cg / 64) and 16-column blocks per input row
-  int SEGR, RPAR;     // segment columns per output row, row phases per wave
-  int nphase;         // ceil(BH / RPAR)
+  int SEGR;           // 16-pixel segment columns per output row
+  // per phase a wave's segment advances WPT = dT * SEGR + dS segments: its input offset
+  // by d_rb bytes and its output offset by d_out elements, plus c_rb / c_out when the
+  // column wraps past the row's end
+  int dS, d_rb, c_rb, d_out, c_out;
   int ni;             // input load instructions per workgroup = HR * NQ * NPB
   int ni0;            // those of the input rows phase 0 reads
   int filt_lds, ep_lds, halo_lds;  // LDS byte offsets
@@ -78,15 +81,19 @@ struct BandArgs {
   // per K-block: LDS slot offset of its (filter row, chunk quad) << 8 | halo column shift
   // (filter column * dilation, < 256); the struct stays within 64 words, one s_load batch
   int tap[kBandMaxKB];
-  int ntiles;         // channel tiles per band: groups * kt_per_group
+  int ntiles;         // workgroup channel tiles per band: groups * kt_per_group
   FastDivM fd_ntiles, fd_bpi, fd_ktpg, fd_rowi, fd_npb;
 };
 
 static_assert(sizeof(BandArgs) <= 256, "kernel arguments fit one s_load batch");
 
-template <int KB, int EPI>
+// MT: more than one 64-channel tile per workgroup (NT > 1); the single-tile
+// instantiation keeps its tile arithmetic at compile time
+template <int KB, int EPI, bool MT>
 __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_in) {
   const BandArgs a = preload_args(a_in);
+  const int NT = MT ? a.NT : 1;
+  const int WPT = MT ? a.WPT : kBandWaves;
   extern __shared__ v4i smem[];
   v4i* filt = smem + a.filt_lds / 16;
   v4i* halo = smem + a.halo_lds / 16;
@@ -105,31 +112,38 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   const int n = fdiv(band, a.fd_bpi);
   const int bi = band - n * a.bands_per_img;
   const int gi = fdiv(ctile, a.fd_ktpg);
-  const int k0 = (ctile - gi * a.kt_per_group) * 64;
+  const int k0 = (ctile - gi * a.kt_per_group) * NT * 64;  // first channel (in group gi)
   const int ho0 = bi * a.BH;
+  // wave -> 64-channel tile tw of the workgroup, and its rank wl among the tile's waves
+  const int tw = MT ? wave / WPT : 0;
+  const int wl = wave - tw * WPT;
   const int row_instr = a.NQ * a.NPB;  // input load instructions per input row
 
   // Scalar work is shared by the waves of a SIMD (one instruction per wave per issue
   // turn), so the loads below use one buffer resource each and keep per-load work to a
   // few instructions.
   //
-  // ---- filter -> LDS.  Fragment f = 4b + j (K-block b, MFMA row block j) goes to wave
-  // f % 8.  Its lane (row_l, grp_l) holds channel k0 + 16*(row_l/4) + 4j + row_l%4, bytes
-  // [16*(4b + grp_l), +16) of that channel's KRSC row; channels at or beyond Kg lie past
-  // num_records (zeros).
+  // ---- filter -> LDS.  Fragment f = 4KB*t + 4b + j (64-channel tile t, K-block b, MFMA
+  // row block j) goes to wave f % 8.  Its lane (row_l, grp_l) holds channel
+  // k0 + 64t + 16*(row_l/4) + 4j + row_l%4, bytes [16*(4b + grp_l), +16) of that channel's
+  // KRSC row; channels at or beyond Kg lie past num_records (zeros).
   {
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + static_cast<size_t>(gi) * a.Kg * a.Kdim, a.Kg * a.Kdim);
     const unsigned lane_row = static_cast<unsigned>((16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
-    for (int f = wave; f < 4 * KB; f += kBandWaves) {
-      load_lds16(rw, filt + f * 64, lane_row, static_cast<unsigned>((k0 + 4 * (f & 3)) * a.Kdim + 64 * (f >> 2)));
+    for (int f = wave; f < NT * 4 * KB; f += kBandWaves) {
+      const int t = MT ? f / (4 * KB) : 0;
+      const int ff = f - t * (4 * KB);
+      load_lds16(rw, filt + f * 64, lane_row,
+                 static_cast<unsigned>((k0 + 64 * t + 4 * (ff & 3)) * a.Kdim + 64 * (ff >> 2)));
     }
   }
-  // ---- bias and per-channel scales of the tile's 64 channels ----
-  if (EPI != kEpiAcc32 && wave == 0) {
-    const int valid = max(0, a.Kg - k0) * 4;
-    const size_t off = static_cast<size_t>(gi) * a.Kg + min(k0, a.Kg);
-    load_lds16(make_rsrc(a.bias ? a.bias + off : nullptr, a.bias ? valid : 0), ep, 16u * lane, 0);
-    load_lds16(make_rsrc(a.wscale + off, valid), ep + 64, 16u * lane, 0);
+  // ---- bias and per-channel scales of tile t's 64 channels (wave t), 2 KB of LDS each ----
+  if (EPI != kEpiAcc32 && wave < NT) {
+    const int kt = k0 + 64 * wave;
+    const int valid = max(0, a.Kg - kt) * 4;
+    const size_t off = static_cast<size_t>(gi) * a.Kg + min(kt, a.Kg);
+    load_lds16(make_rsrc(a.bias ? a.bias + off : nullptr, a.bias ? valid : 0), ep + 128 * wave, 16u * lane, 0);
+    load_lds16(make_rsrc(a.wscale + off, valid), ep + 128 * wave + 64, 16u * lane, 0);
   }
   // ---- every input row of the band, in row order: instruction i = (row * NQ + quad) *
   // NPB + block goes to wave i % 8; its lane l reads column 16 * block + l % 16 - pw, chunk
@@ -166,9 +180,9 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
 #pragma unroll
   for (int b = 0; b < KB; ++b)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) A[b][j] = filt[(b * 4 + j) * 64 + lane];
+    for (int j = 0; j < 4; ++j) A[b][j] = filt[(tw * 4 * KB + b * 4 + j) * 64 + lane];
   // epilogue parameters of this lane's 16 channels kc0 + 4j + r (zero past Kg)
-  const int kc0 = k0 + 16 * grp_l;
+  const int kc0 = k0 + 64 * tw + 16 * grp_l;
   const bool ch_ok = kc0 < a.Kg;  // Kg % 16 == 0: a lane's 16 channels all exist or none does
   v4i bias_v[4];
   v4f mult_v[4];
@@ -177,50 +191,69 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
     bias_v[j] = v4i{0, 0, 0, 0};
     mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (EPI != kEpiAcc32) {
-      bias_v[j] = ep[4 * grp_l + j];
-      const v4i ws = ep[64 + 4 * grp_l + j];
+      bias_v[j] = ep[128 * tw + 4 * grp_l + j];
+      const v4i ws = ep[128 * tw + 64 + 4 * grp_l + j];
 #pragma unroll
       for (int r = 0; r < 4; ++r) mult_v[j][r] = requant_multiplier(a.act_scale, __int_as_float(ws[r]));
     }
   }
 
-  const bool wave_on = wave < a.SEGR * a.RPAR;
-  const int sc = wave_on ? wave % a.SEGR : 0;
-  const int rp = wave_on ? wave / a.SEGR : 0;
-  const int wo = 16 * sc + row_l;
-  // LDS byte address of this lane's fragment of K-block b in the band's first output row:
-  // column x = wo + shift lies in block x / 16 at position x % 16, i.e. slot
+  // Phase p of wave wl works on segment s = wl + p * WPT of the band's band_rows * SEGR
+  // (row t = s / SEGR, segment column sc = s % SEGR: output columns 16 * sc + row_l).
+  // LDS byte address of this lane's fragment of K-block b in segment (0, 0): column
+  // x = row_l + shift lies in block x / 16 at position x % 16, i.e. slot
   // 64 * (x / 16) + x % 16 = x + 48 * (x / 16); plus its chunk and the K-block's row and
-  // quad.  A phase adds one uniform row offset.
+  // quad.  Segment (t, sc) adds the uniform t * row_bytes + sc * 1024.
   const unsigned halo_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(halo) & 0xffffffffu);
   unsigned baddr[KB];
 #pragma unroll
   for (int b = 0; b < KB; ++b) {
     const int x = row_l + (a.tap[b] & 0xff);
-    baddr[b] = halo_addr + 16u * static_cast<unsigned>((a.tap[b] >> 8) + 64 * sc + 16 * grp_l + x + 48 * (x >> 4));
+    baddr[b] = halo_addr + 16u * static_cast<unsigned>((a.tap[b] >> 8) + 16 * grp_l + x + 48 * (x >> 4));
   }
   const unsigned row_bytes = 16u * static_cast<unsigned>(a.sh * row_instr * 64);  // per output row
   const float lo = a.relu ? 0.0f : -128.0f;
 
   // Output through a buffer resource over the band's rows (of image n, group gi): the lane
-  // part of the offset is fixed, the row part goes into soffset.  A lane whose pixel or
-  // channels do not exist, or a row past the band, gets 2^30 and its store is dropped.
+  // part of the offset is fixed, the segment part goes into soffset.  A lane whose pixel or
+  // channels do not exist gets 2^30 more and its store is dropped.
   constexpr int kOutBytes = EPI == kEpiI8 ? 1 : 4;
   const int band_rows = min(a.BH, a.Ho - ho0);
   const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + static_cast<size_t>(gi) * a.Kg;
   const __amdgpu_buffer_rsrc_t ry =
       make_rsrc(static_cast<char*>(a.y) + out0 * kOutBytes, band_rows * a.Wo * a.K * kOutBytes);
-  const unsigned lane_out =
-      (wave_on && wo < a.Wo && ch_ok) ? static_cast<unsigned>((wo * a.K + kc0) * kOutBytes) : 0x40000000u;
-  auto row_off = [&](int q) {
-    const int t = q * a.RPAR + rp;
-    return t < band_rows ? static_cast<unsigned>(t * a.Wo * a.K * kOutBytes) : 0x40000000u;
+  const unsigned lane_out = static_cast<unsigned>((row_l * a.K + kc0) * kOutBytes) + (ch_ok ? 0u : 0x40000000u);
+  const int nseg = band_rows * a.SEGR;
+  // The segment (row t, column seg_c) of the current phase, walked forward by WPT segments
+  // per phase: its input offset seg_in (t * row_bytes + 1024 * seg_c), output soffset
+  // seg_out ((t * Wo + 16 * seg_c) * K elements) and this lane's output offset (2^30 more
+  // for a pixel past the row's end: only the last column can hold one).
+  int seg_t = 0, seg_c = wl;  // wl < 8: a few subtractions
+  while (seg_c >= a.SEGR) {
+    seg_c -= a.SEGR;
+    ++seg_t;
+  }
+  unsigned seg_in = static_cast<unsigned>(seg_t) * row_bytes + 1024u * static_cast<unsigned>(seg_c);
+  int seg_out = (seg_t * a.Wo + 16 * seg_c) * a.K;
+  const unsigned lane_last = lane_out + (16 * (a.SEGR - 1) + row_l < a.Wo ? 0u : 0x40000000u);
+  auto seg_rb = [&]() { return seg_in; };
+  auto seg_soff = [&]() { return static_cast<unsigned>(seg_out * kOutBytes); };
+  auto seg_lane = [&]() { return seg_c == a.SEGR - 1 ? lane_last : lane_out; };
+  auto seg_next = [&]() {
+    seg_c += a.dS;
+    seg_in += static_cast<unsigned>(a.d_rb);
+    seg_out += a.d_out;
+    if (seg_c >= a.SEGR) {
+      seg_c -= a.SEGR;
+      seg_in += static_cast<unsigned>(a.c_rb);
+      seg_out += a.c_out;
+    }
   };
-  auto emit = [&](const v4i (&acc)[4], int q) {
-    const unsigned soff = row_off(q);
+  auto emit = [&](const v4i (&acc)[4], unsigned soff, unsigned lane_out_q) {
     if constexpr (EPI == kEpiI8) {
       const v4i pk = a.relu ? pack_u8_relu(acc, mult_v) : pack_i8(acc, mult_v, lo);
-      __builtin_amdgcn_raw_buffer_store_b128(pk, ry, lane_out, soff, kStoreAux);
+      __builtin_amdgcn_raw_buffer_store_b128(pk, ry, lane_out_q, soff, kStoreAux);
+      store_gap(pk);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -233,13 +266,12 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
             v[r] = __float_as_int(f);
           }
         }
-        __builtin_amdgcn_raw_buffer_store_b128(v, ry, lane_out + 16 * j, soff, kStoreAux);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, lane_out_q + 16 * j, soff, kStoreAux);
+        store_gap(v);
       }
     }
   };
-  auto mfma_phase = [&](int p, v4i (&acc)[4]) {
-    // rows past the band reuse its last row (their results are dropped)
-    const unsigned rb = static_cast<unsigned>(min(p * a.RPAR + rp, a.BH - 1)) * row_bytes;
+  auto mfma_phase = [&](unsigned rb, v4i (&acc)[4]) {
     // input fragments are read RS K-blocks ahead: each read goes out right after the
     // MFMAs that free its register
     constexpr int RS = KB < 4 ? KB : 4;
@@ -273,32 +305,35 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   // The two waves of a SIMD (waves w and w + 4) are skewed by one epilogue: the "leading"
   // wave w < 4 runs MFMA(p) then the epilogue of p; the trailing one runs the epilogue of
   // p - 1 then MFMA(p), so one wave's VALU work runs beside the other's matrix instructions.
-  // Phases whose row lies past the band (or past the image) are skipped, wave-uniformly.
-  const int nph = wave_on ? min(a.nphase, (band_rows - rp + a.RPAR - 1) / a.RPAR) : 0;
+  const int nph = wl < nseg ? (nseg - wl + WPT - 1) / WPT : 0;
   v4i acc[4];
   if (wave < kBandWaves / 2) {
     for (int p = 0; p < nph; ++p) {
-      mfma_phase(p, acc);
+      mfma_phase(seg_rb(), acc);
       if (p == 0) wait_rest();
-      emit(acc, p);
+      emit(acc, seg_soff(), seg_lane());
+      seg_next();
     }
     if (nph == 0) wait_rest();
   } else {
+    unsigned soff_prev = 0, lane_prev = 0;  // the previous phase's output offsets
     for (int p = 0; p < nph; ++p) {
       v4i prev[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) prev[j] = acc[j];
       if (p == 1) wait_rest();
-      if (p > 0) emit(prev, p - 1);
-      mfma_phase(p, acc);
+      if (p > 0) emit(prev, soff_prev, lane_prev);
+      mfma_phase(seg_rb(), acc);
+      soff_prev = seg_soff();
+      lane_prev = seg_lane();
+      seg_next();
     }
     if (nph <= 1) wait_rest();
-    if (nph > 0) emit(acc, nph - 1);
+    if (nph > 0) emit(acc, soff_prev, lane_prev);
   }
 }
-
 struct BandPlan {
-  int KB, NQ, NPB, SEGR, RPAR, BH, bands_per_img, kt_per_group, HR, ni, nphase;
+  int KB, NQ, NPB, SEGR, NT, WPT, BH, bands_per_img, kt_per_group, HR, ni, ni0;
   int filt_lds, ep_lds, halo_lds;
   size_t lds_bytes;
 };
@@ -334,36 +369,51 @@ bool band_plan(const Geom& g, Epi epi, BandPlan* p, std::string* why) {
   p->NQ = g.Cg / 64;
   p->NPB = static_cast<int>((hcols + 15) / 16);
   p->SEGR = (g.Wo + 15) / 16;
-  p->RPAR = p->SEGR > kBandWaves / 2 ? 1 : kBandWaves / p->SEGR;
-  p->kt_per_group = (g.Kg + 63) / 64;
+  const int kt64 = (g.Kg + 63) / 64;  // 64-channel tiles per group
   const int cus = band_cu_count();
-  const size_t filt_bytes = static_cast<size_t>(p->KB) * 4 * 1024;
+  // Cost in cycles of one round of workgroups (one per CU): the busiest SIMD runs two
+  // waves whose matrix instructions and epilogue VALU work do not overlap (measured), so
+  // a phase costs KB * 4 MFMAs of 16 cycles plus about 450 cycles of epilogue, twice;
+  // loading the filter and the input rows costs about a cycle per 25 bytes plus a fixed
+  // 2400 (launch, first loads, barriers).
   bool found = false;
   double best = 0.0;
-  for (int bh = 1; bh <= g.Ho; ++bh) {
-    const long long hr = static_cast<long long>(bh - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
-    const long long ni = hr * p->NQ * p->NPB;
-    if (ni > kBandWaves * 15) break;  // at most 15 input loads per wave (exact vmcnt waits)
-    const int nphase = (bh + p->RPAR - 1) / p->RPAR;
-    const size_t lds = filt_bytes + 2048 + static_cast<size_t>(ni + 1) * 1024;
-    if (lds > static_cast<size_t>(kBandLds)) break;
-    const long long bands = (g.Ho + bh - 1) / bh;
-    const long long wgs = static_cast<long long>(g.N) * bands * g.G * p->kt_per_group;
-    const long long rounds = (wgs + cus - 1) / cus;
-    // phases of work per round plus a fixed cost for the filter and the first input rows
-    const double cost = static_cast<double>(rounds) * (nphase + 2.5);
-    if (!found || cost < best - 1e-9) {
-      found = true;
-      best = cost;
-      p->BH = bh;
-      p->bands_per_img = static_cast<int>(bands);
-      p->HR = static_cast<int>(hr);
-      p->ni = static_cast<int>(ni);
-      p->nphase = nphase;
-      p->filt_lds = 0;
-      p->ep_lds = static_cast<int>(filt_bytes);
-      p->halo_lds = static_cast<int>(filt_bytes + 2048);
-      p->lds_bytes = lds;
+  for (int nt = 1; nt <= kBandWaves; nt *= 2) {
+    if (kt64 % nt != 0) continue;
+    const int wpt = kBandWaves / nt;
+    const size_t filt_bytes = static_cast<size_t>(nt) * p->KB * 4 * 1024;
+    for (int bh = 1; bh <= g.Ho; ++bh) {
+      const long long hr = static_cast<long long>(bh - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
+      const long long ni = hr * p->NQ * p->NPB;
+      if (ni > kBandWaves * 15) break;  // at most 15 input loads per wave (exact vmcnt waits)
+      const size_t lds = filt_bytes + static_cast<size_t>(nt) * 2048 + static_cast<size_t>(ni + 1) * 1024;
+      if (lds > static_cast<size_t>(kBandLds)) break;
+      const long long bands = (g.Ho + bh - 1) / bh;
+      const long long wgs = static_cast<long long>(g.N) * bands * g.G * (kt64 / nt);
+      const long long rounds = (wgs + cus - 1) / cus;
+      const long long nph = (static_cast<long long>(bh) * p->SEGR + wpt - 1) / wpt;
+      const double phase = p->KB * 64.0 + 450.0;
+      const double load = 2400.0 + static_cast<double>(filt_bytes + ni * 1024) / 25.0;
+      const double cost = static_cast<double>(rounds) * (2.0 * static_cast<double>(nph) * phase + load);
+      if (!found || cost < best - 1e-9) {
+        found = true;
+        best = cost;
+        p->NT = nt;
+        p->WPT = wpt;
+        p->kt_per_group = kt64 / nt;
+        p->BH = bh;
+        p->bands_per_img = static_cast<int>(bands);
+        p->HR = static_cast<int>(hr);
+        p->ni = static_cast<int>(ni);
+        // input rows the first phase of every wave reads: segments 0 .. WPT-1
+        const long long rows0 = std::min<long long>(hr, static_cast<long long>((wpt - 1) / p->SEGR) * g.sh +
+                                                            static_cast<long long>(g.R - 1) * g.dh + 1);
+        p->ni0 = static_cast<int>(rows0 * p->NQ * p->NPB);
+        p->filt_lds = 0;
+        p->ep_lds = static_cast<int>(filt_bytes);
+        p->halo_lds = static_cast<int>(filt_bytes + static_cast<size_t>(nt) * 2048);
+        p->lds_bytes = lds;
+      }
     }
   }
   if (!found) return no("band kernel input rows do not fit in LDS");
@@ -377,21 +427,21 @@ void band_launch_kb(const BandArgs& a, const BandPlan& pl, Epi epi, unsigned nbl
   const dim3 grid(nblocks);
   switch (epi) {
     case kEpiI8: {
-      auto kern = i8_band_kernel<KB, kEpiI8>;
+      auto kern = pl.NT > 1 ? i8_band_kernel<KB, kEpiI8, true> : i8_band_kernel<KB, kEpiI8, false>;
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(pl.lds_bytes));
       hipLaunchKernelGGL(kern, grid, dim3(64 * kBandWaves), pl.lds_bytes, stream, a);
       break;
     }
     case kEpiAcc32: {
-      auto kern = i8_band_kernel<KB, kEpiAcc32>;
+      auto kern = pl.NT > 1 ? i8_band_kernel<KB, kEpiAcc32, true> : i8_band_kernel<KB, kEpiAcc32, false>;
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(pl.lds_bytes));
       hipLaunchKernelGGL(kern, grid, dim3(64 * kBandWaves), pl.lds_bytes, stream, a);
       break;
     }
     default: {
-      auto kern = i8_band_kernel<KB, kEpiF32>;
+      auto kern = pl.NT > 1 ? i8_band_kernel<KB, kEpiF32, true> : i8_band_kernel<KB, kEpiF32, false>;
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 static_cast<int>(pl.lds_bytes));
       hipLaunchKernelGGL(kern, grid, dim3(64 * kBandWaves), pl.lds_bytes, stream, a);
@@ -436,14 +486,9 @@ hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t*
   a.H = g.H; a.W = g.W; a.C = g.C; a.K = g.K; a.Ho = g.Ho; a.Wo = g.Wo;
   a.ph = g.ph; a.pw = g.pw; a.sh = g.sh;
   a.Cg = g.Cg; a.Kg = g.Kg; a.Kdim = g.R * g.S * g.Cg;
-  a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.nbands = g.N * pl.bands_per_img;
-  a.kt_per_group = pl.kt_per_group; a.NQ = pl.NQ; a.NPB = pl.NPB; a.SEGR = pl.SEGR; a.RPAR = pl.RPAR;
-  a.nphase = pl.nphase; a.ni = pl.ni;
-  {
-    const long long rows0 = std::min<long long>(pl.HR, static_cast<long long>(pl.RPAR - 1) * g.sh +
-                                                           static_cast<long long>(g.R - 1) * g.dh + 1);
-    a.ni0 = static_cast<int>(rows0) * pl.NQ * pl.NPB;
-  }
+  a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.NT = pl.NT; a.WPT = pl.WPT;
+  a.kt_per_group = pl.kt_per_group; a.NQ = pl.NQ; a.NPB = pl.NPB; a.SEGR = pl.SEGR;
+  a.ni = pl.ni; a.ni0 = pl.ni0;
   a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.halo_lds = pl.halo_lds;
   a.act_scale = rq.act_scale; a.relu = rq.relu;
   // K-block b = chunks 4b .. 4b+3 of the flattened (tap, 16-channel chunk) order, all of
@@ -467,7 +512,16 @@ hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t*
   a.fd_ktpg = fastdiv_m(pl.kt_per_group);
   a.fd_rowi = fastdiv_m(pl.NQ * pl.NPB);
   a.fd_npb = fastdiv_m(pl.NPB);
-  const long long nblocks = static_cast<long long>(a.nbands) * g.G * pl.kt_per_group;
+  {
+    const int dT = pl.WPT / pl.SEGR;
+    const int row_bytes = g.sh * pl.NQ * pl.NPB * 1024;  // LDS bytes of sh input rows
+    a.dS = pl.WPT % pl.SEGR;
+    a.d_rb = dT * row_bytes + 1024 * a.dS;
+    a.c_rb = row_bytes - 1024 * pl.SEGR;
+    a.d_out = (dT * g.Wo + 16 * a.dS) * g.K;
+    a.c_out = (g.Wo - 16 * pl.SEGR) * g.K;
+  }
+  const long long nblocks = static_cast<long long>(g.N) * pl.bands_per_img * g.G * pl.kt_per_group;
   a.nblocks = static_cast<int>(nblocks);
   band_dispatch<kBandMaxKB>(pl.KB, a, pl, epi, static_cast<unsigned>(nblocks), stream);
   return hipGetLastError();

@@ -97,6 +97,19 @@ __device__ __forceinline__ v4i pack_i8(const v4i (&acc)[4], const v4f (&mult)[4]
   return pk;
 }
 
+// Wait states after a 16-byte store before another instruction may overwrite its data
+// registers.  A vector-memory store of more than 64 bits needs one wait state before a
+// VALU write of its data VGPRs; the compiler leaves none when the store ends a loop body
+// and the loop header's first instruction overwrites them (seen: buffer_store_dwordx4
+// v[160:163] directly followed by v_add_u32 v160, and the first dword of some lanes
+// stored wrong, varying from run to run).  Two wait states after every such store close
+// that window: the statement reads the stored registers, so nothing may overwrite them
+// before it, and its "memory" clobber keeps the store ahead of it.
+template <typename V>
+__device__ __forceinline__ void store_gap(const V& data) {
+  asm volatile("s_nop 1" : : "v"(data) : "memory");
+}
+
 // With ReLU the int8 result is clamp(rint(v), 0, 127) (NaN -> 0), so v_cvt_pk_u8_f32 --
 // round to nearest even, saturate to [0, 255], NaN -> 0 (checked on the device against
 // rint for ties, near-ties, NaN and infinities) -- rounds and packs each value of
@@ -176,7 +189,10 @@ __device__ __forceinline__ void store16(void* y, size_t obase, const v4i (&acc)[
       }
       pk[j] = static_cast<int>(u);
     }
-    if (full) *reinterpret_cast<v4i*>(yp) = pk;
+    if (full) {
+      *reinterpret_cast<v4i*>(yp) = pk;
+      store_gap(pk);
+    }
   } else if constexpr (EPI == kEpiAcc32) {
     (void)ep_bias;
     (void)ep_mult;
@@ -186,6 +202,7 @@ __device__ __forceinline__ void store16(void* y, size_t obase, const v4i (&acc)[
     for (int j = 0; j < 4; ++j) {
       if (full) {
         reinterpret_cast<v4i*>(yp)[j] = acc[j];
+        store_gap(acc[j]);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -203,6 +220,7 @@ __device__ __forceinline__ void store16(void* y, size_t obase, const v4i (&acc)[
       for (int r = 0; r < 4; ++r) f[r] = dequant_f32(acc[j][r], bb[r], mm[r], relu);
       if (full) {
         reinterpret_cast<v4f*>(yp)[j] = f;
+        store_gap(f);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -245,7 +263,10 @@ __device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i&
           if (kc0 + 4 * j + r < Kg) yp[4 * j + r] = static_cast<int8_t>(u[r] & 0xffu);
       }
     }
-    if (full) *reinterpret_cast<v4i*>(yp) = pk;
+    if (full) {
+      *reinterpret_cast<v4i*>(yp) = pk;
+      store_gap(pk);
+    }
   } else if constexpr (EPI == kEpiAcc32) {
     (void)ep_mult;
     (void)relu;
@@ -254,6 +275,7 @@ __device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i&
     for (int j = 0; j < 4; ++j) {
       if (full) {
         reinterpret_cast<v4i*>(yp)[j] = *acc[j];
+        store_gap(*acc[j]);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -274,6 +296,7 @@ __device__ __forceinline__ void store16_biased(void* y, size_t obase, const v4i&
       }
       if (full) {
         reinterpret_cast<v4f*>(yp)[j] = f;
+        store_gap(f);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)

@@ -409,6 +409,7 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
     if constexpr (EPI == kEpiI8) {
       const v4i pk = a.relu ? pack_u8_relu(acc, mult_v) : pack_i8(acc, mult_v, lo);
       __builtin_amdgcn_raw_buffer_store_b128(pk, ry, voff, 0, kStoreAux);
+      store_gap(pk);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -422,6 +423,7 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
           }
         }
         __builtin_amdgcn_raw_buffer_store_b128(v, ry, voff + 16 * j, 0, kStoreAux);
+        store_gap(v);
       }
     }
   }

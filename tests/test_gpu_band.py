@@ -1,9 +1,9 @@
 """The row-band kernel (filter held in registers, input rows streamed into LDS) against the
 CPU oracle on every geometry class it accepts: output widths that leave partial 16-pixel
-segments (1 to 4 segment columns per row, so 4, 2 and 1 row phases per wave), a last band
-of the image that is only partly filled, vertical stride and dilation, padding wider than
-the filter reach, groups, several 64-channel tiles and a partial one, and inputs whose
-rows need two 64-column loads.  Integer outputs are bit-exact; the fp32 view is compared
+segments (1 to 4 segment columns per row), 1, 2, 4 or 8 channel tiles per workgroup, a
+last band of the image that is only partly filled, vertical stride and dilation, padding
+wider than the filter reach, groups, several 64-channel tiles and a partial one, and
+inputs whose rows need two 64-column loads.  Integer outputs are bit-exact; the fp32 view is compared
 bit for bit (tolerance 1 ulp, met with 0 ulp)."""
 import numpy as np
 import pytest
@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 SHAPES = [
     (2, 12, 12, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),     # Wo 12: one segment column, 4 row phases
     (1, 9, 29, 64, 32, 3, 3, (1, 1, 1, 1, 1, 1, 1)),      # Wo 29: two columns, partial channel tile
-    (2, 7, 40, 64, 48, 3, 3, (1, 1, 1, 1, 1, 1, 1)),      # Wo 40: three columns (one idle wave)
+    (2, 7, 40, 64, 48, 3, 3, (1, 1, 1, 1, 1, 1, 1)),      # Wo 40: three columns
     (3, 11, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),     # the r50 3x3 row shape, odd band split
     (1, 10, 64, 64, 80, 3, 3, (1, 1, 1, 1, 1, 1, 1)),     # Wo 64: rows of 66 columns, two loads each
     (2, 13, 20, 128, 64, 1, 3, (0, 1, 2, 1, 1, 1, 1)),    # stride_h 2, Cg16 = 8 (two K-blocks per tap)
@@ -32,6 +32,23 @@ SHAPES = [
 ]
 
 
+# Larger problems, for which the planner puts 2, 4 or 8 64-channel tiles in a workgroup
+# (fewer, fuller rounds) or bands of several rows whose last band is partly filled; the
+# comment gives the plan (tiles per workgroup, segment columns, band rows / output rows).
+SHAPES_TILES = [
+    (4, 19, 12, 64, 256, 3, 3, (1, 1, 1, 1, 1, 1, 1)),    # 1 tile, 1 column, bands of 2 / 19 rows
+    (4, 19, 40, 64, 256, 3, 3, (1, 1, 1, 1, 1, 1, 1)),    # 1 tile, 3 columns, 2 / 19
+    (4, 13, 50, 128, 512, 1, 1, (0, 0, 1, 1, 1, 1, 1)),   # 1 tile, 4 columns, 2 / 13
+    (8, 37, 12, 128, 512, 1, 1, (0, 0, 1, 1, 1, 1, 1)),   # 2 tiles, 1 column, 5 / 37
+    (24, 19, 20, 64, 256, 3, 3, (1, 1, 1, 1, 1, 1, 1)),   # 2 tiles, 2 columns, 3x3, 4 / 19
+    (8, 13, 40, 128, 512, 1, 1, (0, 0, 1, 1, 1, 1, 1)),   # 2 tiles, 3 columns, 2 / 13
+    (24, 19, 12, 128, 512, 1, 1, (0, 0, 1, 1, 1, 1, 1)),  # 4 tiles, 1 column, 4 / 19
+    (12, 28, 40, 128, 512, 1, 1, (0, 0, 1, 1, 1, 1, 1)),  # 4 tiles, 3 columns, 3 / 28
+    (12, 28, 50, 128, 512, 1, 1, (0, 0, 1, 1, 1, 1, 1)),  # 4 tiles, 4 columns, 3 / 28
+    (40, 30, 50, 128, 512, 1, 1, (0, 0, 1, 1, 1, 1, 1)),  # 8 tiles, 4 columns, 5 / 30
+]
+
+
 def _id(s):
     n, h, w, c, k, r, sz, conv = s
     return f"n{n}h{h}w{w}c{c}k{k}r{r}s{sz}p{conv[0]}{conv[1]}s{conv[2]}d{conv[4]}{conv[5]}g{conv[6]}"
@@ -39,9 +56,17 @@ def _id(s):
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[_id(s) for s in SHAPES])
 def test_band_kernel_matches_oracle(device, shape):
+    check_band(device, shape, 7000 + SHAPES.index(shape) * 16)
+
+
+@pytest.mark.parametrize("shape", SHAPES_TILES, ids=[_id(s) for s in SHAPES_TILES])
+def test_band_kernel_tiles_per_workgroup(device, shape):
+    check_band(device, shape, 7500 + SHAPES_TILES.index(shape) * 16)
+
+
+def check_band(device, shape, seed):
     n, h, wd, c, k, r, s, conv = shape
     g = conv[6]
-    seed = 7000 + SHAPES.index(shape) * 16
     x = W.fill_i8_uniform(n * h * wd * c, seed, -128, 127).reshape(n, h, wd, c)
     w = W.fill_i8_uniform(k * r * s * (c // g), seed + 1, -127, 127).reshape(k, r, s, c // g)
     bias = W.fill_i32_uniform(k, seed + 2, -1024, 1024)
