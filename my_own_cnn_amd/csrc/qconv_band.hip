@@ -2,12 +2,17 @@
 // filter-stationary MFMA (v_mfma_i32_16x16x64_i8), the band's input rows staged in LDS.
 //
 // Work decomposition.  A workgroup of 8 waves (two per SIMD) owns a band of BH consecutive
-// output rows of one image and one 64-channel tile of one group.  Output rows are cut into
-// 16-pixel segments (segment column sc covers wo = 16*sc .. 16*sc + 15; the last one may
-// be partly outside the image).  Wave w owns segment column w % SEGR of the rows
-// t = w / SEGR (mod RPAR) of the band, one row per phase.  A SIMD runs two waves so that
-// one wave's LDS reads and epilogue overlap the other's MFMAs: one wave cannot overlap
-// them with its own matrix instructions.
+// output rows of one image and NT (1, 2, 4 or 8) consecutive 64-channel tiles of one group;
+// WPT = 8 / NT waves work on each tile.  Output rows are cut into 16-pixel segments
+// (segment column sc covers wo = 16*sc .. 16*sc + 15; the last one may be partly outside
+// the image), numbered row-major over the band: s = t * SEGR + sc.  Wave wl of a tile
+// computes segments wl, wl + WPT, wl + 2*WPT, ... (one per phase), advancing its input and
+// output offsets incrementally.  The channel tile is the fastest index of the workgroup
+// order, so the workgroups of one band run side by side and share its input rows in one
+// XCD's L2.  A SIMD runs two waves so that one wave's LDS reads and epilogue overlap the
+// other's MFMAs: one wave cannot overlap them with its own matrix instructions.  The host
+// planner picks NT and BH by a cycle estimate: rounds of workgroups over the CUs x (phases
+// x (MFMA + epilogue) + start-up + the loads of filter and rows).
 //
 // Filter-stationary.  Each wave keeps the whole 64-channel filter of the workgroup in
 // registers: KB = R*S*Cg/64 K-blocks x 4 MFMA row blocks of 16 bytes per lane.  The only
@@ -37,8 +42,9 @@
 // wave's VALU work runs beside the other's matrix instructions.
 //
 // Epilogue.  Accumulators start at the bias; the output is convert, scale, clamp, round
-// (the 1.5*2^23 addition) and one 16-byte store of 16 consecutive channels per lane, the
-// arithmetic of the other int8 kernels.
+// (the 1.5*2^23 addition; with ReLU, v_cvt_pk_u8_f32 rounds to nearest even and packs) and
+// one 16-byte store of 16 consecutive channels per lane, the arithmetic of the other int8
+// kernels.  Every 16-byte store is followed by store_gap() on its data registers.
 
 #include "qconv_device.h"
 
