@@ -40,14 +40,17 @@ typedef enum miq_status {
 
 /* Kernel families of the int8 entry points (miq_qconv_desc.algo). */
 typedef enum miq_algo {
-  MIQ_ALGO_AUTO = 0,   /* pick by shape: band kernel, else implicit GEMM, else stem kernel for thin C,
-                          else direct */
+  MIQ_ALGO_AUTO = 0,   /* pick by shape: band kernel, else stream kernel, else implicit GEMM, else stem
+                          kernel for thin C, else direct */
   MIQ_ALGO_DIRECT = 1, /* VALU direct convolution: any shape, bandwidth-bound fallback */
   MIQ_ALGO_IGEMM = 2,  /* int8 MFMA implicit GEMM: needs (c/groups) % 16 == 0, 16-byte aligned tensors */
   MIQ_ALGO_STEM = 3,   /* int8 MFMA thin-channel kernel: c/groups < 16, groups == 1 */
   MIQ_ALGO_BAND = 4    /* int8 MFMA row-band kernel with the filter held in registers: needs
                           (c/groups) % 64 == 0, (k/groups) % 16 == 0, stride_w == 1, output width
-                          <= 64, r*s*c/groups <= 576, 16-byte aligned tensors, bias and scales */
+                          <= 64, r*s*c/groups <= 576, 16-byte aligned tensors, bias and scales */,
+  MIQ_ALGO_STREAM = 5  /* int8 MFMA row-band kernel with the filter streamed through LDS: needs
+                          (c/groups) % 64 == 0, (k/groups) % 128 == 0, stride_w <= 4, input rows of a
+                          band that fit in LDS, 16-byte aligned tensors, bias and scales */
 } miq_algo;
 
 /* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */

@@ -29,8 +29,9 @@ MIQ_ALGO_DIRECT = 1
 MIQ_ALGO_IGEMM = 2
 MIQ_ALGO_STEM = 3
 MIQ_ALGO_BAND = 4
+MIQ_ALGO_STREAM = 5
 ALGOS = {"auto": MIQ_ALGO_AUTO, "direct": MIQ_ALGO_DIRECT, "igemm": MIQ_ALGO_IGEMM, "stem": MIQ_ALGO_STEM,
-         "band": MIQ_ALGO_BAND}
+         "band": MIQ_ALGO_BAND, "stream": MIQ_ALGO_STREAM}
 ALGO_NAMES = {v: k for k, v in ALGOS.items()}
 
 

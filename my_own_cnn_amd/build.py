@@ -29,6 +29,7 @@ SOURCES = [
     "qconv_igemm.hip",
     "qconv_stem.hip",
     "qconv_band.hip",
+    "qconv_stream.hip",
     "conv_quant_host.cpp",
     "verify.cpp",
     "bench.cpp",

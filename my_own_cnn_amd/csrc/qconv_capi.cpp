@@ -108,6 +108,8 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
     case MIQ_ALGO_AUTO:
       if (miq::band_eligible(*g, x, w, y, rq, epi, nullptr)) {
         *algo = MIQ_ALGO_BAND;
+      } else if (miq::stream_eligible(*g, x, w, y, rq, epi, nullptr)) {
+        *algo = MIQ_ALGO_STREAM;
       } else if (miq::igemm_eligible(*g, x, w, y, epi, nullptr)) {
         *algo = MIQ_ALGO_IGEMM;
       } else if (miq::stem_eligible(*g, x, w, y, epi, nullptr)) {
@@ -130,6 +132,10 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
     case MIQ_ALGO_BAND:
       if (!miq::band_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       *algo = MIQ_ALGO_BAND;
+      break;
+    case MIQ_ALGO_STREAM:
+      if (!miq::stream_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_STREAM;
       break;
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
@@ -160,6 +166,7 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
     case MIQ_ALGO_IGEMM: e = miq::launch_i8_igemm(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_STEM: e = miq::launch_i8_stem(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_BAND: e = miq::launch_i8_band(g, epi, x, w, y, rq, s); break;
+    case MIQ_ALGO_STREAM: e = miq::launch_i8_stream(g, epi, x, w, y, rq, s); break;
     default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");

@@ -83,6 +83,13 @@ bool band_eligible(const Geom& g, const void* x, const void* w, const void* y, c
 hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
 
+// int8 MFMA kernel with the filter streamed through LDS: (C/groups) % 64 == 0,
+// (K/groups) % 128 == 0, stride_w <= 4.
+bool stream_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                     std::string* why);
+hipError_t launch_i8_stream(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                            hipStream_t stream);
+
 // int8 MFMA thin-channel kernel for stems: groups == 1, C < 16.
 bool stem_eligible(const Geom& g, const void* x, const void* w, const void* y, Epi epi, std::string* why);
 hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,

@@ -169,7 +169,7 @@ def test_python_mirror_errors():
 
 
 @pytest.mark.parametrize("name,algo", [("tiny", "igemm"), ("r50_3x3", "band"), ("r50_1x1", "band"),
-                                       ("down_s2", "igemm"), ("stem", "stem")])
+                                       ("down_s2", "stream"), ("stem", "stem")])
 def test_plan_of_the_workloads(name, algo):
     wl = M.WORKLOADS[name]
     d = M.make_desc((wl.n, wl.h, wl.w, wl.c), (wl.k, wl.r, wl.s, wl.c), stride=wl.stride, padding=wl.pad,
