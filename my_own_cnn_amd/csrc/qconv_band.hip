@@ -59,6 +59,10 @@ constexpr int kBandWaves = 8;  // two per SIMD: one wave's LDS reads and epilogu
 constexpr int kBandMaxKB = 9;  // filter registers per lane: 16 * KB
 constexpr int kBandLds = 160 * 1024;
 
+// LDS of one 64-channel tile's filter, in 16-byte slots: 4 * KB kilobytes, plus one for the
+// block shifts of the contiguous (odd KB) layout
+__host__ __device__ constexpr int band_tile_slots(int KB) { return 64 * (4 * KB + (KB & 1)); }
+
 struct BandArgs {
   const int8_t* x;
   const int8_t* w;
@@ -129,18 +133,36 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   // turn), so the loads below use one buffer resource each and keep per-load work to a
   // few instructions.
   //
-  // ---- filter -> LDS.  Fragment f = 4KB*t + 4b + j (64-channel tile t, K-block b, MFMA
-  // row block j) goes to wave f % 8.  Its lane (row_l, grp_l) holds channel
+  // ---- filter -> LDS, instruction f to wave f % 8.  Even KB: fragment order; fragment
+  // f = 4KB*t + 4b + j (64-channel tile t, K-block b, MFMA row block j) is one
+  // instruction, whose lane (row_l, grp_l) holds channel
   // k0 + 64t + 16*(row_l/4) + 4j + row_l%4, bytes [16*(4b + grp_l), +16) of that channel's
   // KRSC row; channels at or beyond Kg lie past num_records (zeros).
+  //
+  // Odd KB: the tile's 64 KRSC rows (64 * Kdim = 4 * KB kilobytes) are one contiguous
+  // range, loaded as it lies, 1 KB per instruction (the fastest global -> LDS form).  A
+  // block of 16 channels is KB instructions; blocks 2 and 3 land 2 slots (32 bytes)
+  // further on.  A ds_read_b128 serves 16 lanes per cycle: one half-wave's lane quads of
+  // equal quad-index parity.  A fragment read then gives each cycle the slots
+  // 4 * (KB * a mod 4) + grp_l + 2 * (m / 2) + const modulo 16 for channels 16m + 4j + a,
+  // all distinct: no bank conflicts.
   {
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + static_cast<size_t>(gi) * a.Kg * a.Kdim, a.Kg * a.Kdim);
-    const unsigned lane_row = static_cast<unsigned>((16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
-    for (int f = wave; f < NT * 4 * KB; f += kBandWaves) {
-      const int t = MT ? f / (4 * KB) : 0;
-      const int ff = f - t * (4 * KB);
-      load_lds16(rw, filt + f * 64, lane_row,
-                 static_cast<unsigned>((k0 + 64 * t + 4 * (ff & 3)) * a.Kdim + 64 * (ff >> 2)));
+    if constexpr (KB & 1) {
+      for (int f = wave; f < NT * 4 * KB; f += kBandWaves) {
+        const int t = MT ? f / (4 * KB) : 0;
+        const int u = f - t * (4 * KB);
+        load_lds16(rw, filt + t * band_tile_slots(KB) + 64 * u + 2 * ((u / KB) >> 1), 16u * lane,
+                   static_cast<unsigned>((k0 + 64 * t) * a.Kdim + 1024 * u));
+      }
+    } else {
+      const unsigned lane_row = static_cast<unsigned>((16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
+      for (int f = wave; f < NT * 4 * KB; f += kBandWaves) {
+        const int t = MT ? f / (4 * KB) : 0;
+        const int ff = f - t * (4 * KB);
+        load_lds16(rw, filt + f * 64, lane_row,
+                   static_cast<unsigned>((k0 + 64 * t + 4 * (ff & 3)) * a.Kdim + 64 * (ff >> 2)));
+      }
     }
   }
   // ---- bias and per-channel scales of tile t's 64 channels (wave t), 2 KB of LDS each ----
@@ -183,10 +205,21 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   barrier_only();
 
   v4i A[KB][4];
+  if constexpr (KB & 1) {
+    // lane (row_l, grp_l) of fragment (b, j): channel n = 16 * (row_l / 4) + 4j + row_l % 4
+    // of the tile, 16-byte unit 4 * KB * n + 4b + grp_l, plus its block's shift
+    const v4i* ft = filt + tw * band_tile_slots(KB) + 4 * KB * (16 * (row_l >> 2) + (row_l & 3)) + grp_l +
+                    2 * (row_l >> 3);
 #pragma unroll
-  for (int b = 0; b < KB; ++b)
+    for (int b = 0; b < KB; ++b)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) A[b][j] = filt[(tw * 4 * KB + b * 4 + j) * 64 + lane];
+      for (int j = 0; j < 4; ++j) A[b][j] = ft[16 * KB * j + 4 * b];
+  } else {
+#pragma unroll
+    for (int b = 0; b < KB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) A[b][j] = filt[(tw * 4 * KB + b * 4 + j) * 64 + lane];
+  }
   // epilogue parameters of this lane's 16 channels kc0 + 4j + r (zero past Kg)
   const int kc0 = k0 + 64 * tw + 16 * grp_l;
   const bool ch_ok = kc0 < a.Kg;  // Kg % 16 == 0: a lane's 16 channels all exist or none does
@@ -387,7 +420,7 @@ bool band_plan(const Geom& g, Epi epi, BandPlan* p, std::string* why) {
   for (int nt = 1; nt <= kBandWaves; nt *= 2) {
     if (kt64 % nt != 0) continue;
     const int wpt = kBandWaves / nt;
-    const size_t filt_bytes = static_cast<size_t>(nt) * p->KB * 4 * 1024;
+    const size_t filt_bytes = static_cast<size_t>(nt) * band_tile_slots(p->KB) * 16;
     for (int bh = 1; bh <= g.Ho; ++bh) {
       const long long hr = static_cast<long long>(bh - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
       const long long ni = hr * p->NQ * p->NPB;
