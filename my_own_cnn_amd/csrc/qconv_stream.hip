@@ -23,11 +23,12 @@
 // Filter.  K-block b (tap b / NQ, chunk quad b % NQ; NQ = Cg / 64) of the workgroup's KT
 // channels is 4 * WK fragments of 1 KB (64-channel tile t, MFMA row block j; lane l's 16
 // bytes at l * 16), one load instruction each.  K-blocks stream through a ring of D
-// buffers: D - 1 are in flight while one is computed.  Before K-block b a wave waits for
-// its own loads of b (loads complete in order and no store is issued before the
-// epilogue, so the count is exact) and a barrier publishes every wave's; the same barrier
-// shows that every wave is done with K-block b - 1, whose buffer then receives K-block
-// b + D - 1.
+// buffers.  The K-loop is software-pipelined: while the MFMAs of K-block b run from
+// registers, the fragments of K-block b + 1 are read from LDS.  Before those reads a wave
+// waits for its own loads of b + 1 (loads complete in order and no store is issued before
+// the epilogue, so the count is exact) and a barrier publishes every wave's; the same
+// barrier shows that every wave has read K-block b into its registers, so b's buffer then
+// receives K-block b + D.
 //
 // Output channels are permuted as in the other MFMA kernels (MFMA j row rho <-> channel
 // 16 * (rho / 4) + 4j + rho % 4), so each lane holds 16 consecutive channels of one pixel.
@@ -167,7 +168,7 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
       load_lds16(rw, buf + f * 64, lane_row, static_cast<unsigned>((kwg0 + 64 * t + 4 * j) * a.Kdim + 64 * b));
     }
   };
-  const int pre = min(a.D - 1, a.KB);
+  const int pre = min(a.D, a.KB);
   for (int b = 0; b < pre; ++b) issue_filter(b);
 
   // per segment i of this wave: packed pixel p = 16 * (wp + i * WP) + row_l of the band,
@@ -191,17 +192,18 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   const unsigned halo_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(halo) & 0xffffffffu);
   const unsigned ring_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(ring) & 0xffffffffu);
 
-  // loads of K-block b (and everything issued before it) are in on every wave; the
-  // barrier also ends every wave's reads of K-block b - 1
-  auto sync_kblock = [&](int b) {
-    const int later = (min(b + a.D - 2, a.KB - 1) - b) * LPW;
+  // loads of K-block c (and everything issued before it) are in on every wave, given the
+  // K-blocks issued so far (0 .. issued_hi); the barrier also ends every wave's reads of
+  // the K-block before c
+  auto sync_kblock = [&](int c, int issued_hi) {
+    const int later = (min(issued_hi, a.KB - 1) - c) * LPW;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     wait_vmcnt(later);
     barrier_only();
   };
 
   // epilogue parameters of this lane's 16 channels kc0 + 4j + r
-  sync_kblock(0);
+  sync_kblock(0, pre - 1);
   v4i bias_v[4];
   v4f mult_v[4];
 #pragma unroll
@@ -216,8 +218,9 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
     }
   }
 
-  // K-loop over taps (r, s) and chunk quads q; K-block b = (r * S + s) * NQ + q.  NS = the
-  // wave's segment count (0 .. 4): a wave without segments still loads and synchronises.
+  // K-loop over K-blocks b = (r * S + s) * NQ + q (taps (r, s), chunk quads q), two per
+  // pass so the fragment registers alternate without copies.  NS = the wave's segment
+  // count (0 .. 4): a wave without segments still loads and synchronises.
   v4i acc[4][kStreamNseg];
   auto kloop = [&](auto ns_tag) {
     constexpr int NS = decltype(ns_tag)::value;
@@ -225,42 +228,67 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < kStreamNseg; ++i) acc[j][i] = bias_v[j];
-    int b = 0;
-    int tap_row = 0;  // r * dh * RowS
-    int s = 0;
-    while (b < a.KB) {
-      // this tap's parity plane and shift, and each segment's slot (quad 0) for it
+    // tap and quad of the K-block whose fragments are read next, and each segment's slot
+    // (quad 0) for that tap
+    int q = 0, s = 0, tap_row = 0;  // tap_row = r * dh * RowS
+    unsigned baddr[kStreamNseg > 0 ? kStreamNseg : 1];
+    auto tap_addrs = [&]() {
       const int sdw = s * a.dw;
       const int sft = fdiv(sdw, a.fd_sw);
       const int par = sdw - sft * a.sw;
-      unsigned baddr[kStreamNseg];
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
         const int x = lwo[i] + sft;
         baddr[i] = halo_addr + 16u * static_cast<unsigned>(rbase[i] + tap_row + par * a.NPB * 64 + x + 48 * (x >> 4) +
                                                            16 * grp_l);
       }
-      for (int q = 0; q < a.NQ; ++q, ++b) {
-        if (b > 0) sync_kblock(b);
-        if (b + a.D - 1 < a.KB) issue_filter(b + a.D - 1);
-        if constexpr (NS > 0) {
-          const unsigned aaddr = ring_addr + 16u * static_cast<unsigned>((b % a.D) * (4 * WK * 64) + (4 * wk) * 64 + lane);
-          const unsigned qoff = 16u * static_cast<unsigned>(q * a.sw * a.NPB * 64);
-          v4i A[4], B[NS];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) A[j] = lds_read16(aaddr + 1024u * j);
-#pragma unroll
-          for (int i = 0; i < NS; ++i) B[i] = lds_read16(baddr[i] + qoff);
-#pragma unroll
-          for (int i = 0; i < NS; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j], B[i], acc[j][i], 0, 0, 0);
+    };
+    auto advance = [&]() {
+      if (++q == a.NQ) {
+        q = 0;
+        if (++s == a.S) {
+          s = 0;
+          tap_row += a.dh * a.RowS;
         }
+        tap_addrs();
       }
-      if (++s == a.S) {
-        s = 0;
-        tap_row += a.dh * a.RowS;
+    };
+    auto read_frags = [&](int b, v4i (&A)[4], v4i (&B)[NS > 0 ? NS : 1]) {
+      if constexpr (NS > 0) {
+        const unsigned aaddr = ring_addr + 16u * static_cast<unsigned>((b % a.D) * (4 * WK * 64) + (4 * wk) * 64 + lane);
+        const unsigned qoff = 16u * static_cast<unsigned>(q * a.sw * a.NPB * 64);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) A[j] = lds_read16(aaddr + 1024u * j);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) B[i] = lds_read16(baddr[i] + qoff);
       }
+    };
+    auto mma = [&](const v4i (&A)[4], const v4i (&B)[NS > 0 ? NS : 1]) {
+      if constexpr (NS > 0) {
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j], B[i], acc[j][i], 0, 0, 0);
+      }
+    };
+    // step b: K-block b's fragments are in registers; publish b + 1, refill b's buffer
+    // with b + D, read b + 1's fragments, then run b's MFMAs
+    auto next = [&](int b, v4i (&A)[4], v4i (&B)[NS > 0 ? NS : 1]) {
+      sync_kblock(b + 1, b + a.D - 1);
+      if (b + a.D < a.KB) issue_filter(b + a.D);
+      read_frags(b + 1, A, B);
+      advance();
+    };
+    v4i A0[4], A1[4], B0[NS > 0 ? NS : 1], B1[NS > 0 ? NS : 1];
+    tap_addrs();
+    read_frags(0, A0, B0);
+    advance();
+    for (int b = 0; b < a.KB; b += 2) {
+      if (b + 1 < a.KB) next(b, A1, B1);
+      mma(A0, B0);
+      if (b + 1 >= a.KB) break;
+      if (b + 2 < a.KB) next(b + 1, A0, B0);
+      mma(A1, B1);
     }
   };
   dispatch_count_z<kStreamNseg>(nsv, kloop);
