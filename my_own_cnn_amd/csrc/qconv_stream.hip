@@ -48,7 +48,7 @@ namespace {
 constexpr int kStreamWaves = 8;
 constexpr int kStreamNseg = 4;  // segments per wave at most
 constexpr int kStreamLds = 160 * 1024;
-constexpr int kStreamMaxRing = 6;
+constexpr int kStreamMaxRing = 6;  // ring depths 3 .. 6 are instantiated
 
 struct StreamArgs {
   const int8_t* x;
@@ -65,7 +65,7 @@ struct StreamArgs {
   int nblocks;        // workgroups of the launch
   int NQ, NPB;        // chunk quads per tap (Cg / 64), 16-column blocks per parity plane
   int RowS;           // LDS slots (16 bytes) per input row, padded
-  int KB, D;          // K-blocks, ring buffers
+  int KB;             // K-blocks
   int ni;             // input load instructions per workgroup: HR * NQ * sw * NPB
   int ring_lds, ep_lds, halo_lds;  // LDS byte offsets
   float act_scale;
@@ -91,7 +91,15 @@ __device__ __forceinline__ void dispatch_count_z(int n, F&& f) {
   }
 }
 
-template <int WK, int EPI>
+// s_waitcnt vmcnt(n) lgkmcnt(0), n <= 15, as the builtin: the compiler's own wait
+// insertion then knows that every LDS read issued before it has completed.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N <= 15, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x70 | N);
+}
+
+template <int WK, int EPI, int D>
 __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamArgs a_in) {
   const StreamArgs a = preload_args(a_in);
   constexpr int WP = kStreamWaves / WK;  // waves per 64-channel tile
@@ -158,8 +166,8 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   // row bytes tap * Cg + 64q = 64b).
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + static_cast<size_t>(gi) * a.Kg * a.Kdim, a.Kg * a.Kdim);
   const unsigned lane_row = static_cast<unsigned>((16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
-  auto issue_filter = [&](int b) {
-    v4i* buf = ring + (b % a.D) * (4 * WK * 64);
+  auto issue_filter = [&](int b, int slot) {  // K-block b into ring buffer `slot`
+    v4i* buf = ring + slot * (4 * WK * 64);
 #pragma unroll
     for (int u = 0; u < LPW; ++u) {
       const int f = wave + kStreamWaves * u;
@@ -168,8 +176,8 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
       load_lds16(rw, buf + f * 64, lane_row, static_cast<unsigned>((kwg0 + 64 * t + 4 * j) * a.Kdim + 64 * b));
     }
   };
-  const int pre = min(a.D, a.KB);
-  for (int b = 0; b < pre; ++b) issue_filter(b);
+  const int pre = min(D, a.KB);
+  for (int b = 0; b < pre; ++b) issue_filter(b, b);
 
   // per segment i of this wave: packed pixel p = 16 * (wp + i * WP) + row_l of the band,
   // output row lho = p / Wo, column lwo = p % Wo; pixels outside the band read row 0 /
@@ -192,18 +200,18 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   const unsigned halo_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(halo) & 0xffffffffu);
   const unsigned ring_addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(ring) & 0xffffffffu);
 
-  // loads of K-block c (and everything issued before it) are in on every wave, given the
-  // K-blocks issued so far (0 .. issued_hi); the barrier also ends every wave's reads of
-  // the K-block before c
-  auto sync_kblock = [&](int c, int issued_hi) {
-    const int later = (min(issued_hi, a.KB - 1) - c) * LPW;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    wait_vmcnt(later);
-    barrier_only();
-  };
+  // Loads of K-block c (and everything issued before it) are in on every wave; the
+  // barrier also ends every wave's reads of the K-block before c.  In steady state this
+  // wave's loads issued after c's are those of the next D - 2 K-blocks (D - 1 after the
+  // prologue); near the end fewer are, and the wait takes all (they are old by then).
+  if (a.KB >= D) {
+    wait_vm_lgkm0<(D - 1) * LPW>();
+  } else {
+    wait_vm_lgkm0<0>();
+  }
+  barrier_only();
 
   // epilogue parameters of this lane's 16 channels kc0 + 4j + r
-  sync_kblock(0, pre - 1);
   v4i bias_v[4];
   v4f mult_v[4];
 #pragma unroll
@@ -253,9 +261,9 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
         tap_addrs();
       }
     };
-    auto read_frags = [&](int b, v4i (&A)[4], v4i (&B)[NS > 0 ? NS : 1]) {
+    auto read_frags = [&](int rslot, v4i (&A)[4], v4i (&B)[NS > 0 ? NS : 1]) {  // from ring buffer rslot
       if constexpr (NS > 0) {
-        const unsigned aaddr = ring_addr + 16u * static_cast<unsigned>((b % a.D) * (4 * WK * 64) + (4 * wk) * 64 + lane);
+        const unsigned aaddr = ring_addr + 16u * static_cast<unsigned>(rslot * (4 * WK * 64) + (4 * wk) * 64 + lane);
         const unsigned qoff = 16u * static_cast<unsigned>(q * a.sw * a.NPB * 64);
 #pragma unroll
         for (int j = 0; j < 4; ++j) A[j] = lds_read16(aaddr + 1024u * j);
@@ -272,23 +280,39 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
       }
     };
     // step b: K-block b's fragments are in registers; publish b + 1, refill b's buffer
-    // with b + D, read b + 1's fragments, then run b's MFMAs
+    // (slot) with b + D, read b + 1's fragments, then run b's MFMAs
+    int slot = 0;  // ring buffer of K-block b: b % D
     auto next = [&](int b, v4i (&A)[4], v4i (&B)[NS > 0 ? NS : 1]) {
-      sync_kblock(b + 1, b + a.D - 1);
-      if (b + a.D < a.KB) issue_filter(b + a.D);
-      read_frags(b + 1, A, B);
+      if (b + D <= a.KB) {
+        wait_vm_lgkm0<(D - 2) * LPW>();
+      } else {
+        wait_vm_lgkm0<0>();
+      }
+      barrier_only();
+      if (b + D < a.KB) issue_filter(b + D, slot);
+      slot = slot + 1 == D ? 0 : slot + 1;
+      read_frags(slot, A, B);
       advance();
     };
     v4i A0[4], A1[4], B0[NS > 0 ? NS : 1], B1[NS > 0 ? NS : 1];
     tap_addrs();
     read_frags(0, A0, B0);
     advance();
-    for (int b = 0; b < a.KB; b += 2) {
-      if (b + 1 < a.KB) next(b, A1, B1);
+    // both steps of a pass unconditional, so the compiler sees no path on which the
+    // fragments about to be multiplied are still being read
+    int b = 0;
+    for (; b + 2 < a.KB; b += 2) {
+      next(b, A1, B1);
       mma(A0, B0);
-      if (b + 1 >= a.KB) break;
-      if (b + 2 < a.KB) next(b + 1, A0, B0);
+      next(b + 1, A0, B0);
       mma(A1, B1);
+    }
+    if (b + 1 < a.KB) {
+      next(b, A1, B1);
+      mma(A0, B0);
+      mma(A1, B1);
+    } else {
+      mma(A0, B0);
     }
   };
   dispatch_count_z<kStreamNseg>(nsv, kloop);
@@ -420,7 +444,7 @@ bool stream_plan(const Geom& g, Epi epi, StreamPlan* p, std::string* why) {
   return true;
 }
 
-template <int WK>
+template <int WK, int D>
 void stream_launch(const StreamArgs& a, const StreamPlan& pl, Epi epi, unsigned nblocks, hipStream_t stream) {
   auto go = [&](auto kern) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -428,9 +452,19 @@ void stream_launch(const StreamArgs& a, const StreamPlan& pl, Epi epi, unsigned 
     hipLaunchKernelGGL(kern, dim3(nblocks), dim3(64 * kStreamWaves), pl.lds_bytes, stream, a);
   };
   switch (epi) {
-    case kEpiI8: go(i8_stream_kernel<WK, kEpiI8>); break;
-    case kEpiAcc32: go(i8_stream_kernel<WK, kEpiAcc32>); break;
-    default: go(i8_stream_kernel<WK, kEpiF32>); break;
+    case kEpiI8: go(i8_stream_kernel<WK, kEpiI8, D>); break;
+    case kEpiAcc32: go(i8_stream_kernel<WK, kEpiAcc32, D>); break;
+    default: go(i8_stream_kernel<WK, kEpiF32, D>); break;
+  }
+}
+
+template <int WK>
+void stream_launch_d(const StreamArgs& a, const StreamPlan& pl, Epi epi, unsigned nblocks, hipStream_t stream) {
+  switch (pl.D) {
+    case 3: stream_launch<WK, 3>(a, pl, epi, nblocks, stream); break;
+    case 4: stream_launch<WK, 4>(a, pl, epi, nblocks, stream); break;
+    case 5: stream_launch<WK, 5>(a, pl, epi, nblocks, stream); break;
+    default: stream_launch<WK, 6>(a, pl, epi, nblocks, stream); break;
   }
 }
 
@@ -460,7 +494,7 @@ hipError_t launch_i8_stream(const Geom& g, Epi epi, const int8_t* x, const int8_
   a.ph = g.ph; a.pw = g.pw; a.sh = g.sh; a.sw = g.sw; a.dh = g.dh; a.dw = g.dw;
   a.S = g.S; a.Cg = g.Cg; a.Kg = g.Kg; a.Kdim = g.R * g.S * g.Cg;
   a.RB = pl.RB; a.bands_per_img = pl.bands_per_img; a.kt_per_group = pl.kt_per_group;
-  a.NQ = pl.NQ; a.NPB = pl.NPB; a.RowS = pl.RowS; a.KB = pl.KB; a.D = pl.D; a.ni = pl.ni;
+  a.NQ = pl.NQ; a.NPB = pl.NPB; a.RowS = pl.RowS; a.KB = pl.KB; a.ni = pl.ni;
   a.ring_lds = pl.ring_lds; a.ep_lds = pl.ep_lds; a.halo_lds = pl.halo_lds;
   a.act_scale = rq.act_scale; a.relu = rq.relu;
   a.ntiles = g.G * pl.kt_per_group;
@@ -474,9 +508,9 @@ hipError_t launch_i8_stream(const Geom& g, Epi epi, const int8_t* x, const int8_
   const long long nblocks = static_cast<long long>(g.N) * pl.bands_per_img * g.G * pl.kt_per_group;
   a.nblocks = static_cast<int>(nblocks);
   if (pl.WK == 4) {
-    stream_launch<4>(a, pl, epi, static_cast<unsigned>(nblocks), stream);
+    stream_launch_d<4>(a, pl, epi, static_cast<unsigned>(nblocks), stream);
   } else {
-    stream_launch<2>(a, pl, epi, static_cast<unsigned>(nblocks), stream);
+    stream_launch_d<2>(a, pl, epi, static_cast<unsigned>(nblocks), stream);
   }
   return hipGetLastError();
 }
