@@ -194,11 +194,25 @@ def main():
         ms = t0.elapsed_time(t1) / args.steps
         tops = wl.ops / (ms * 1e-3) / 1e12
         gbs = wl.bytes / (ms * 1e-3) / 1e9
+        # reference-style per-launch timing (src/bench.cpp:27-43): one event pair around each of
+        # up to 200 eager launches, median and the floor(0.9 * (n - 1))-th sample; reported
+        # beside the back-to-back figure, never as `value`
+        nper = min(args.steps, 200)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nper)]
+        for i, (ea, eb) in enumerate(evs):
+            ea.record(stream)
+            step(i)
+            eb.record(stream)
+        torch.cuda.synchronize()
+        per = sorted(ea.elapsed_time(eb) for ea, eb in evs)
+        per_launch = {"median_us": round(per[len(per) // 2] * 1e3, 3),
+                      "p90_us": round(per[int(0.9 * (len(per) - 1))] * 1e3, 3), "launches": nper,
+                      "timing": "eager, one event pair per launch"}
         t_mfma = wl.ops / (PEAK_INT8_TOPS * 1e12)
         t_hbm = wl.bytes / (PEAK_HBM_GBS * 1e9)
         bound = "mfma" if t_mfma >= t_hbm else "hbm"
         results[name] = dict(ms=ms, tops=tops, gbs=gbs, bound=bound, verified=verified, algo=algo, mode=mode,
-                             nsets=nsets, wall=wall, wl=wl)
+                             nsets=nsets, wall=wall, wl=wl, per_launch=per_launch)
         del xs, ys, graph
         torch.cuda.empty_cache()
 
@@ -240,16 +254,18 @@ def main():
         "gbs": round(head["gbs"], 2),
         "verified_bit_exact": head["verified"],
         "roofline": roof,
+        "per_launch": head["per_launch"],
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(wl)
     if args.all:
-        print(f"{'config':10s} {'kernel':7s} {'us':>9s} {'TOPS':>8s} {'GB/s':>8s} {'bound':5s} {'frac':>6s} exact",
-              file=sys.stderr)
+        print(f"{'config':10s} {'kernel':7s} {'us':>9s} {'TOPS':>8s} {'GB/s':>8s} {'bound':5s} {'frac':>6s} exact"
+              f" {'med us':>7s} {'p90 us':>7s}", file=sys.stderr)
         for name, r in results.items():
             frac = r["tops"] / PEAK_INT8_TOPS if r["bound"] == "mfma" else r["gbs"] / PEAK_HBM_GBS
             print(f"{name:10s} {r['algo']:7s} {r['ms'] * 1e3:9.2f} {r['tops']:8.1f} {r['gbs']:8.1f} {r['bound']:5s} "
-                  f"{frac:6.3f} {r['verified']}", file=sys.stderr)
+                  f"{frac:6.3f} {str(r['verified']):5s} {r['per_launch']['median_us']:7.2f} {r['per_launch']['p90_us']:7.2f}",
+                  file=sys.stderr)
     print(json.dumps(line), flush=True)
     os.sys.stdout.flush()
 
