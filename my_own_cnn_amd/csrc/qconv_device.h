@@ -9,10 +9,11 @@ namespace miq {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Cache policy of the row-band kernels' output stores: non-temporal (nt), so the next
-// kernel does not have to write this one's output back from L2 before its own loads
-// (measured: ~5% per launch).
-constexpr int kStoreAux = 2;
+// Cache policy of the int8 kernels' output stores: non-temporal (nt) with system-scope
+// write-through (sc0 | sc1), so the next kernel does not have to write this one's output
+// back from L2 before its own loads.  Measured against nt alone: 3-5% per launch on the
+// row-band kernels (r50_3x3 7.05 -> 6.8 us); plain write-back stores are 10-20% slower.
+constexpr int kStoreAux = 19;  // sc0 (1) | nt (2) | sc1 (16)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
