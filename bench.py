@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--algo", default="auto")
     ap.add_argument("--all", action="store_true", help="also print a per-config table on stderr")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--bmm", action="store_true",
+                    help="measure the int32 batched matrix product (bmm_matmul_i32) instead of the convolution")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -66,6 +68,108 @@ def copy_calibration(mib: int) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": n, "launches": 3}), flush=True)
+
+
+# int32 products: (name, batch, M, N, K, trans_a, trans_b).  The first is the reference's own
+# call site on the headline layer (cuda_kernels.cu:1381: im2col columns of ResNet-50 conv2_x,
+# N=32, times the packed 64 x 576 filter, trans_b); the rest are plain square and batched
+# products.
+BMM_SHAPES = [
+    ("r50_3x3_im2col", 1, 32 * 56 * 56, 64, 576, False, True),
+    ("square_4096", 1, 4096, 4096, 4096, False, False),
+    ("batched_512", 32, 512, 512, 512, False, False),
+    ("square_4096_tt", 1, 4096, 4096, 4096, True, True),
+]
+BMM_BYTE_PRODUCTS = 16  # int8 MFMA products per int32 multiply-add (4 shift groups x 4 digit bytes)
+
+
+def bench_bmm(args) -> None:
+    """Times bmm_matmul_i32 per shape (HIP events over back-to-back launches on one stream),
+    checks sampled rows against the oracle, prints a table on stderr and one JSON line."""
+    import numpy as np
+    import torch
+
+    import my_own_cnn_amd as M
+    import oracle  # checker of sampled output rows and the cpu_baseline leg only
+
+    dev = torch.device("cuda:0")
+    peak = PEAK_INT8_TOPS / BMM_BYTE_PRODUCTS  # int32 ops/s the int8 matrix cores can deliver
+    rows = []
+    for name, batch, m, n, k, ta, tb in BMM_SHAPES:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1234)
+        a = torch.randint(-2 ** 31, 2 ** 31 - 1, (batch, k, m) if ta else (batch, m, k), dtype=torch.int32,
+                          device=dev, generator=gen)
+        b = torch.randint(-2 ** 31, 2 ** 31 - 1, (batch, n, k) if tb else (batch, k, n), dtype=torch.int32,
+                          device=dev, generator=gen)
+        c = torch.empty((batch, m, n), dtype=torch.int32, device=dev)
+        stream = torch.cuda.current_stream()
+
+        def step():
+            M.bmm_matmul_i32(a, b, c, batch, m, n, k, ta, tb, stream=stream)
+
+        step()
+        torch.cuda.synchronize()
+        # exact check of 64 sampled output rows of the first and last batch entries
+        rng = np.random.default_rng(7)
+        pick = np.sort(rng.choice(m, size=min(m, 64), replace=False))
+        an, bn, cn = a.cpu().numpy(), b.cpu().numpy(), c.cpu().numpy()
+        ok = True
+        for bi in {0, batch - 1}:
+            asub = an[bi][:, pick] if ta else an[bi][pick]
+            want = oracle.bmm_i32(asub[None], bn[bi][None], ta, tb)[0]
+            ok &= bool(np.array_equal(cn[bi][pick], want))
+        for _ in range(args.warmup):
+            step()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(args.steps):
+            step()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        ops = 2.0 * batch * m * n * k
+        tops = ops / (ms * 1e-3) / 1e12
+        rows.append(dict(name=name, batch=batch, M=m, N=n, K=k, trans_a=ta, trans_b=tb, us=round(ms * 1e3, 3),
+                         tops=round(tops, 3), frac=round(tops / peak, 4), exact_sampled=ok))
+        del a, b, c
+        torch.cuda.empty_cache()
+    print(f"{'shape':16s} {'batch':>5s} {'M':>7s} {'N':>5s} {'K':>5s} {'tt':2s} {'us':>10s} {'TOPS':>8s} {'frac':>6s} exact",
+          file=sys.stderr)
+    for r in rows:
+        print(f"{r['name']:16s} {r['batch']:5d} {r['M']:7d} {r['N']:5d} {r['K']:5d} {int(r['trans_a'])}{int(r['trans_b'])} "
+              f"{r['us']:10.2f} {r['tops']:8.2f} {r['frac']:6.3f} {r['exact_sampled']}", file=sys.stderr)
+    head = rows[0]
+    line = {
+        "metric": "int32 bmm TOPS (wrap-around int32, 2 ops per multiply-add), reference call site on the "
+                  "ResNet-50 3x3 layer N=32",
+        "value": head["tops"], "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int32", "data": "synthetic",
+        "config": {"workload": head["name"], "batch": head["batch"], "M": head["M"], "N": head["N"], "K": head["K"],
+                   "trans_a": head["trans_a"], "trans_b": head["trans_b"], "timing": "eager back-to-back"},
+        "roofline": {"bound": "mfma", "achieved": head["tops"], "peak": peak, "unit": "TOPS",
+                     "frac": head["frac"], "traffic": None,
+                     "peak_note": f"int8 MFMA {PEAK_INT8_TOPS:.0f} TOPS / {BMM_BYTE_PRODUCTS} byte products per "
+                                  "int32 multiply-add"},
+        "shapes": rows,
+    }
+    if not args.no_cpu_baseline:
+        _, batch, m, n, k, ta, tb = BMM_SHAPES[0]
+        rng = np.random.default_rng(3)
+        msub = 2048
+        a = rng.integers(-2 ** 31, 2 ** 31, size=(1, msub, k), dtype=np.int64).astype(np.int32)
+        b = rng.integers(-2 ** 31, 2 ** 31, size=(1, n, k), dtype=np.int64).astype(np.int32)
+        t0 = time.perf_counter()
+        oracle.bmm_i32(a, b, False, True, nthreads=1)
+        secs = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": round(2.0 * msub * n * k / secs / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": f"{msub} of the {m} rows of {BMM_SHAPES[0][0]} ({2.0 * msub * n * k / 1e9:.2f} Gop) in "
+                      f"{secs:.2f} s; oracle/qconv_oracle.c orc_bmm_i32 (gcc -O3), 1 thread on {cpu_model()}",
+        }
+    print(json.dumps(line), flush=True)
 
 
 def cpu_model() -> str:
@@ -124,6 +228,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.bmm:
+        bench_bmm(args)
+        return
     dev = torch.device("cuda:0")
     names = [args.config or W.HEADLINE]
     if args.all:

@@ -184,6 +184,25 @@ int miq_qconv2d_nhwc_i8_acc32(const miq_qconv_desc* d, const int8_t* x, const in
 int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const int8_t* w,
                                 const int32_t* bias, const float* w_scale, float* y, void* stream);
 
+/* ---- int32 batched matrix product -------------------------------------------------- */
+/* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and
+ * sums, exact for every int32 input.  Row-major, batch strides M*K, K*N and M*N:
+ *   A[b] is M x K, or stored K x M when trans_a != 0;
+ *   B[b] is K x N, or stored N x K when trans_b != 0;
+ *   C[b] is M x N, fully overwritten (K == 0 writes zeros).
+ * Extents must be >= 0; batch, M or N == 0 enqueues nothing. */
+
+/* The stream-ordered, status-returning form of bmm_matmul_i32. */
+int miq_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N,
+                int32_t K, int32_t trans_a, int32_t trans_b, void* stream);
+
+/* Replaces bmm_matmul_i32 (/root/reference/bmm.cu:298-322, declared bmm.h:69-73): same
+ * symbol, arguments and meaning, on the default stream.  Like the reference it returns
+ * nothing; a rejected call enqueues nothing and leaves its reason in
+ * miq_last_error_message(). */
+void bmm_matmul_i32(const int32_t* A, const int32_t* B, int32_t* C, int batch, int M, int N, int K,
+                    int trans_a, int trans_b);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

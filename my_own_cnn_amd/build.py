@@ -30,6 +30,7 @@ SOURCES = [
     "qconv_stem.hip",
     "qconv_band.hip",
     "qconv_stream.hip",
+    "gemm_i32.hip",
     "conv_quant_host.cpp",
     "verify.cpp",
     "bench.cpp",

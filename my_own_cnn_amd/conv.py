@@ -222,7 +222,44 @@ def qconv2d_nhwc_i8_dequant(x, w, bias, w_scale, *, stride=1, padding=0, dilatio
     return y
 
 
+
+def bmm_matmul_i32(d_A: Pointer, d_B: Pointer, d_C: Pointer, batch: int, M: int, N: int, K: int, trans_a: int,
+                   trans_b: int, stream=None) -> None:
+    """bmm_matmul_i32 (/root/reference/bmm.cu:298-322) on device pointers: C[b] = op(A[b]) op(B[b])
+    with int32 wrap-around, A[b] M x K (stored K x M when trans_a), B[b] K x N (stored N x K
+    when trans_b).  Raises MiqError where the C symbol would record an error and return."""
+    check(lib().miq_bmm_i32(_addr(d_A), _addr(d_B), _addr(d_C), batch, M, N, K, 1 if trans_a else 0,
+                            1 if trans_b else 0, _stream(stream)), "bmm_matmul_i32")
+
+
+def bmm_i32(a, b, *, trans_a=False, trans_b=False, out=None, stream=None):
+    """int32 batched product of device tensors: a (batch, M, K), or (batch, K, M) when
+    trans_a; b (batch, K, N), or (batch, N, K) when trans_b; 2-D operands are one batch
+    entry.  Returns (batch, M, N) int32 (2-D when both operands were)."""
+    if a.dtype != torch.int32 or b.dtype != torch.int32:
+        raise ValueError("bmm_i32 operands must be int32")
+    two_d = a.dim() == 2 and b.dim() == 2
+    a3 = a.unsqueeze(0) if a.dim() == 2 else a
+    b3 = b.unsqueeze(0) if b.dim() == 2 else b
+    if a3.dim() != 3 or b3.dim() != 3 or a3.shape[0] != b3.shape[0]:
+        raise ValueError(f"bmm_i32 operands must be 3-D with equal batch, got {tuple(a.shape)} and {tuple(b.shape)}")
+    batch = a3.shape[0]
+    m, k = (a3.shape[2], a3.shape[1]) if trans_a else (a3.shape[1], a3.shape[2])
+    n, kb = (b3.shape[1], b3.shape[2]) if trans_b else (b3.shape[2], b3.shape[1])
+    if k != kb:
+        raise ValueError(f"bmm_i32 inner extents differ: {k} and {kb}")
+    shape = (batch, m, n)
+    if out is None:
+        y = torch.empty(shape, dtype=torch.int32, device=a.device)
+    else:
+        if tuple(out.shape) not in (shape, shape[1:]) or out.dtype != torch.int32:
+            raise ValueError(f"out must be int32 of shape {shape}")
+        y = out
+    bmm_matmul_i32(a3, b3, y, batch, m, n, k, trans_a, trans_b, stream)
+    return y[0] if two_d and out is None else y
+
 __all__ = [
+    "bmm_i32", "bmm_matmul_i32",
     "DataType", "Conv2DParams", "BlockConv2DParams", "QParamsU8", "QParamsS5", "QConvDesc", "MiqError",
     "qparams_array", "infer_conv_shape", "infer_block_conv_shape", "launch_fprop_nhwc_qi32",
     "launch_block_fprop_nhwc_qi32", "make_desc", "plan", "qconv2d_nhwc_i8", "qconv2d_nhwc_i8_acc32",

@@ -282,4 +282,28 @@ int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const 
   return i8_entry(miq::kEpiF32, d, x, w, bias, w_scale, y, stream);
 }
 
+int miq_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,
+                int32_t trans_a, int32_t trans_b, void* stream) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "bmm extents must be >= 0");
+  constexpr int32_t kMaxExtent = 0x7fffffff - 64;  // tile and chunk indices stay in int32
+  if (M > kMaxExtent || N > kMaxExtent || K > kMaxExtent) {
+    return fail(MIQ_ERR_UNSUPPORTED, "bmm extents must be <= 2^31 - 65");
+  }
+  if (batch == 0 || M == 0 || N == 0) return MIQ_OK;
+  if (C == nullptr) return fail(MIQ_ERR_NULL_POINTER, "bmm output pointer C is NULL");
+  if (K > 0 && A == nullptr) return fail(MIQ_ERR_NULL_POINTER, "bmm input pointer A is NULL");
+  if (K > 0 && B == nullptr) return fail(MIQ_ERR_NULL_POINTER, "bmm input pointer B is NULL");
+  const long long tiles = ((M + 127LL) / 128) * ((N + 63LL) / 64);
+  if (tiles > (1LL << 22)) return fail(MIQ_ERR_UNSUPPORTED, "bmm matrix has more than 2^22 128x64 output tiles");
+  const hipError_t e = miq::launch_i32_gemm(A, B, C, batch, M, N, K, trans_a != 0, trans_b != 0,
+                                            static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "int32 bmm launch");
+  return MIQ_OK;
+}
+
+void bmm_matmul_i32(const int32_t* A, const int32_t* B, int32_t* C, int batch, int M, int N, int K, int trans_a,
+                    int trans_b) {
+  (void)miq_bmm_i32(A, B, C, batch, M, N, K, trans_a, trans_b, nullptr);
+}
+
 }  // extern "C"

@@ -95,6 +95,11 @@ bool stem_eligible(const Geom& g, const void* x, const void* w, const void* y, E
 hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
 
+// int32 batched GEMM (wrap-around arithmetic) on the int8 matrix cores; extents already
+// validated (>= 0), pointers non-null where the extents need them.
+hipError_t launch_i32_gemm(const int32_t* A, const int32_t* B, int32_t* C, int batch, int M, int N, int K, bool ta,
+                           bool tb, hipStream_t stream);
+
 #if defined(__HIPCC__)
 __device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
   const uint32_t un = static_cast<uint32_t>(n);

@@ -48,6 +48,7 @@ def orc() -> C.CDLL:
         h.orc_conv_i8_acc.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
         h.orc_requant_i8.argtypes = [_P, C.c_int64, _I, _P, _P, C.c_float, C.c_float, _I, _P]
         h.orc_dequant_f32.argtypes = [_P, C.c_int64, _I, _P, _P, C.c_float, C.c_float, _I, _P]
+        h.orc_bmm_i32.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I]
         _orc = h
     return _orc
 
@@ -149,6 +150,22 @@ def conv_i8_acc(x: np.ndarray, wt: np.ndarray, conv, nthreads: int = 0) -> np.nd
     if orc().orc_conv_i8_acc(_p(x), n, h, w, c, _p(wt), r, s, k, _p(cv), _p(y), nthreads) != 0:
         raise ValueError("rejected shape")
     return y
+
+
+def bmm_i32(a: np.ndarray, b: np.ndarray, trans_a: bool = False, trans_b: bool = False,
+            nthreads: int = 0) -> np.ndarray:
+    """C[i] = op(a[i]) @ op(b[i]) with int32 wrap-around; a is (batch, M, K), or (batch, K, M)
+    stored when trans_a; b is (batch, K, N), or (batch, N, K) when trans_b."""
+    a = np.ascontiguousarray(a, np.int32)
+    b = np.ascontiguousarray(b, np.int32)
+    assert a.ndim == 3 and b.ndim == 3 and a.shape[0] == b.shape[0]
+    batch = a.shape[0]
+    m, k = (a.shape[2], a.shape[1]) if trans_a else (a.shape[1], a.shape[2])
+    n, kb = (b.shape[1], b.shape[2]) if trans_b else (b.shape[2], b.shape[1])
+    assert k == kb, (a.shape, b.shape)
+    c = np.empty((batch, m, n), np.int32)
+    orc().orc_bmm_i32(_p(a), _p(b), _p(c), batch, m, n, k, int(bool(trans_a)), int(bool(trans_b)), nthreads)
+    return c
 
 
 def requant_i8(acc: np.ndarray, bias, w_scale, in_scale, out_scale, relu) -> np.ndarray:

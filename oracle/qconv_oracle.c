@@ -12,6 +12,11 @@
  *   orc_requant_i8 /     no reference counterpart (the reference has no requantization):
  *   orc_dequant_f32      hand-computed known answers and float64 bounds.
  *   orc_fill_*           fixed known outputs of splitmix64.
+ *   orc_bmm_i32          unsigned 64-bit numpy products reduced mod 2^32, brute force on
+ *                        tiny inputs, wrap-around known answers (INT_MIN, INT_MAX), and at
+ *                        the reference's call site (cuda_kernels.cu:1381: im2col columns x
+ *                        packed filter, trans_b) the convolution accumulators of
+ *                        orc_conv_qi32 and of oracle/_ref.
  */
 #include "qconv_oracle.h"
 
@@ -224,6 +229,43 @@ void orc_dequant_f32(const int32_t* acc, int64_t npix, int32_t k, const int32_t*
       float v = (float)t * m;
       if (relu) v = (v > 0.0f) ? v : 0.0f;
       y[i] = v;
+    }
+  }
+}
+
+/* ---- int32 batched matrix product --------------------------------------------------- */
+
+/* bmm_matmul_i32 (/root/reference/bmm.cu:298-322, kernel bmm.cu:155-246): for each batch
+ * entry b, C[b][m][n] = sum_k op(A)[m][k] * op(B)[k][n] with A[b] at offset b*M*K stored
+ * M x K (K x M when trans_a, read as A[k*M + m], bmm.cu:185-191), B[b] at b*K*N stored K x N
+ * (N x K when trans_b, read as B[n*K + k], bmm.cu:200-206), C[b] at b*M*N.  The reference
+ * accumulates in int32 on the GPU, where signed multiply and add wrap modulo 2^32; the
+ * restatement computes in uint32, whose arithmetic is defined to wrap the same way.  Rows
+ * (b, m) are spread over `nthreads` OpenMP threads (<= 0: the OpenMP default). */
+void orc_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,
+                 int32_t trans_a, int32_t trans_b, int32_t nthreads) {
+  const int64_t rows = (int64_t)batch * M;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 16) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t row = 0; row < rows; ++row) {
+    const int64_t b = row / M;
+    const int64_t m = row % M;
+    const int32_t* Ab = A + b * M * K;
+    const int32_t* Bb = B + b * K * N;
+    uint32_t* Cr = (uint32_t*)C + b * M * N + m * N;
+    for (int32_t n = 0; n < N; ++n) Cr[n] = 0;
+    for (int32_t k = 0; k < K; ++k) {
+      const uint32_t a = (uint32_t)(trans_a ? Ab[(int64_t)k * M + m] : Ab[m * K + k]);
+      if (trans_b) {
+        for (int32_t n = 0; n < N; ++n) Cr[n] += a * (uint32_t)Bb[(int64_t)n * K + k];
+      } else {
+        const int32_t* Bk = Bb + (int64_t)k * N;
+        for (int32_t n = 0; n < N; ++n) Cr[n] += a * (uint32_t)Bk[n];
+      }
     }
   }
 }

@@ -46,6 +46,12 @@ void orc_requant_i8(const int32_t* acc, int64_t npix, int32_t k, const int32_t* 
 void orc_dequant_f32(const int32_t* acc, int64_t npix, int32_t k, const int32_t* bias, const float* w_scale,
                      float in_scale, float out_scale, int32_t relu, float* y);
 
+/* int32 batched matrix product with wrap-around arithmetic, the semantics of the
+ * reference's bmm_matmul_i32: A[b] M x K (stored K x M when trans_a), B[b] K x N (stored
+ * N x K when trans_b), C[b] M x N, batch strides M*K, K*N, M*N. */
+void orc_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,
+                 int32_t trans_a, int32_t trans_b, int32_t nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -221,3 +221,39 @@ def test_cpp_harness_verify_tensors():
         "shape error: groups must be > 0", "shape error: input channels must be divisible by groups",
         "shape error: output channels must be divisible by groups",
         "shape error: invalid output size (negative numerator)", "shape error: stride must be > 0"]
+
+
+def test_bmm_dropin_symbol_is_exported():
+    # bmm.h declares it inside extern "C": the unmangled name is the drop-in ABI
+    assert "bmm_matmul_i32" in exported()
+
+
+def test_bmm_rejects_before_touching_the_gpu():
+    lib = M.lib()
+    p = C.c_void_p(256)  # never dereferenced: every call below fails validation or has no work
+    for args, status in [((p, p, p, -1, 2, 2, 2, 0, 0), _capi.MIQ_ERR_INVALID_ARGUMENT),
+                         ((p, p, p, 1, 2, -2, 2, 0, 0), _capi.MIQ_ERR_INVALID_ARGUMENT),
+                         ((p, p, p, 1, 2, 2, -1, 1, 1), _capi.MIQ_ERR_INVALID_ARGUMENT),
+                         ((p, p, None, 1, 2, 2, 2, 0, 0), _capi.MIQ_ERR_NULL_POINTER),
+                         ((None, p, p, 1, 2, 2, 2, 0, 0), _capi.MIQ_ERR_NULL_POINTER),
+                         ((p, None, p, 1, 2, 2, 2, 0, 1), _capi.MIQ_ERR_NULL_POINTER),
+                         ((p, p, p, 1, 2 ** 31 - 1, 2, 2, 0, 0), _capi.MIQ_ERR_UNSUPPORTED),
+                         ((p, p, p, 1, 2 ** 24, 2 ** 16, 2, 0, 0), _capi.MIQ_ERR_UNSUPPORTED),
+                         ((None, None, None, 0, 5, 5, 5, 0, 0), _capi.MIQ_OK),
+                         ((None, None, None, 3, 0, 5, 5, 0, 0), _capi.MIQ_OK),
+                         ((None, None, None, 3, 5, 0, 5, 1, 0), _capi.MIQ_OK)]:
+        assert lib.miq_bmm_i32(*args, None) == status, args
+    assert lib.miq_bmm_i32(p, p, p, 1, 2, 2, -1, 0, 0, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert b"extents" in lib.miq_last_error_message()
+    # the void drop-in records the reason and enqueues nothing
+    drop = lib.bmm_matmul_i32
+    drop.restype = None
+    drop.argtypes = [C.c_void_p] * 3 + [C.c_int] * 6
+    drop(p, p, None, 1, 2, 2, 2, 0, 0)
+    assert b"output pointer C is NULL" in lib.miq_last_error_message()
+
+
+def test_bmm_python_mirror_errors():
+    with pytest.raises(M.MiqError, match="extents must be >= 0"):
+        M.bmm_matmul_i32(256, 256, 256, 1, -3, 2, 2, 0, 0, stream=0)
+    M.bmm_matmul_i32(None, None, None, 0, 4, 4, 4, 0, 0, stream=0)  # empty batch: no work, no error
