@@ -1,6 +1,7 @@
 """Throughput of the int8 NHWC convolution on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config r50_3x3] [--cache cold|warm] [--all]
+    python bench.py --bmm [--config r50_3x3_im2col]      # the int32 matrix product instead
 
 One step = one fused conv + bias + requantize (+ ReLU) pass of libmiq_qconv over one batch
 of synthetic int8 input (BASELINE.json configs[1] by default: ResNet-50 conv2_x 3x3, N=32)
@@ -83,6 +84,15 @@ BMM_SHAPES = [
 BMM_BYTE_PRODUCTS = 16  # int8 MFMA products per int32 multiply-add (4 shift groups x 4 digit bytes)
 
 
+def bmm_traffic(name: str):
+    """HBM bytes per launch of a --bmm shape from its committed rocprofv3 counter summary, or None."""
+    f = ROOT / "profiles" / f"traffic_bmm_{name}.json"
+    try:
+        return json.loads(f.read_text()).get("bytes_per_launch") if f.exists() else None
+    except (ValueError, OSError):
+        return None
+
+
 def bench_bmm(args) -> None:
     """Times bmm_matmul_i32 per shape (HIP events over back-to-back launches on one stream),
     checks sampled rows against the oracle, prints a table on stderr and one JSON line."""
@@ -95,7 +105,11 @@ def bench_bmm(args) -> None:
     dev = torch.device("cuda:0")
     peak = PEAK_INT8_TOPS / BMM_BYTE_PRODUCTS  # int32 ops/s the int8 matrix cores can deliver
     rows = []
-    for name, batch, m, n, k, ta, tb in BMM_SHAPES:
+    shapes = [sh for sh in BMM_SHAPES if args.config in (None, sh[0])]
+    if not shapes:
+        print(f"bench.py: unknown --bmm shape {args.config}; known: {[sh[0] for sh in BMM_SHAPES]}", file=sys.stderr)
+        sys.exit(2)
+    for name, batch, m, n, k, ta, tb in shapes:
         gen = torch.Generator(device=dev)
         gen.manual_seed(1234)
         a = torch.randint(-2 ** 31, 2 ** 31 - 1, (batch, k, m) if ta else (batch, m, k), dtype=torch.int32,
@@ -150,12 +164,12 @@ def bench_bmm(args) -> None:
         "config": {"workload": head["name"], "batch": head["batch"], "M": head["M"], "N": head["N"], "K": head["K"],
                    "trans_a": head["trans_a"], "trans_b": head["trans_b"], "timing": "eager back-to-back"},
         "roofline": {"bound": "mfma", "achieved": head["tops"], "peak": peak, "unit": "TOPS",
-                     "frac": head["frac"], "traffic": None,
+                     "frac": head["frac"], "traffic": bmm_traffic(head["name"]),
                      "peak_note": f"int8 MFMA {PEAK_INT8_TOPS:.0f} TOPS / {BMM_BYTE_PRODUCTS} byte products per "
                                   "int32 multiply-add"},
         "shapes": rows,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and head["name"] == BMM_SHAPES[0][0]:
         _, batch, m, n, k, ta, tb = BMM_SHAPES[0]
         rng = np.random.default_rng(3)
         msub = 2048
