@@ -2,6 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--config r50_3x3] [--cache cold|warm] [--all]
     python bench.py --bmm [--config r50_3x3_im2col]      # the int32 matrix product instead
+    python bench.py --fp32 [--config resnet_like_56x56]  # the fp32 convolution (conv_bench suite)
 
 One step = one fused conv + bias + requantize (+ ReLU) pass of libmiq_qconv over one batch
 of synthetic int8 input (BASELINE.json configs[1] by default: ResNet-50 conv2_x 3x3, N=32)
@@ -50,6 +51,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--bmm", action="store_true",
                     help="measure the int32 batched matrix product (bmm_matmul_i32) instead of the convolution")
+    ap.add_argument("--fp32", action="store_true",
+                    help="measure the fp32 convolution (launch_fprop_nhwc) on the reference's conv_bench suite")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -186,6 +189,114 @@ def bench_bmm(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+# The reference's conv_bench default suite (src/main.cpp:163-174):
+# (name, n, h, w, c, k, r, s, (pad_h, pad_w, stride_h, stride_w, dil_h, dil_w, groups))
+FP32_SUITE = [
+    ("resnet_like_56x56", 32, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("resnet_like_28x28", 32, 28, 28, 128, 256, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("downsample_stride2", 32, 112, 112, 32, 32, 3, 3, (1, 1, 2, 2, 1, 1, 1)),
+    ("depthwise_3x3", 32, 56, 56, 128, 128, 3, 3, (1, 1, 1, 1, 1, 1, 128)),
+    ("grouped_g4", 32, 56, 56, 128, 128, 3, 3, (1, 1, 1, 1, 1, 1, 4)),
+    ("pointwise_1x1", 32, 56, 56, 128, 256, 1, 1, (0, 0, 1, 1, 1, 1, 1)),
+    ("dilated_3x3", 16, 64, 64, 64, 64, 3, 3, (2, 2, 1, 1, 2, 2, 1)),
+    ("small_batch", 1, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+]
+PEAK_FP32_TFLOPS = 157.3  # dense fp32 MFMA, MI355X
+
+
+def bench_fp32(args) -> None:
+    """Times launch_fprop_nhwc on the conv_bench suite (HIP events over back-to-back launches),
+    checks image 0 of every shape against the oracle with the reference's verify rule, prints
+    a table on stderr and one JSON line for the first shape."""
+    import numpy as np
+    import torch
+
+    import my_own_cnn_amd as M
+    import oracle  # checker of the sampled image and the cpu_baseline leg only
+
+    dev = torch.device("cuda:0")
+    rows = []
+    for name, n, h, w, c, k, r, s_, conv in FP32_SUITE:
+        if args.config not in (None, name):
+            continue
+        ph, pw, sh, sw, dh, dw, g = conv
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(42)
+        x = torch.rand((n, h, w, c), device=dev, generator=gen) * 2 - 1
+        wt = torch.rand((k, r, s_, c // g), device=dev, generator=gen) * 2 - 1
+        kw = dict(stride=(sh, sw), padding=(ph, pw), dilation=(dh, dw), groups=g)
+        y = M.conv2d_nhwc_f32(x, wt, **kw)
+        torch.cuda.synchronize()
+        want = oracle.conv_f32(x[:1].cpu().numpy(), wt.cpu().numpy(), conv)
+        ok = oracle.verify_tensors(want, y[:1].cpu().numpy(), 1e-4, 1e-3)
+        stream = torch.cuda.current_stream()
+        for _ in range(args.warmup):
+            M.conv2d_nhwc_f32(x, wt, out=y, stream=stream, **kw)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(args.steps):
+            M.conv2d_nhwc_f32(x, wt, out=y, stream=stream, **kw)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        ho, wo = y.shape[1], y.shape[2]
+        flops = 2.0 * n * ho * wo * k * r * s_ * (c // g)  # conv_flops, src/main.cpp:143-145
+        nbytes = 4.0 * (x.numel() + wt.numel() + y.numel())
+        t_mfma = flops / (PEAK_FP32_TFLOPS * 1e12)
+        t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+        bound = "mfma" if t_mfma >= t_hbm else "hbm"
+        tf = flops / (ms * 1e-3) / 1e12
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        frac = tf / PEAK_FP32_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
+        algo = "igemm" if (c // g) % 4 == 0 else "direct"
+        rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, kernel=algo,
+                         us=round(ms * 1e3, 2), tflops=round(tf, 3), gbs=round(gbs, 1), bound=bound,
+                         frac=round(frac, 4), verified_image0=ok))
+        del x, wt, y
+        torch.cuda.empty_cache()
+    if not rows:
+        print(f"bench.py: unknown --fp32 shape {args.config}; known: {[c[0] for c in FP32_SUITE]}", file=sys.stderr)
+        sys.exit(2)
+    print(f"{'shape':20s} {'kernel':7s} {'us':>10s} {'TFLOP/s':>8s} {'GB/s':>8s} {'bound':5s} {'frac':>6s} verified",
+          file=sys.stderr)
+    for r in rows:
+        print(f"{r['name']:20s} {r['kernel']:7s} {r['us']:10.2f} {r['tflops']:8.2f} {r['gbs']:8.1f} {r['bound']:5s} "
+              f"{r['frac']:6.3f} {r['verified_image0']}", file=sys.stderr)
+    head = rows[0]
+    line = {
+        "metric": "fp32 conv TFLOP/s, conv_bench default suite (src/main.cpp:163-174)",
+        "value": head["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": head["name"], "N": head["n"], "H": head["h"], "W": head["w"], "C": head["c"],
+                   "K": head["k"], "R": head["r"], "S": head["s"], "groups": head["groups"], "kernel": head["kernel"],
+                   "timing": "eager back-to-back", "cache": "warm"},
+        "roofline": {"bound": head["bound"], "achieved": head["tflops"] if head["bound"] == "mfma" else head["gbs"],
+                     "peak": PEAK_FP32_TFLOPS if head["bound"] == "mfma" else PEAK_HBM_GBS,
+                     "unit": "TFLOP/s" if head["bound"] == "mfma" else "GB/s", "frac": head["frac"], "traffic": None},
+        "shapes": rows,
+    }
+    if not args.no_cpu_baseline and head["name"] == FP32_SUITE[0][0]:
+        _, n, h, w, c, k, r, s_, conv = FP32_SUITE[0]
+        rng = np.random.default_rng(3)
+        x1 = rng.uniform(-1, 1, size=(1, h, w, c)).astype(np.float32)
+        w1 = rng.uniform(-1, 1, size=(k, r, s_, c // conv[6])).astype(np.float32)
+        if oracle.ref() is not None:
+            y1, secs = oracle.ref_conv_f32(x1, w1, conv)
+            kind, what = "reference", "cpu_fprop_nhwc of /root/reference/src/cpu_ref.cpp (g++ -O3)"
+        else:
+            t0 = time.perf_counter()
+            y1 = oracle.conv_f32(x1, w1, conv, nthreads=1)
+            secs = time.perf_counter() - t0
+            kind, what = "port", "oracle/qconv_oracle.c orc_conv_f32 (gcc -O3)"
+        flops1 = 2.0 * y1.shape[1] * y1.shape[2] * k * r * s_ * (c // conv[6])
+        line["cpu_baseline"] = {"value": round(flops1 / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
+                                "sample": f"1 of the {n} images of {FP32_SUITE[0][0]} ({flops1 / 1e9:.2f} GFLOP) in "
+                                          f"{secs:.2f} s; {what}, 1 thread on {cpu_model()}"}
+    print(json.dumps(line), flush=True)
+
+
 def cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -244,6 +355,9 @@ def main():
         sys.exit(1)
     if args.bmm:
         bench_bmm(args)
+        return
+    if args.fp32:
+        bench_fp32(args)
         return
     dev = torch.device("cuda:0")
     names = [args.config or W.HEADLINE]

@@ -5,8 +5,9 @@
 // and :213-342 declare for this path, with the same names, members, defaults and
 // signatures, so that callers written against the reference (quant_conv_test.cu and the
 // verify_tensors / benchmark_cuda_op harness) compile unchanged and resolve to this
-// library's implementations.  The fp32 training kernels and cuDNN comparison functions
-// of the reference header are not part of this path and are not declared here.
+// library's implementations.  Of the fp32 functions, launch_fprop_nhwc is declared; the fp32
+// bprop / grad / blocked kernels and the cuDNN comparison functions of the reference header
+// are not part of this build and are not declared here.
 //
 // Additions beside the reference surface (nothing existing changes):
 //   * RequantParams and the native int8 launchers launch_fprop_nhwc_qi8{,_acc32,_dequant}
@@ -337,6 +338,12 @@ struct RequantParams {
   float out_scale = 1.f;
   bool relu = false;
 };
+
+// fp32 convolution, the reference's launch_fprop_nhwc (/root/reference/src/conv_types.h:287-289,
+// cuda_kernels.cu:767-823): same signature and meaning, default stream, asynchronous.
+void launch_fprop_nhwc(const float* d_x, const float* d_w, float* d_y,
+                       int n, int h, int w, int c, int r, int s, int k,
+                       const Conv2DParams& p);
 
 // y (int8 NHWC) = requant(conv(x, w)); x int8 NHWC, w int8 KRSC, all device pointers.
 void launch_fprop_nhwc_qi8(const int8_t* d_x, const int8_t* d_w, int8_t* d_y,

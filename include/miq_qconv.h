@@ -184,6 +184,18 @@ int miq_qconv2d_nhwc_i8_acc32(const miq_qconv_desc* d, const int8_t* x, const in
 int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const int8_t* w,
                                 const int32_t* bias, const float* w_scale, float* y, void* stream);
 
+/* ---- fp32 convolution --------------------------------------------------------------- */
+
+/* y = conv(x, w) in fp32, NHWC input and output, KRSC filter, with the shape rules of
+ * infer_conv_shape.  algo: MIQ_ALGO_AUTO (the MFMA implicit GEMM when (c/groups) % 4 == 0 and
+ * x, w are 16-byte aligned, else the direct kernel), MIQ_ALGO_IGEMM (MIQ_ERR_UNSUPPORTED
+ * where it does not apply) or MIQ_ALGO_DIRECT (the reference CPU loop's order and rounding:
+ * cpu_fprop_nhwc's result bit for bit).  The implicit GEMM sums in another order; it agrees
+ * with cpu_fprop_nhwc within the reference's own check (abs 1e-4 / rel 1e-3).
+ * Replaces launch_fprop_nhwc (/root/reference/src/cuda_kernels.cu:767-823). */
+int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
+
 /* ---- int32 batched matrix product -------------------------------------------------- */
 /* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and
  * sums, exact for every int32 input.  Row-major, batch strides M*K, K*N and M*N:

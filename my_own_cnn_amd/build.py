@@ -31,6 +31,7 @@ SOURCES = [
     "qconv_band.hip",
     "qconv_stream.hip",
     "gemm_i32.hip",
+    "conv_f32.hip",
     "conv_quant_host.cpp",
     "verify.cpp",
     "bench.cpp",

@@ -223,6 +223,34 @@ def qconv2d_nhwc_i8_dequant(x, w, bias, w_scale, *, stride=1, padding=0, dilatio
 
 
 
+F32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2}
+
+
+def launch_fprop_nhwc(d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,
+                      k: int, p=None, algo: str = "auto", stream=None) -> None:
+    """Mirror of launch_fprop_nhwc (conv_types.h:287-289, cuda_kernels.cu:767-823): fp32 NHWC
+    convolution on device pointers; `algo` 'auto', 'igemm' (MFMA) or 'direct'."""
+    params = _as_params(p)
+    check(lib().miq_fprop_nhwc_f32(_addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k, C.byref(params),
+                                   F32_ALGOS[algo], _stream(stream)), "launch_fprop_nhwc")
+
+
+def conv2d_nhwc_f32(x, w, *, stride=1, padding=0, dilation=1, groups=1, algo="auto", out=None, stream=None):
+    """fp32 convolution of device tensors: x (N, H, W, C), w (K, R, S, C/groups) -> (N, Ho, Wo, K)."""
+    if x.dtype != torch.float32 or w.dtype != torch.float32:
+        raise ValueError("conv2d_nhwc_f32 operands must be float32")
+    n, h, wd, c = (int(v) for v in x.shape)
+    k, r, s = int(w.shape[0]), int(w.shape[1]), int(w.shape[2])
+    (sh, sw), (ph, pw), (dh, dw) = _pair(stride), _pair(padding), _pair(dilation)
+    params = Conv2DParams(ph, pw, sh, sw, dh, dw, groups)
+    ho, wo = infer_conv_shape(n, h, wd, c, r, s, k, params)
+    if out is None:
+        out = torch.empty((n, ho, wo, k), dtype=torch.float32, device=x.device)
+    elif tuple(out.shape) != (n, ho, wo, k) or out.dtype != torch.float32:
+        raise ValueError(f"out must be float32 of shape {(n, ho, wo, k)}")
+    launch_fprop_nhwc(x, w, out, n, h, wd, c, r, s, k, params, algo, stream)
+    return out
+
 def bmm_matmul_i32(d_A: Pointer, d_B: Pointer, d_C: Pointer, batch: int, M: int, N: int, K: int, trans_a: int,
                    trans_b: int, stream=None) -> None:
     """bmm_matmul_i32 (/root/reference/bmm.cu:298-322) on device pointers: C[b] = op(A[b]) op(B[b])
@@ -259,7 +287,7 @@ def bmm_i32(a, b, *, trans_a=False, trans_b=False, out=None, stream=None):
     return y[0] if two_d and out is None else y
 
 __all__ = [
-    "bmm_i32", "bmm_matmul_i32",
+    "bmm_i32", "bmm_matmul_i32", "conv2d_nhwc_f32", "launch_fprop_nhwc",
     "DataType", "Conv2DParams", "BlockConv2DParams", "QParamsU8", "QParamsS5", "QConvDesc", "MiqError",
     "qparams_array", "infer_conv_shape", "infer_block_conv_shape", "launch_fprop_nhwc_qi32",
     "launch_block_fprop_nhwc_qi32", "make_desc", "plan", "qconv2d_nhwc_i8", "qconv2d_nhwc_i8_acc32",

@@ -1,0 +1,285 @@
+// fp32 NHWC convolution, the semantics of the reference's launch_fprop_nhwc
+// (/root/reference/src/cuda_kernels.cu:767-823; CPU definition cpu_ref.cpp:116-146):
+//   y[n,ho,wo,g*Kg+ko] = sum over in-bounds taps (r, s) and ci < Cg of
+//                        x[n, ho*sh-ph+r*dh, wo*sw-pw+s*dw, g*Cg+ci] * w[g*Kg+ko, r, s, ci]
+//
+// f32_igemm_kernel: implicit GEMM on v_mfma_f32_16x16x4f32.  GEMM rows are output pixels
+// (M = N*Ho*Wo) and output channels of one group (Kg); the reduction runs over
+// kdim = R*S*Cg in the reference's (r, s, ci) order, in chunks of 16 values.
+//   - A workgroup of 8 waves computes 128 pixels x 64 channels of one group; wave w computes
+//     channels 32 (w % 2) .. +31 of pixels 32 (w / 2) .. +31: 2 x 2 MFMA tiles.
+//   - Staging: each thread gathers one float4 of 4 consecutive input channels of one tap
+//     for one pixel (Cg % 4 == 0) and one float2 of its filter row (KRSC rows are
+//     kdim-contiguous), into a double-buffered LDS tile [row][16 values] of 64-byte rows
+//     whose 16-byte slot g sits at g ^ (2 * bit 3 of the row): a fragment read (16 rows,
+//     one slot per lane group) is free of bank conflicts.
+//   - A lane's fragment slot holds 4 consecutive reduction values, one per K-step of the
+//     chunk's four MFMAs.  The MFMA's A operand is the channel rows, so a lane's
+//     accumulators hold 4 consecutive channels of one pixel: one 16-byte NHWC store.
+//   - Two chunks are in flight per thread.  Every pass of the loop issues the same loads:
+//     taps outside the image, values past kdim and rows past M or Kg read a valid address
+//     and are zeroed (or never stored), so the compiler's load counters stay exact.
+//   The sum order differs from the reference's sequential fp32 loop; results agree within
+//   the reference's own check (verify_tensors with abs 1e-4 / rel 1e-3, main.cpp:306-316).
+//
+// f32_direct_kernel: one thread per output element, the reference CPU loop order and one
+// fp32 multiply and one add per tap (no contraction): the reference CPU result bit for bit.
+// Used for every shape the implicit GEMM does not take (Cg % 4 != 0, depthwise, unaligned).
+
+#include "qconv_device.h"
+
+#include <algorithm>
+
+namespace miq {
+namespace {
+
+constexpr int kF32Waves = 8;
+constexpr int kF32BM = 128;  // pixels per workgroup
+constexpr int kF32BN = 64;   // channels per workgroup
+constexpr int kF32KC = 16;   // reduction values per chunk
+constexpr int kF32Depth = 2; // chunks in flight per thread
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+struct F32Args {
+  const float* x;
+  const float* w;
+  float* y;
+  Geom g;
+  int M;         // N * Ho * Wo
+  int kdim;      // R * S * Cg
+  int nchunks;   // ceil(kdim / 16)
+  int tn;        // channel tiles per group
+  int tiles;     // pixel tiles * channel tiles per group
+  FastDivM fd_tn, fd_tiles;
+};
+
+__device__ __forceinline__ int f32_slot(int row, int g) { return 4 * row + (g ^ (((row >> 3) & 1) << 1)); }
+
+// Gather cursor of one thread's input float4: reduction index k = 16 * chunk + ka, decoded
+// as (r, s, ci) and advanced one chunk at a time.
+struct TapCursor {
+  int r, s, ci;
+  __device__ __forceinline__ void advance(int Cg, int S) {
+    ci += kF32KC;
+    while (ci >= Cg) {
+      ci -= Cg;
+      if (++s == S) {
+        s = 0;
+        ++r;
+      }
+    }
+  }
+};
+
+__global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a) {
+  __shared__ v4f sA[2][kF32BM * 4];
+  __shared__ v4f sB[2][kF32BN * 4];
+  const Geom& g = a.g;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+
+  const int lin = blockIdx.x;
+  const int grp = fdiv(lin, a.fd_tiles);
+  const int rem = lin - grp * a.tiles;
+  const int tmi = fdiv(rem, a.fd_tn);
+  const int tni = rem - tmi * a.tn;
+  const int m0 = tmi * kF32BM;
+  const int n0 = tni * kF32BN;
+
+  // A: pixel row ar, reduction values 4 aq .. 4 aq + 3 of each chunk
+  const int ar = t >> 2;
+  const int aq = t & 3;
+  const int pix = min(m0 + ar, a.M - 1);
+  const int hw = g.Ho * g.Wo;
+  const int pn = pix / hw;
+  const int prem = pix - pn * hw;
+  const int pho = prem / g.Wo;
+  const int pwo = prem - pho * g.Wo;
+  const int hbase = pho * g.sh - g.ph;
+  const int wbase = pwo * g.sw - g.pw;
+  const float* xn = a.x + static_cast<size_t>(pn) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
+  TapCursor cur;
+  {
+    const int k = 4 * aq;
+    const int tap = k / g.Cg;
+    cur.ci = k - tap * g.Cg;
+    cur.r = tap / g.S;
+    cur.s = tap - cur.r * g.S;
+  }
+  int cur_chunk = 0;
+  // B: filter row br (channel of the group), reduction values 2 bp, 2 bp + 1 of each chunk
+  const int br = t >> 3;
+  const int bp = t & 7;
+  const int brow = grp * g.Kg + min(n0 + br, g.Kg - 1);
+  const float* wr = a.w + static_cast<size_t>(brow) * a.kdim;
+
+  auto load = [&](int c, v4f& va, v2f& vb, bool& oka, bool& okb) {
+    if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
+      cur.advance(g.Cg, g.S);
+      ++cur_chunk;
+    }
+    const int hi = hbase + cur.r * g.dh;
+    const int wi = wbase + cur.s * g.dw;
+    oka = cur.r < g.R && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
+    const size_t xo = oka ? (static_cast<size_t>(hi) * g.W + wi) * g.C + cur.ci : 0;
+    va = *reinterpret_cast<const v4f*>(xn + xo);
+    const int kb = c * kF32KC + 2 * bp;
+    okb = kb < a.kdim;
+    vb = *reinterpret_cast<const v2f*>(wr + (okb ? kb : 0));
+  };
+  const int sa_slot = f32_slot(ar, aq);
+  const int sb_slot = f32_slot(br, bp >> 1);
+  auto stage = [&](int buf, const v4f& va, const v2f& vb, bool oka, bool okb) {
+    sA[buf][sa_slot] = oka ? va : v4f{0.f, 0.f, 0.f, 0.f};
+    *(reinterpret_cast<v2f*>(&sB[buf][sb_slot]) + (bp & 1)) = okb ? vb : v2f{0.f, 0.f};
+  };
+
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int fb0 = f32_slot(32 * wn + (lane & 15), lane >> 4);
+  const int fb1 = f32_slot(32 * wn + 16 + (lane & 15), lane >> 4);
+  const int fa0 = f32_slot(32 * wm + (lane & 15), lane >> 4);
+  const int fa1 = f32_slot(32 * wm + 16 + (lane & 15), lane >> 4);
+  v4f acc[2][2];
+#pragma unroll
+  for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+    for (int im = 0; im < 2; ++im) acc[jn][im] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int P = kF32Depth;
+  const int nch = a.nchunks;
+  if (nch > 0) {
+    const int last = nch - 1;
+    v4f va[P];
+    v2f vb[P];
+    bool oka[P], okb[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) load(min(j, last), va[j], vb[j], oka[j], okb[j]);
+    stage(0, va[0], vb[0], oka[0], okb[0]);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // whole groups of P chunks; chunks past the last load the last one again and stage zeros
+    for (int c0 = 0; c0 < nch; c0 += P) {
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const int c = c0 + j;
+        load(min(c + P, last), va[j], vb[j], oka[j], okb[j]);  // set j was staged last pass
+        const int buf = c & 1;
+        const v4f Bf[2] = {sB[buf][fb0], sB[buf][fb1]};
+        const v4f Af[2] = {sA[buf][fa0], sA[buf][fa1]};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+            for (int im = 0; im < 2; ++im)
+              acc[jn][im] = __builtin_amdgcn_mfma_f32_16x16x4f32(Bf[jn][kk], Af[im][kk], acc[jn][im], 0, 0, 0);
+        const int jn1 = (j + 1) % P;
+        const bool live = c + 1 <= last;
+        stage(buf ^ 1, va[jn1], vb[jn1], live && oka[jn1], live && okb[jn1]);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+    }
+  }
+
+  // lane (c = lane % 16, q = lane / 16) of tile (jn, im): pixel m0 + 32 wm + 16 im + c,
+  // channels n0 + 32 wn + 16 jn + 4 q .. + 3 of the group
+  const bool vec = (g.K & 3) == 0 && (g.Kg & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0;
+#pragma unroll
+  for (int jn = 0; jn < 2; ++jn) {
+#pragma unroll
+    for (int im = 0; im < 2; ++im) {
+      const int m = m0 + 32 * wm + 16 * im + (lane & 15);
+      const int ch = n0 + 32 * wn + 16 * jn + 4 * (lane >> 4);
+      if (m >= a.M) continue;
+      float* yp = a.y + static_cast<size_t>(m) * g.K + static_cast<size_t>(grp) * g.Kg + ch;
+      const v4f r = acc[jn][im];
+      if (vec && ch + 3 < g.Kg) {
+        *reinterpret_cast<v4f*>(yp) = r;
+        store_gap(r);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (ch + i < g.Kg) yp[i] = r[i];
+      }
+    }
+  }
+}
+
+constexpr int kDirectThreads = 256;
+
+__global__ void __launch_bounds__(kDirectThreads) f32_direct_kernel(const float* __restrict__ x,
+                                                                    const float* __restrict__ w,
+                                                                    float* __restrict__ y, Geom g, long long total) {
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;
+  const int k = static_cast<int>(e % g.K);
+  const long long pix = e / g.K;
+  const int wo = static_cast<int>(pix % g.Wo);
+  const long long tq = pix / g.Wo;
+  const int ho = static_cast<int>(tq % g.Ho);
+  const int n = static_cast<int>(tq / g.Ho);
+  const int grp = k / g.Kg;
+  const float* wk = w + static_cast<size_t>(k) * g.R * g.S * g.Cg;
+  const float* xg = x + static_cast<size_t>(n) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
+  float acc = 0.0f;
+  for (int r = 0; r < g.R; ++r) {
+    const int hi = ho * g.sh - g.ph + r * g.dh;
+    if (hi < 0 || hi >= g.H) continue;
+    for (int s = 0; s < g.S; ++s) {
+      const int wi = wo * g.sw - g.pw + s * g.dw;
+      if (wi < 0 || wi >= g.W) continue;
+      const float* xp = xg + (static_cast<size_t>(hi) * g.W + wi) * g.C;
+      const float* wp = wk + (static_cast<size_t>(r) * g.S + s) * g.Cg;
+      for (int ci = 0; ci < g.Cg; ++ci) acc = __fadd_rn(acc, __fmul_rn(xp[ci], wp[ci]));
+    }
+  }
+  y[e] = acc;
+}
+
+}  // namespace
+
+bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why) {
+  auto no = [&](const char* m) {
+    if (why) *why = m;
+    return false;
+  };
+  if (g.Cg % 4 != 0) return no("fp32 implicit GEMM needs (c/groups) % 4 == 0");
+  if (g.H == 0 || g.W == 0) return no("fp32 implicit GEMM needs a non-empty input image");
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(w) & 15u) != 0) {
+    return no("fp32 implicit GEMM needs 16-byte aligned x and w");
+  }
+  const long long m = static_cast<long long>(g.N) * g.Ho * g.Wo;
+  const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
+  if (m >= (1LL << 31) - kF32BM || kdim >= (1LL << 31) - kF32KC) return no("fp32 implicit GEMM extents exceed int32");
+  const long long tiles = ((m + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G;
+  if (tiles > (1LL << 22)) return no("fp32 implicit GEMM grid exceeds 2^22 workgroups");
+  return true;
+}
+
+hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {
+  F32Args a;
+  a.x = x; a.w = w; a.y = y; a.g = g;
+  a.M = g.N * g.Ho * g.Wo;
+  a.kdim = g.R * g.S * g.Cg;
+  a.nchunks = (a.kdim + kF32KC - 1) / kF32KC;
+  a.tn = (g.Kg + kF32BN - 1) / kF32BN;
+  a.tiles = ((a.M + kF32BM - 1) / kF32BM) * a.tn;
+  a.fd_tn = fastdiv_m(a.tn);
+  a.fd_tiles = fastdiv_m(a.tiles);
+  const unsigned blocks = static_cast<unsigned>(a.tiles) * static_cast<unsigned>(g.G);
+  hipLaunchKernelGGL(f32_igemm_kernel, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {
+  const long long total = static_cast<long long>(g.N) * g.Ho * g.Wo * g.K;
+  if (total == 0) return hipSuccess;
+  const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
+  hipLaunchKernelGGL(f32_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, x, w,
+                     y, g, total);
+  return hipGetLastError();
+}
+
+}  // namespace miq

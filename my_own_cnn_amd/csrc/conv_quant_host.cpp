@@ -57,6 +57,13 @@ miq_qconv_desc make_desc(int n, int h, int w, int c, int r, int s, int k, const 
 
 }  // namespace
 
+void launch_fprop_nhwc(const float* d_x, const float* d_w, float* d_y, int n, int h, int w, int c, int r, int s,
+                       int k, const Conv2DParams& p) {
+  const miq_conv2d_params cp = to_c(p);
+  throw_on_error(miq_fprop_nhwc_f32(d_x, d_w, d_y, n, h, w, c, r, s, k, &cp, MIQ_ALGO_AUTO, nullptr),
+                 "launch_fprop_nhwc");
+}
+
 namespace conv_quant_detail {
 
 void launch_fprop_nhwc_qi32_u8(const float* d_x, const float* d_w, int32_t* d_y, int n, int h, int w, int c, int r,

@@ -282,6 +282,31 @@ int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const 
   return i8_entry(miq::kEpiF32, d, x, w, bias, w_scale, y, stream);
 }
 
+int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
+  miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  st = check_tensors(g, filt_elems(g), x, w, y);
+  if (st != MIQ_OK) return st;
+  std::string why;
+  bool igemm = false;
+  switch (algo) {
+    case MIQ_ALGO_AUTO: igemm = miq::f32_igemm_eligible(g, x, w, nullptr); break;
+    case MIQ_ALGO_DIRECT: igemm = false; break;
+    case MIQ_ALGO_IGEMM:
+      if (!miq::f32_igemm_eligible(g, x, w, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      igemm = true;
+      break;
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 convolution algo must be AUTO, DIRECT or IGEMM");
+  }
+  if (out_elems(g) == 0) return MIQ_OK;
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const hipError_t e = igemm ? miq::launch_f32_igemm(g, x, w, y, hs) : miq::launch_f32_direct(g, x, w, y, hs);
+  if (e != hipSuccess) return hip_fail(e, "fp32 convolution launch");
+  return MIQ_OK;
+}
+
 int miq_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,
                 int32_t trans_a, int32_t trans_b, void* stream) {
   if (batch < 0 || M < 0 || N < 0 || K < 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "bmm extents must be >= 0");

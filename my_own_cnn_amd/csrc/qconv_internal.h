@@ -95,6 +95,12 @@ bool stem_eligible(const Geom& g, const void* x, const void* w, const void* y, E
 hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
 
+// fp32 NHWC convolution: MFMA implicit GEMM for (C/groups) % 4 == 0 with 16-byte aligned x
+// and w and a non-empty image; the direct kernel (reference CPU loop order) for any shape.
+bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why);
+hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
+hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
+
 // int32 batched GEMM (wrap-around arithmetic) on the int8 matrix cores; extents already
 // validated (>= 0), pointers non-null where the extents need them.
 hipError_t launch_i32_gemm(const int32_t* A, const int32_t* B, int32_t* C, int batch, int M, int N, int K, bool ta,

@@ -49,6 +49,7 @@ def orc() -> C.CDLL:
         h.orc_requant_i8.argtypes = [_P, C.c_int64, _I, _P, _P, C.c_float, C.c_float, _I, _P]
         h.orc_dequant_f32.argtypes = [_P, C.c_int64, _I, _P, _P, C.c_float, C.c_float, _I, _P]
         h.orc_bmm_i32.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I]
+        h.orc_conv_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
         _orc = h
     return _orc
 
@@ -61,6 +62,7 @@ def ref() -> Optional[C.CDLL]:
         h.ref_last_error.restype = C.c_char_p
         h.ref_fprop_qi32.argtypes = [C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int,
                                      _P, _P, _I, C.c_int, C.c_int, _P, _P]
+        h.ref_fprop_f32.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, _P, _P]
         h.ref_verify_tensors.argtypes = [_P, _P, C.c_size_t, C.c_float, C.c_float, _P, _P, _P, _P, _P]
         _ref = h
     return _ref
@@ -150,6 +152,53 @@ def conv_i8_acc(x: np.ndarray, wt: np.ndarray, conv, nthreads: int = 0) -> np.nd
     if orc().orc_conv_i8_acc(_p(x), n, h, w, c, _p(wt), r, s, k, _p(cv), _p(y), nthreads) != 0:
         raise ValueError("rejected shape")
     return y
+
+
+def conv_f32(x: np.ndarray, wt: np.ndarray, conv, nthreads: int = 0) -> np.ndarray:
+    """fp32 convolution in the reference CPU loop's order and rounding; x NHWC, wt KRSC."""
+    x = np.ascontiguousarray(x, np.float32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    n, h, w, c = x.shape
+    k, r, s, _ = wt.shape
+    cv = _conv7(conv)
+    shp = conv_output_shape(n, h, w, c, r, s, k, cv)
+    if shp is None:
+        raise ValueError("rejected shape")
+    y = np.empty((n, shp[0], shp[1], k), np.float32)
+    if orc().orc_conv_f32(_p(x), n, h, w, c, _p(wt), r, s, k, _p(cv), _p(y), nthreads) != 0:
+        raise ValueError("rejected shape")
+    return y
+
+
+def ref_conv_f32(x, wt, conv) -> Tuple[np.ndarray, float]:
+    """(fp32 output, seconds) of the reference's own cpu_fprop_nhwc (oracle/_ref)."""
+    h = ref()
+    if h is None:
+        raise RuntimeError("oracle/_ref/libref_cpu.so was not built")
+    x = np.ascontiguousarray(x, np.float32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    n, hh, w, c = x.shape
+    k, r, s, _ = wt.shape
+    cv = _conv7(conv)
+    shp = conv_output_shape(n, hh, w, c, r, s, k, cv)
+    if shp is None:
+        raise ValueError("rejected shape")
+    y = np.empty((n, shp[0], shp[1], k), np.float32)
+    secs = C.c_double()
+    if h.ref_fprop_f32(_p(x), n, hh, w, c, _p(wt), r, s, k, _p(cv), _p(y), C.byref(secs)) != 0:
+        raise RuntimeError(h.ref_last_error().decode())
+    return y, secs.value
+
+
+def verify_tensors(ref_v: np.ndarray, got: np.ndarray, abs_eps: float = 1e-4, rel_eps: float = 1e-3) -> bool:
+    """The pass rule of the reference's verify_tensors (src/verify.cpp:7-36): an element fails
+    when |a - b| > abs_eps and (|a| <= 1e-6 or |a - b| / max(|a|, 1e-6) > rel_eps)."""
+    a = np.asarray(ref_v, np.float32).ravel()
+    b = np.asarray(got, np.float32).ravel()
+    err = np.abs(a - b)
+    rel = err / np.maximum(np.abs(a), np.float32(1e-6))
+    fail = (err > abs_eps) & ((np.abs(a) <= 1e-6) | (rel > rel_eps))
+    return not bool(fail.any())
 
 
 def bmm_i32(a: np.ndarray, b: np.ndarray, trans_a: bool = False, trans_b: bool = False,

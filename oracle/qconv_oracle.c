@@ -12,6 +12,8 @@
  *   orc_requant_i8 /     no reference counterpart (the reference has no requantization):
  *   orc_dequant_f32      hand-computed known answers and float64 bounds.
  *   orc_fill_*           fixed known outputs of splitmix64.
+ *   orc_conv_f32         the reference's own cpu_fprop_nhwc compiled in oracle/_ref (bit for
+ *                        bit: same loop order and fp32 operations), float64 convolution.
  *   orc_bmm_i32          unsigned 64-bit numpy products reduced mod 2^32, brute force on
  *                        tiny inputs, wrap-around known answers (INT_MIN, INT_MAX), and at
  *                        the reference's call site (cuda_kernels.cu:1381: im2col columns x
@@ -268,4 +270,49 @@ void orc_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, 
       }
     }
   }
+}
+
+/* ---- fp32 convolution ----------------------------------------------------------------- */
+
+/* cpu_fprop_nhwc (/root/reference/src/cpu_ref.cpp:116-146): for each output (n, ho, wo, g, ko)
+ * in that loop order, acc = 0.0f and then acc += x * w over r, s, ci (in-bounds taps only),
+ * each product and sum one fp32 operation (the library is compiled -ffp-contract=off).
+ * Returns 0, or -1 on a shape orc_conv_output_shape rejects. */
+int orc_conv_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r, int32_t s,
+                 int32_t k, const int32_t conv[7], float* y, int32_t nthreads) {
+  int32_t ho_n, wo_n;
+  if (orc_conv_output_shape(n, h, w, c, r, s, k, conv, &ho_n, &wo_n) != 0) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int64_t nrows = (int64_t)n * ho_n;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t row = 0; row < nrows; ++row) {
+    const int32_t ni = (int32_t)(row / ho_n);
+    const int32_t ho = (int32_t)(row % ho_n);
+    for (int32_t wo = 0; wo < wo_n; ++wo) {
+      for (int32_t g = 0; g < g_n; ++g) {
+        for (int32_t ko = 0; ko < kg; ++ko) {
+          float acc = 0.0f;
+          for (int32_t rr = 0; rr < r; ++rr) {
+            const int32_t hi = ho * sh - ph + rr * dh;
+            if (hi < 0 || hi >= h) continue;
+            for (int32_t ss = 0; ss < s; ++ss) {
+              const int32_t wi = wo * sw - pw + ss * dw;
+              if (wi < 0 || wi >= w) continue;
+              const float* xp = x + (((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg;
+              const float* wp = wt + ((((size_t)g * kg + ko) * r + rr) * s + ss) * cg;
+              for (int32_t ci = 0; ci < cg; ++ci) acc += xp[ci] * wp[ci];
+            }
+          }
+          y[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + (size_t)g * kg + ko] = acc;
+        }
+      }
+    }
+  }
+  return 0;
 }

@@ -46,6 +46,11 @@ void orc_requant_i8(const int32_t* acc, int64_t npix, int32_t k, const int32_t* 
 void orc_dequant_f32(const int32_t* acc, int64_t npix, int32_t k, const int32_t* bias, const float* w_scale,
                      float in_scale, float out_scale, int32_t relu, float* y);
 
+/* fp32 convolution in the loop order and rounding of the reference's cpu_fprop_nhwc;
+ * 0, or -1 on a rejected shape. */
+int orc_conv_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r, int32_t s,
+                 int32_t k, const int32_t conv[7], float* y, int32_t nthreads);
+
 /* int32 batched matrix product with wrap-around arithmetic, the semantics of the
  * reference's bmm_matmul_i32: A[b] M x K (stored K x M when trans_a), B[b] K x N (stored
  * N x K when trans_b), C[b] M x N, batch strides M*K, K*N, M*N. */

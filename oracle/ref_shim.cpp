@@ -5,7 +5,8 @@
 // bench.py's cpu_baseline leg.  Builds the reference's TensorNHWC / FilterKRSC /
 // BlockFilterKByBxRSC from flat arrays, calls cpu_fprop_nhwc_qi32<Tin> /
 // cpu_block_fprop_nhwc_qi32<Tin> (/root/reference/src/conv_types.h:255-285 ->
-// cpu_ref.cpp:36-112, :371-401) and verify_tensors (src/verify.cpp:7-36).
+// cpu_ref.cpp:36-112, :371-401), cpu_fprop_nhwc (cpu_ref.cpp:116-146) and verify_tensors
+// (src/verify.cpp:7-36).
 
 #include <chrono>
 #include <cstdint>
@@ -92,6 +93,29 @@ int ref_fprop_qi32(int kind, const float* x, int n, int h, int w, int c, const f
                    double* seconds) {
   if (kind == 0) return run<DataType::LinQuantU8>(x, n, h, w, c, wt, r, s, k, conv, in_zp, f_zp, by, bx, y, seconds);
   return run<DataType::LinQuantS5>(x, n, h, w, c, wt, r, s, k, conv, in_zp, f_zp, by, bx, y, seconds);
+}
+
+// cpu_fprop_nhwc (cpu_ref.cpp:116-146) on flat NHWC / KRSC arrays; `seconds` (nullable)
+// receives the wall time of the reference call alone.
+int ref_fprop_f32(const float* x, int n, int h, int w, int c, const float* wt, int r, int s, int k,
+                  const int32_t conv[7], float* y, double* seconds) {
+  try {
+    const Conv2DParams p = to_params(conv);
+    TensorNHWC xt(n, h, w, c);
+    std::memcpy(xt.ptr(), x, xt.elements() * sizeof(float));
+    const int cg = (p.groups > 0) ? c / p.groups : 0;
+    FilterKRSC ft(r, s, cg, k);
+    std::memcpy(ft.ptr(), wt, ft.elements() * sizeof(float));
+    TensorNHWC yt;
+    const auto t1 = std::chrono::steady_clock::now();
+    cpu_fprop_nhwc(xt, ft, p, yt);
+    if (seconds) *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+    std::memcpy(y, yt.ptr(), yt.elements() * sizeof(float));
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
 }
 
 int ref_verify_tensors(const float* ref, const float* got, size_t count, float abs_eps, float rel_eps,

@@ -257,3 +257,21 @@ def test_bmm_python_mirror_errors():
     with pytest.raises(M.MiqError, match="extents must be >= 0"):
         M.bmm_matmul_i32(256, 256, 256, 1, -3, 2, 2, 0, 0, stream=0)
     M.bmm_matmul_i32(None, None, None, 0, 4, 4, 4, 0, 0, stream=0)  # empty batch: no work, no error
+
+
+def test_fp32_conv_dropin_and_validation():
+    need = "_Z17launch_fprop_nhwcPKfS0_PfiiiiiiiRK12Conv2DParams"  # the reference's conv_types.h:287-289
+    assert need in exported()
+    lib = M.lib()
+    p = C.c_void_p(256)  # never dereferenced: each call fails validation or has no work
+    ok = _capi.Conv2DParams(1, 1, 1, 1, 1, 1, 1)
+    bad = _capi.Conv2DParams(1, 1, 0, 1, 1, 1, 1)
+    assert lib.miq_fprop_nhwc_f32(p, p, p, 1, 5, 5, 4, 3, 3, 4, C.byref(bad), 0, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert b"stride must be > 0" in lib.miq_last_error_message()
+    assert lib.miq_fprop_nhwc_f32(p, p, None, 1, 5, 5, 4, 3, 3, 4, C.byref(ok), 0, None) == _capi.MIQ_ERR_NULL_POINTER
+    assert lib.miq_fprop_nhwc_f32(p, p, p, 1, 5, 5, 4, 3, 3, 4, C.byref(ok), 7, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert lib.miq_fprop_nhwc_f32(p, p, p, 1, 5, 5, 6, 3, 3, 4, C.byref(ok), 2, None) == _capi.MIQ_ERR_UNSUPPORTED
+    assert b"% 4" in lib.miq_last_error_message()
+    assert lib.miq_fprop_nhwc_f32(None, p, None, 0, 5, 5, 4, 3, 3, 4, C.byref(ok), 0, None) == _capi.MIQ_OK  # n == 0
+    with pytest.raises(M.MiqError, match="stride must be > 0"):
+        M.launch_fprop_nhwc(256, 256, 256, 1, 5, 5, 4, 3, 3, 4, (1, 1, 0, 1, 1, 1, 1), stream=0)

@@ -1,0 +1,96 @@
+"""The fp32 convolution on the GPU (launch_fprop_nhwc / miq_fprop_nhwc_f32) against the
+oracle's restatement of the reference's cpu_fprop_nhwc (cpu_ref.cpp:116-146):
+  - the MFMA implicit GEMM within the reference's own check, verify_tensors with abs 1e-4 /
+    rel 1e-3 (main.cpp:306-316), on the reference's conv_bench suite shapes (main.cpp:163-174,
+    batch cut to keep the oracle in seconds) and on edge shapes: channel tiles and pixel
+    tiles partly filled, taps spanning a chunk (c/groups = 4, 12), stride 3, padding wider
+    than the filter, 5x5 and 7x7 taps, K % 4 != 0 (scalar stores), an unaligned output;
+  - the direct kernel bit for bit (it keeps the reference loop's order and rounding)."""
+import numpy as np
+import pytest
+import torch
+
+import my_own_cnn_amd as M
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+# name, n, h, w, c, k, r, s, (ph, pw, sh, sw, dh, dw, groups)
+SUITE = [
+    ("resnet_like_56x56", 1, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("resnet_like_28x28", 1, 28, 28, 128, 256, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("downsample_stride2", 1, 112, 112, 32, 32, 3, 3, (1, 1, 2, 2, 1, 1, 1)),
+    ("depthwise_3x3", 1, 56, 56, 128, 128, 3, 3, (1, 1, 1, 1, 1, 1, 128)),
+    ("grouped_g4", 1, 56, 56, 128, 128, 3, 3, (1, 1, 1, 1, 1, 1, 4)),
+    ("pointwise_1x1", 1, 56, 56, 128, 256, 1, 1, (0, 0, 1, 1, 1, 1, 1)),
+    ("dilated_3x3", 1, 64, 64, 64, 64, 3, 3, (2, 2, 1, 1, 2, 2, 1)),
+    ("small_batch", 1, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+]
+EDGE = [
+    ("kg24_m_tail", 2, 9, 13, 16, 24, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("cg4_taps_span", 1, 17, 19, 4, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("cg12_taps_span", 2, 11, 7, 24, 36, 3, 3, (1, 1, 2, 1, 1, 1, 2)),
+    ("stride3_wide_pad", 1, 15, 21, 32, 96, 3, 3, (4, 3, 3, 3, 1, 1, 1)),
+    ("5x5_dil2", 1, 20, 20, 16, 80, 5, 5, (4, 4, 1, 1, 2, 2, 1)),
+    ("7x7_s2_c4", 2, 30, 30, 4, 64, 7, 7, (3, 3, 2, 2, 1, 1, 1)),
+    ("k_odd_scalar_store", 1, 10, 10, 8, 30, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("groups3_kg5", 1, 8, 9, 12, 15, 1, 3, (0, 1, 1, 1, 1, 1, 3)),
+]
+CASES = SUITE + EDGE
+
+
+def _data(case, seed):
+    _, n, h, w, c, k, r, s, conv = case
+    rng = np.random.default_rng(seed)
+    x = rng.uniform(-1, 1, size=(n, h, w, c)).astype(np.float32)
+    wt = rng.uniform(-1, 1, size=(k, r, s, c // conv[6])).astype(np.float32)
+    return x, wt
+
+
+def _run(device, x, wt, conv, algo):
+    ph, pw, sh, sw, dh, dw, g = conv
+    xd, wd = torch.from_numpy(x).to(device), torch.from_numpy(wt).to(device)
+    y = M.conv2d_nhwc_f32(xd, wd, stride=(sh, sw), padding=(ph, pw), dilation=(dh, dw), groups=g, algo=algo)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_fp32_conv_matches_reference_cpu(device, case):
+    x, wt = _data(case, 500 + CASES.index(case))
+    conv = case[8]
+    want = oracle.conv_f32(x, wt, conv)
+    got = _run(device, x, wt, conv, "auto")
+    assert oracle.verify_tensors(want, got, 1e-4, 1e-3), float(np.abs(got - want).max())
+    direct = _run(device, x, wt, conv, "direct")
+    np.testing.assert_array_equal(direct.view(np.uint32), want.view(np.uint32))
+
+
+def test_fp32_igemm_is_what_auto_runs_where_it_applies(device):
+    x, wt = _data(SUITE[0], 1)
+    conv = SUITE[0][8]
+    a = _run(device, x, wt, conv, "auto")
+    b = _run(device, x, wt, conv, "igemm")
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    with pytest.raises(M.MiqError, match="% 4"):
+        _run(device, *_data(SUITE[3], 2)[:2], SUITE[3][8], "igemm")  # depthwise: c/groups == 1
+
+
+def test_fp32_unaligned_output_and_empty_image(device):
+    x, wt = _data(EDGE[0], 3)
+    conv = EDGE[0][8]
+    n, h, w, c = x.shape
+    k = wt.shape[0]
+    want = oracle.conv_f32(x, wt, conv)
+    buf = torch.zeros(want.size + 1, dtype=torch.float32, device=device)
+    xd, wd = torch.from_numpy(x).to(device), torch.from_numpy(wt).to(device)
+    M.launch_fprop_nhwc(xd, wd, buf[1:], n, h, w, c, 3, 3, k, conv, algo="igemm")
+    torch.cuda.synchronize()
+    got = buf[1:].cpu().numpy().reshape(want.shape)
+    assert oracle.verify_tensors(want, got) and float(buf[0]) == 0.0
+    # H == 0 with padding: every tap is outside the image, the output is zeros
+    xe = torch.empty((1, 0, 4, 8), dtype=torch.float32, device=device)
+    we = torch.ones((8, 1, 1, 8), dtype=torch.float32, device=device)
+    ye = M.conv2d_nhwc_f32(xe, we, padding=1)
+    torch.cuda.synchronize()
+    assert tuple(ye.shape) == (1, 2, 6, 8) and float(ye.abs().max()) == 0.0
