@@ -53,6 +53,8 @@ def parse():
                     help="measure the int32 batched matrix product (bmm_matmul_i32) instead of the convolution")
     ap.add_argument("--fp32", action="store_true",
                     help="measure the fp32 convolution (launch_fprop_nhwc) on the reference's conv_bench suite")
+    ap.add_argument("--op", choices=["fprop", "bprop", "grad"], default="fprop",
+                    help="with --fp32: the pass to time (launch_fprop_nhwc / launch_bprop_nhwc / launch_grad_nhwc)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -227,20 +229,44 @@ def bench_fp32(args) -> None:
         kw = dict(stride=(sh, sw), padding=(ph, pw), dilation=(dh, dw), groups=g)
         y = M.conv2d_nhwc_f32(x, wt, **kw)
         torch.cuda.synchronize()
-        want = oracle.conv_f32(x[:1].cpu().numpy(), wt.cpu().numpy(), conv)
-        ok = oracle.verify_tensors(want, y[:1].cpu().numpy(), 1e-4, 1e-3)
+        ho, wo = y.shape[1], y.shape[2]
         stream = torch.cuda.current_stream()
+        if args.op == "fprop":
+            want = oracle.conv_f32(x[:1].cpu().numpy(), wt.cpu().numpy(), conv)
+            ok = oracle.verify_tensors(want, y[:1].cpu().numpy(), 1e-4, 1e-3)
+
+            def step():
+                M.conv2d_nhwc_f32(x, wt, out=y, stream=stream, **kw)
+        elif args.op == "bprop":
+            dy = torch.rand(y.shape, device=dev, generator=gen) * 2 - 1
+            dx = torch.empty_like(x)
+            M.launch_bprop_nhwc(dy, wt, dx, n, h, w, c, r, s_, k, conv, stream=stream)
+            torch.cuda.synchronize()
+            want = oracle.bprop_f32(dy[:1].cpu().numpy(), wt.cpu().numpy(), (1, h, w, c), conv)
+            ok = bool(np.array_equal(dx[:1].cpu().numpy().view(np.uint32), want.view(np.uint32)))
+
+            def step():
+                M.launch_bprop_nhwc(dy, wt, dx, n, h, w, c, r, s_, k, conv, stream=stream)
+        else:
+            dy = torch.rand(y.shape, device=dev, generator=gen) * 2 - 1
+            dw = torch.empty_like(wt)
+            M.launch_grad_nhwc(x[:1], dy[:1], dw, 1, h, w, c, r, s_, k, conv, stream=stream)  # one-image check
+            torch.cuda.synchronize()
+            want = oracle.grad_f32(x[:1].cpu().numpy(), dy[:1].cpu().numpy(), tuple(wt.shape), conv)
+            ok = bool(np.array_equal(dw.cpu().numpy().view(np.uint32), want.view(np.uint32)))
+
+            def step():
+                M.launch_grad_nhwc(x, dy, dw, n, h, w, c, r, s_, k, conv, stream=stream)
         for _ in range(args.warmup):
-            M.conv2d_nhwc_f32(x, wt, out=y, stream=stream, **kw)
+            step()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0.record(stream)
         for _ in range(args.steps):
-            M.conv2d_nhwc_f32(x, wt, out=y, stream=stream, **kw)
+            step()
         t1.record(stream)
         torch.cuda.synchronize()
         ms = t0.elapsed_time(t1) / args.steps
-        ho, wo = y.shape[1], y.shape[2]
         flops = 2.0 * n * ho * wo * k * r * s_ * (c // g)  # conv_flops, src/main.cpp:143-145
         nbytes = 4.0 * (x.numel() + wt.numel() + y.numel())
         t_mfma = flops / (PEAK_FP32_TFLOPS * 1e12)
@@ -249,7 +275,7 @@ def bench_fp32(args) -> None:
         tf = flops / (ms * 1e-3) / 1e12
         gbs = nbytes / (ms * 1e-3) / 1e9
         frac = tf / PEAK_FP32_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
-        algo = "igemm" if (c // g) % 4 == 0 else "direct"
+        algo = "igemm" if (c // g) % 4 == 0 and args.op == "fprop" else "direct"
         rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, kernel=algo,
                          us=round(ms * 1e3, 2), tflops=round(tf, 3), gbs=round(gbs, 1), bound=bound,
                          frac=round(frac, 4), verified_image0=ok))
@@ -265,7 +291,7 @@ def bench_fp32(args) -> None:
               f"{r['frac']:6.3f} {r['verified_image0']}", file=sys.stderr)
     head = rows[0]
     line = {
-        "metric": "fp32 conv TFLOP/s, conv_bench default suite (src/main.cpp:163-174)",
+        "metric": f"fp32 conv {args.op} TFLOP/s, conv_bench default suite (src/main.cpp:163-174)",
         "value": head["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(head["us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
@@ -277,7 +303,7 @@ def bench_fp32(args) -> None:
                      "unit": "TFLOP/s" if head["bound"] == "mfma" else "GB/s", "frac": head["frac"], "traffic": None},
         "shapes": rows,
     }
-    if not args.no_cpu_baseline and head["name"] == FP32_SUITE[0][0]:
+    if not args.no_cpu_baseline and head["name"] == FP32_SUITE[0][0] and args.op == "fprop":
         _, n, h, w, c, k, r, s_, conv = FP32_SUITE[0]
         rng = np.random.default_rng(3)
         x1 = rng.uniform(-1, 1, size=(1, h, w, c)).astype(np.float32)

@@ -5,9 +5,9 @@
 // and :213-342 declare for this path, with the same names, members, defaults and
 // signatures, so that callers written against the reference (quant_conv_test.cu and the
 // verify_tensors / benchmark_cuda_op harness) compile unchanged and resolve to this
-// library's implementations.  Of the fp32 functions, launch_fprop_nhwc is declared; the fp32
-// bprop / grad / blocked kernels and the cuDNN comparison functions of the reference header
-// are not part of this build and are not declared here.
+// library's implementations.  Of the fp32 functions, launch_fprop_nhwc, launch_bprop_nhwc and
+// launch_grad_nhwc are declared; the blocked fp32 kernels and the cuDNN comparison functions
+// of the reference header are not part of this build and are not declared here.
 //
 // Additions beside the reference surface (nothing existing changes):
 //   * RequantParams and the native int8 launchers launch_fprop_nhwc_qi8{,_acc32,_dequant}
@@ -344,6 +344,14 @@ struct RequantParams {
 void launch_fprop_nhwc(const float* d_x, const float* d_w, float* d_y,
                        int n, int h, int w, int c, int r, int s, int k,
                        const Conv2DParams& p);
+// dx and dw of the fp32 convolution, the reference's launch_bprop_nhwc / launch_grad_nhwc
+// (conv_types.h:290-295, cuda_kernels.cu:825-937): same signatures and meaning.
+void launch_bprop_nhwc(const float* d_dy, const float* d_w, float* d_dx,
+                       int n, int h, int w, int c, int r, int s, int k,
+                       const Conv2DParams& p);
+void launch_grad_nhwc(const float* d_x, const float* d_dy, float* d_dw,
+                      int n, int h, int w, int c, int r, int s, int k,
+                      const Conv2DParams& p);
 
 // y (int8 NHWC) = requant(conv(x, w)); x int8 NHWC, w int8 KRSC, all device pointers.
 void launch_fprop_nhwc_qi8(const int8_t* d_x, const int8_t* d_w, int8_t* d_y,

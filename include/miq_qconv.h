@@ -196,6 +196,19 @@ int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const 
 int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
                        int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
 
+/* dx = the gradient of the convolution with respect to x, for output gradient dy (NHWC,
+ * n x ho x wo x k) and filter w; dx is NHWC n x h x w x c, fully overwritten.  The loop order
+ * and rounding of cpu_bprop_nhwc: its result bit for bit.
+ * Replaces launch_bprop_nhwc (/root/reference/src/cuda_kernels.cu:825-872). */
+int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream);
+
+/* dw = the gradient with respect to the KRSC filter (k x r x s x c/groups, fully overwritten)
+ * for input x and output gradient dy.  The loop order and rounding of cpu_grad_nhwc.
+ * Replaces launch_grad_nhwc (/root/reference/src/cuda_kernels.cu:874-937). */
+int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream);
+
 /* ---- int32 batched matrix product -------------------------------------------------- */
 /* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and
  * sums, exact for every int32 input.  Row-major, batch strides M*K, K*N and M*N:

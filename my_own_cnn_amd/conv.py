@@ -235,6 +235,22 @@ def launch_fprop_nhwc(d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, 
                                    F32_ALGOS[algo], _stream(stream)), "launch_fprop_nhwc")
 
 
+
+def launch_bprop_nhwc(d_dy: Pointer, d_w: Pointer, d_dx: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,
+                      k: int, p=None, stream=None) -> None:
+    """Mirror of launch_bprop_nhwc (conv_types.h:290-292): dx of the fp32 convolution."""
+    params = _as_params(p)
+    check(lib().miq_bprop_nhwc_f32(_addr(d_dy), _addr(d_w), _addr(d_dx), n, h, w, c, r, s, k, C.byref(params),
+                                   _stream(stream)), "launch_bprop_nhwc")
+
+
+def launch_grad_nhwc(d_x: Pointer, d_dy: Pointer, d_dw: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,
+                     k: int, p=None, stream=None) -> None:
+    """Mirror of launch_grad_nhwc (conv_types.h:293-295): dw of the fp32 convolution."""
+    params = _as_params(p)
+    check(lib().miq_grad_nhwc_f32(_addr(d_x), _addr(d_dy), _addr(d_dw), n, h, w, c, r, s, k, C.byref(params),
+                                  _stream(stream)), "launch_grad_nhwc")
+
 def conv2d_nhwc_f32(x, w, *, stride=1, padding=0, dilation=1, groups=1, algo="auto", out=None, stream=None):
     """fp32 convolution of device tensors: x (N, H, W, C), w (K, R, S, C/groups) -> (N, Ho, Wo, K)."""
     if x.dtype != torch.float32 or w.dtype != torch.float32:
@@ -287,7 +303,7 @@ def bmm_i32(a, b, *, trans_a=False, trans_b=False, out=None, stream=None):
     return y[0] if two_d and out is None else y
 
 __all__ = [
-    "bmm_i32", "bmm_matmul_i32", "conv2d_nhwc_f32", "launch_fprop_nhwc",
+    "bmm_i32", "bmm_matmul_i32", "conv2d_nhwc_f32", "launch_fprop_nhwc", "launch_bprop_nhwc", "launch_grad_nhwc",
     "DataType", "Conv2DParams", "BlockConv2DParams", "QParamsU8", "QParamsS5", "QConvDesc", "MiqError",
     "qparams_array", "infer_conv_shape", "infer_block_conv_shape", "launch_fprop_nhwc_qi32",
     "launch_block_fprop_nhwc_qi32", "make_desc", "plan", "qconv2d_nhwc_i8", "qconv2d_nhwc_i8_acc32",

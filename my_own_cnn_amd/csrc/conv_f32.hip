@@ -25,6 +25,10 @@
 // f32_direct_kernel: one thread per output element, the reference CPU loop order and one
 // fp32 multiply and one add per tap (no contraction): the reference CPU result bit for bit.
 // Used for every shape the implicit GEMM does not take (Cg % 4 != 0, depthwise, unaligned).
+//
+// f32_bprop_direct_kernel / f32_grad_direct_kernel: dx and dw (launch_bprop_nhwc,
+// launch_grad_nhwc, cuda_kernels.cu:825-937) the same way, in the loop orders of
+// cpu_bprop_nhwc / cpu_grad_nhwc: their results bit for bit.
 
 #include "qconv_device.h"
 
@@ -238,7 +242,96 @@ __global__ void __launch_bounds__(kDirectThreads) f32_direct_kernel(const float*
   y[e] = acc;
 }
 
+// dx of the convolution, the reference's cpu_bprop_nhwc order (cpu_ref.cpp:150-190): one
+// thread per dx element; for each tap (r, s) whose output position ho = (hi + ph - r dh) / sh
+// is whole and in range (likewise wo), acc += dy * w over the group's output channels.
+__global__ void __launch_bounds__(kDirectThreads) f32_bprop_direct_kernel(const float* __restrict__ dy,
+                                                                          const float* __restrict__ w,
+                                                                          float* __restrict__ dx, Geom g,
+                                                                          long long total) {
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;
+  const int c = static_cast<int>(e % g.C);
+  const long long pix = e / g.C;
+  const int wi = static_cast<int>(pix % g.W);
+  const long long tq = pix / g.W;
+  const int hi = static_cast<int>(tq % g.H);
+  const int n = static_cast<int>(tq / g.H);
+  const int grp = c / g.Cg;
+  const int ci = c - grp * g.Cg;
+  const size_t wstride = static_cast<size_t>(g.R) * g.S * g.Cg;  // between output channels
+  float acc = 0.0f;
+  for (int r = 0; r < g.R; ++r) {
+    const int hn = hi + g.ph - r * g.dh;
+    if (hn < 0 || hn % g.sh != 0) continue;
+    const int ho = hn / g.sh;
+    if (ho >= g.Ho) continue;
+    for (int s = 0; s < g.S; ++s) {
+      const int wn = wi + g.pw - s * g.dw;
+      if (wn < 0 || wn % g.sw != 0) continue;
+      const int wo = wn / g.sw;
+      if (wo >= g.Wo) continue;
+      const float* dyp = dy + ((static_cast<size_t>(n) * g.Ho + ho) * g.Wo + wo) * g.K + static_cast<size_t>(grp) * g.Kg;
+      const float* wp = w + static_cast<size_t>(grp) * g.Kg * wstride + (static_cast<size_t>(r) * g.S + s) * g.Cg + ci;
+      for (int ko = 0; ko < g.Kg; ++ko) acc = __fadd_rn(acc, __fmul_rn(dyp[ko], wp[ko * wstride]));
+    }
+  }
+  dx[e] = acc;
+}
+
+// dw of the convolution, the reference's cpu_grad_nhwc order (cpu_ref.cpp:192-230): one thread
+// per dw[k][r][s][ci] element, acc += x * dy over n, ho, wo in that order (in-bounds taps).
+__global__ void __launch_bounds__(kDirectThreads) f32_grad_direct_kernel(const float* __restrict__ x,
+                                                                         const float* __restrict__ dy,
+                                                                         float* __restrict__ dw, Geom g,
+                                                                         long long total) {
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;
+  const int ci = static_cast<int>(e % g.Cg);
+  const long long t1 = e / g.Cg;
+  const int s = static_cast<int>(t1 % g.S);
+  const long long t2 = t1 / g.S;
+  const int r = static_cast<int>(t2 % g.R);
+  const int k = static_cast<int>(t2 / g.R);
+  const int grp = k / g.Kg;
+  const float* xc = x + static_cast<size_t>(grp) * g.Cg + ci;
+  const float* dyk = dy + k;
+  float acc = 0.0f;
+  for (int n = 0; n < g.N; ++n) {
+    for (int ho = 0; ho < g.Ho; ++ho) {
+      const int hi = ho * g.sh - g.ph + r * g.dh;
+      if (hi < 0 || hi >= g.H) continue;
+      const float* xrow = xc + (static_cast<size_t>(n) * g.H + hi) * g.W * g.C;
+      const float* dyrow = dyk + (static_cast<size_t>(n) * g.Ho + ho) * g.Wo * g.K;
+      for (int wo = 0; wo < g.Wo; ++wo) {
+        const int wi = wo * g.sw - g.pw + s * g.dw;
+        if (wi < 0 || wi >= g.W) continue;
+        acc = __fadd_rn(acc, __fmul_rn(xrow[static_cast<size_t>(wi) * g.C], dyrow[static_cast<size_t>(wo) * g.K]));
+      }
+    }
+  }
+  dw[e] = acc;
+}
+
 }  // namespace
+
+hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream) {
+  const long long total = static_cast<long long>(g.N) * g.H * g.W * g.C;
+  if (total == 0) return hipSuccess;
+  const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
+  hipLaunchKernelGGL(f32_bprop_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream,
+                     dy, w, dx, g, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream) {
+  const long long total = static_cast<long long>(g.K) * g.R * g.S * g.Cg;
+  if (total == 0) return hipSuccess;
+  const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
+  hipLaunchKernelGGL(f32_grad_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, x,
+                     dy, dw, g, total);
+  return hipGetLastError();
+}
 
 bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why) {
   auto no = [&](const char* m) {

@@ -307,6 +307,36 @@ int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int3
   return MIQ_OK;
 }
 
+int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream) {
+  miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  // dy has the output's extent, dx the input's
+  if (in_elems(g) > 0 && dx == nullptr) return fail(MIQ_ERR_NULL_POINTER, "dx pointer is NULL");
+  if (out_elems(g) > 0 && dy == nullptr) return fail(MIQ_ERR_NULL_POINTER, "dy pointer is NULL");
+  if (filt_elems(g) > 0 && w == nullptr) return fail(MIQ_ERR_NULL_POINTER, "filter pointer is NULL");
+  if (in_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dx has more than 2^32-256 elements");
+  if (in_elems(g) == 0) return MIQ_OK;
+  const hipError_t e = miq::launch_f32_bprop_direct(g, dy, w, dx, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "fp32 bprop launch");
+  return MIQ_OK;
+}
+
+int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream) {
+  miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  st = check_tensors(g, filt_elems(g), x, dw, dy);
+  if (st != MIQ_OK) return st;
+  if (filt_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dw has more than 2^32-256 elements");
+  if (filt_elems(g) == 0) return MIQ_OK;
+  const hipError_t e = miq::launch_f32_grad_direct(g, x, dy, dw, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "fp32 grad launch");
+  return MIQ_OK;
+}
+
 int miq_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,
                 int32_t trans_a, int32_t trans_b, void* stream) {
   if (batch < 0 || M < 0 || N < 0 || K < 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "bmm extents must be >= 0");

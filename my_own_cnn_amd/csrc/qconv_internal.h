@@ -100,6 +100,9 @@ hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t*
 bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why);
 hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
 hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
+// fp32 dx and dw in the reference CPU loop orders (one thread per output element).
+hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
+hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
 
 // int32 batched GEMM (wrap-around arithmetic) on the int8 matrix cores; extents already
 // validated (>= 0), pointers non-null where the extents need them.

@@ -50,6 +50,8 @@ def orc() -> C.CDLL:
         h.orc_dequant_f32.argtypes = [_P, C.c_int64, _I, _P, _P, C.c_float, C.c_float, _I, _P]
         h.orc_bmm_i32.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I]
         h.orc_conv_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
+        h.orc_bprop_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
+        h.orc_grad_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
         _orc = h
     return _orc
 
@@ -62,6 +64,7 @@ def ref() -> Optional[C.CDLL]:
         h.ref_last_error.restype = C.c_char_p
         h.ref_fprop_qi32.argtypes = [C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int,
                                      _P, _P, _I, C.c_int, C.c_int, _P, _P]
+        h.ref_backward_f32.argtypes = [C.c_int, _P, _P] + [C.c_int] * 7 + [_P, _P, _P]
         h.ref_fprop_f32.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, _P, _P]
         h.ref_verify_tensors.argtypes = [_P, _P, C.c_size_t, C.c_float, C.c_float, _P, _P, _P, _P, _P]
         _ref = h
@@ -188,6 +191,48 @@ def ref_conv_f32(x, wt, conv) -> Tuple[np.ndarray, float]:
     if h.ref_fprop_f32(_p(x), n, hh, w, c, _p(wt), r, s, k, _p(cv), _p(y), C.byref(secs)) != 0:
         raise RuntimeError(h.ref_last_error().decode())
     return y, secs.value
+
+
+def bprop_f32(dy: np.ndarray, wt: np.ndarray, x_shape, conv, nthreads: int = 0) -> np.ndarray:
+    """dx (x_shape, NHWC) of the fp32 convolution in the loop order of cpu_bprop_nhwc."""
+    dy = np.ascontiguousarray(dy, np.float32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    n, h, w, c = (int(v) for v in x_shape)
+    k, r, s, _ = wt.shape
+    dx = np.empty((n, h, w, c), np.float32)
+    if orc().orc_bprop_f32(_p(dy), n, h, w, c, _p(wt), r, s, k, _p(_conv7(conv)), _p(dx), nthreads) != 0:
+        raise ValueError("rejected shape")
+    return dx
+
+
+def grad_f32(x: np.ndarray, dy: np.ndarray, w_shape, conv, nthreads: int = 0) -> np.ndarray:
+    """dw (w_shape, KRSC) of the fp32 convolution in the loop order of cpu_grad_nhwc."""
+    x = np.ascontiguousarray(x, np.float32)
+    dy = np.ascontiguousarray(dy, np.float32)
+    n, h, w, c = x.shape
+    k, r, s, cg = (int(v) for v in w_shape)
+    dw = np.empty((k, r, s, cg), np.float32)
+    if orc().orc_grad_f32(_p(x), n, h, w, c, _p(dy), r, s, k, _p(_conv7(conv)), _p(dw), nthreads) != 0:
+        raise ValueError("rejected shape")
+    return dw
+
+
+def ref_backward_f32(op: str, a, b, x_shape, w_shape, conv) -> Tuple[np.ndarray, float]:
+    """(dx or dw, seconds) of the reference's own cpu_bprop_nhwc ('bprop': a = dy, b = w) or
+    cpu_grad_nhwc ('grad': a = x, b = dy), compiled in oracle/_ref."""
+    h = ref()
+    if h is None:
+        raise RuntimeError("oracle/_ref/libref_cpu.so was not built")
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    n, hh, w, c = (int(v) for v in x_shape)
+    k, r, s, cg = (int(v) for v in w_shape)
+    out = np.empty((n, hh, w, c) if op == "bprop" else (k, r, s, cg), np.float32)
+    secs = C.c_double()
+    if h.ref_backward_f32(0 if op == "bprop" else 1, _p(a), _p(b), n, hh, w, c, r, s, k, _p(_conv7(conv)), _p(out),
+                          C.byref(secs)) != 0:
+        raise RuntimeError(h.ref_last_error().decode())
+    return out, secs.value
 
 
 def verify_tensors(ref_v: np.ndarray, got: np.ndarray, abs_eps: float = 1e-4, rel_eps: float = 1e-3) -> bool:

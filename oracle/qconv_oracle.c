@@ -12,8 +12,9 @@
  *   orc_requant_i8 /     no reference counterpart (the reference has no requantization):
  *   orc_dequant_f32      hand-computed known answers and float64 bounds.
  *   orc_fill_*           fixed known outputs of splitmix64.
- *   orc_conv_f32         the reference's own cpu_fprop_nhwc compiled in oracle/_ref (bit for
- *                        bit: same loop order and fp32 operations), float64 convolution.
+ *   orc_conv_f32,        the reference's own cpu_fprop_nhwc / cpu_bprop_nhwc / cpu_grad_nhwc
+ *   orc_bprop_f32,       compiled in oracle/_ref (bit for bit: same loop orders and fp32
+ *   orc_grad_f32         operations); float64 torch convolution and its autograd gradients.
  *   orc_bmm_i32          unsigned 64-bit numpy products reduced mod 2^32, brute force on
  *                        tiny inputs, wrap-around known answers (INT_MIN, INT_MAX), and at
  *                        the reference's call site (cuda_kernels.cu:1381: im2col columns x
@@ -313,6 +314,95 @@ int orc_conv_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, con
         }
       }
     }
+  }
+  return 0;
+}
+
+/* cpu_bprop_nhwc (cpu_ref.cpp:150-190): for each dx element (n, hi, wi, g, ci) in that order,
+ * acc = 0.0f, then over taps r, s whose ho = (hi + ph - r dh) / sh is whole and in range
+ * (likewise wo), acc += dy[n, ho, wo, g Kg + ko] * w[g Kg + ko, r, s, ci] over ko. */
+int orc_bprop_f32(const float* dy, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r, int32_t s,
+                  int32_t k, const int32_t conv[7], float* dx, int32_t nthreads) {
+  int32_t ho_n, wo_n;
+  if (orc_conv_output_shape(n, h, w, c, r, s, k, conv, &ho_n, &wo_n) != 0) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int64_t nrows = (int64_t)n * h;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t row = 0; row < nrows; ++row) {
+    const int32_t ni = (int32_t)(row / h);
+    const int32_t hi = (int32_t)(row % h);
+    for (int32_t wi = 0; wi < w; ++wi) {
+      for (int32_t g = 0; g < g_n; ++g) {
+        for (int32_t ci = 0; ci < cg; ++ci) {
+          float acc = 0.0f;
+          for (int32_t rr = 0; rr < r; ++rr) {
+            const int32_t hn = hi + ph - rr * dh;
+            if (hn < 0 || hn % sh != 0) continue;
+            const int32_t ho = hn / sh;
+            if (ho >= ho_n) continue;
+            for (int32_t ss = 0; ss < s; ++ss) {
+              const int32_t wn = wi + pw - ss * dw;
+              if (wn < 0 || wn % sw != 0) continue;
+              const int32_t wo = wn / sw;
+              if (wo >= wo_n) continue;
+              for (int32_t ko = 0; ko < kg; ++ko) {
+                const float dyv = dy[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + (size_t)g * kg + ko];
+                const float wv = wt[((((size_t)g * kg + ko) * r + rr) * s + ss) * cg + ci];
+                acc += dyv * wv;
+              }
+            }
+          }
+          dx[(((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg + ci] = acc;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* cpu_grad_nhwc (cpu_ref.cpp:192-230): for each dw element (r, s, g, ci, ko) in that order,
+ * acc = 0.0f, then acc += x[n, hi, wi, g Cg + ci] * dy[n, ho, wo, g Kg + ko] over n, ho, wo
+ * (in-bounds taps); dw is KRSC. */
+int orc_grad_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* dy, int32_t r, int32_t s,
+                 int32_t k, const int32_t conv[7], float* dwt, int32_t nthreads) {
+  int32_t ho_n, wo_n;
+  if (orc_conv_output_shape(n, h, w, c, r, s, k, conv, &ho_n, &wo_n) != 0) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int64_t nel = (int64_t)k * r * s * cg;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 16) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t e = 0; e < nel; ++e) {
+    const int32_t ci = (int32_t)(e % cg);
+    const int32_t ss = (int32_t)((e / cg) % s);
+    const int32_t rr = (int32_t)((e / ((int64_t)cg * s)) % r);
+    const int32_t kk = (int32_t)(e / ((int64_t)cg * s * r));
+    const int32_t g = kk / kg;
+    float acc = 0.0f;
+    for (int32_t ni = 0; ni < n; ++ni) {
+      for (int32_t ho = 0; ho < ho_n; ++ho) {
+        const int32_t hi = ho * sh - ph + rr * dh;
+        if (hi < 0 || hi >= h) continue;
+        for (int32_t wo = 0; wo < wo_n; ++wo) {
+          const int32_t wi = wo * sw - pw + ss * dw;
+          if (wi < 0 || wi >= w) continue;
+          const float xv = x[(((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg + ci];
+          const float dyv = dy[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + kk];
+          acc += xv * dyv;
+        }
+      }
+    }
+    dwt[e] = acc;
   }
   return 0;
 }

@@ -51,6 +51,13 @@ void orc_dequant_f32(const int32_t* acc, int64_t npix, int32_t k, const int32_t*
 int orc_conv_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r, int32_t s,
                  int32_t k, const int32_t conv[7], float* y, int32_t nthreads);
 
+/* dx and dw of the fp32 convolution in the loop orders and rounding of the reference's
+ * cpu_bprop_nhwc / cpu_grad_nhwc; dy is n x ho x wo x k; 0, or -1 on a rejected shape. */
+int orc_bprop_f32(const float* dy, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r, int32_t s,
+                  int32_t k, const int32_t conv[7], float* dx, int32_t nthreads);
+int orc_grad_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* dy, int32_t r, int32_t s,
+                 int32_t k, const int32_t conv[7], float* dw, int32_t nthreads);
+
 /* int32 batched matrix product with wrap-around arithmetic, the semantics of the
  * reference's bmm_matmul_i32: A[b] M x K (stored K x M when trans_a), B[b] K x N (stored
  * N x K when trans_b), C[b] M x N, batch strides M*K, K*N, M*N. */

@@ -5,7 +5,8 @@
 // bench.py's cpu_baseline leg.  Builds the reference's TensorNHWC / FilterKRSC /
 // BlockFilterKByBxRSC from flat arrays, calls cpu_fprop_nhwc_qi32<Tin> /
 // cpu_block_fprop_nhwc_qi32<Tin> (/root/reference/src/conv_types.h:255-285 ->
-// cpu_ref.cpp:36-112, :371-401), cpu_fprop_nhwc (cpu_ref.cpp:116-146) and verify_tensors
+// cpu_ref.cpp:36-112, :371-401), cpu_fprop_nhwc / cpu_bprop_nhwc / cpu_grad_nhwc
+// (cpu_ref.cpp:116-230) and verify_tensors
 // (src/verify.cpp:7-36).
 
 #include <chrono>
@@ -111,6 +112,40 @@ int ref_fprop_f32(const float* x, int n, int h, int w, int c, const float* wt, i
     cpu_fprop_nhwc(xt, ft, p, yt);
     if (seconds) *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
     std::memcpy(y, yt.ptr(), yt.elements() * sizeof(float));
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+// cpu_bprop_nhwc (cpu_ref.cpp:150-190) / cpu_grad_nhwc (:192-230) on flat arrays: `a` is dy
+// (op 0, result dx, n x h x w x c) or x (op 1, result dw, KRSC), `b` the filter (op 0) or dy
+// (op 1).
+int ref_backward_f32(int op, const float* a, const float* b, int n, int h, int w, int c, int r, int s, int k,
+                     const int32_t conv[7], float* out, double* seconds) {
+  try {
+    const Conv2DParams p = to_params(conv);
+    const int cg = (p.groups > 0) ? c / p.groups : 0;
+    TensorNHWC xs(n, h, w, c);
+    FilterKRSC fs(r, s, cg, k);
+    const ConvShape sh = infer_conv_shape(xs, fs, p);
+    TensorNHWC dy(n, sh.ho, sh.wo, k);
+    const auto t1 = std::chrono::steady_clock::now();
+    if (op == 0) {
+      std::memcpy(dy.ptr(), a, dy.elements() * sizeof(float));
+      std::memcpy(fs.ptr(), b, fs.elements() * sizeof(float));
+      TensorNHWC dx(n, h, w, c);
+      cpu_bprop_nhwc(dy, fs, p, dx);
+      std::memcpy(out, dx.ptr(), dx.elements() * sizeof(float));
+    } else {
+      std::memcpy(xs.ptr(), a, xs.elements() * sizeof(float));
+      std::memcpy(dy.ptr(), b, dy.elements() * sizeof(float));
+      FilterKRSC dw(r, s, cg, k);
+      cpu_grad_nhwc(xs, dy, p, dw);
+      std::memcpy(out, dw.ptr(), dw.elements() * sizeof(float));
+    }
+    if (seconds) *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
     return 0;
   } catch (const std::exception& e) {
     g_err = e.what();

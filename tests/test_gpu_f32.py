@@ -94,3 +94,25 @@ def test_fp32_unaligned_output_and_empty_image(device):
     ye = M.conv2d_nhwc_f32(xe, we, padding=1)
     torch.cuda.synchronize()
     assert tuple(ye.shape) == (1, 2, 6, 8) and float(ye.abs().max()) == 0.0
+
+
+BACKWARD = [c for c in CASES if c[0] not in ("resnet_like_28x28", "downsample_stride2", "pointwise_1x1")] + [
+    ("resnet_like_28x28_n1_small", 1, 14, 14, 128, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("downsample_stride2_small", 1, 40, 40, 32, 32, 3, 3, (1, 1, 2, 2, 1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", BACKWARD, ids=[c[0] for c in BACKWARD])
+def test_fp32_bprop_and_grad_bit_exact(device, case):
+    _, n, h, w, c, k, r, s, conv = case
+    x, wt = _data(case, 700 + BACKWARD.index(case))
+    ho, wo = oracle.conv_output_shape(n, h, w, c, r, s, k, conv)
+    dy = np.random.default_rng(800 + BACKWARD.index(case)).uniform(-1, 1, size=(n, ho, wo, k)).astype(np.float32)
+    xd, wd, dyd = (torch.from_numpy(a).to(device) for a in (x, wt, dy))
+    dx = torch.full(x.shape, 7.0, dtype=torch.float32, device=device)
+    dw = torch.full(wt.shape, 7.0, dtype=torch.float32, device=device)
+    M.launch_bprop_nhwc(dyd, wd, dx, n, h, w, c, r, s, k, conv)
+    M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dx.cpu().numpy().view(np.uint32), oracle.bprop_f32(dy, wt, x.shape, conv).view(np.uint32))
+    np.testing.assert_array_equal(dw.cpu().numpy().view(np.uint32), oracle.grad_f32(x, dy, wt.shape, conv).view(np.uint32))

@@ -74,3 +74,41 @@ def test_verify_rule_matches_reference():
     for got in cases:
         want = oracle.ref_verify_tensors(a, got, 1e-4, 1e-3)["passed"]
         assert oracle.verify_tensors(a, got) == want, got
+
+
+def _dy(shape, seed):
+    n, h, w, c, k, r, s, conv = shape
+    ho_wo = oracle.conv_output_shape(n, h, w, c, r, s, k, conv)
+    return np.random.default_rng(seed).uniform(-1, 1, size=(n, ho_wo[0], ho_wo[1], k)).astype(np.float32)
+
+
+@pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref (the reference's cpu_ref.cpp) not built here")
+@pytest.mark.parametrize("shape", SHAPES)
+def test_bprop_grad_f32_bit_exact_with_reference_cpu(shape):
+    x, wt = _data(shape, 51 + SHAPES.index(shape))
+    dy = _dy(shape, 71 + SHAPES.index(shape))
+    conv = shape[7]
+    want_dx, _ = oracle.ref_backward_f32("bprop", dy, wt, x.shape, wt.shape, conv)
+    np.testing.assert_array_equal(oracle.bprop_f32(dy, wt, x.shape, conv).view(np.uint32), want_dx.view(np.uint32))
+    want_dw, _ = oracle.ref_backward_f32("grad", x, dy, x.shape, wt.shape, conv)
+    np.testing.assert_array_equal(oracle.grad_f32(x, dy, wt.shape, conv).view(np.uint32), want_dw.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_bprop_grad_f32_against_float64_autograd(shape):
+    x, wt = _data(shape, 91 + SHAPES.index(shape))
+    dy = _dy(shape, 111 + SHAPES.index(shape))
+    ph, pw, sh, sw, dh, dw, g = shape[7]
+    xt = torch.from_numpy(x.astype(np.float64)).permute(0, 3, 1, 2).requires_grad_(True)
+    wtt = torch.from_numpy(wt.astype(np.float64)).permute(0, 3, 1, 2).requires_grad_(True)
+    y = torch.nn.functional.conv2d(torch.nn.functional.pad(xt, (pw, pw, ph, ph)), wtt, stride=(sh, sw),
+                                   dilation=(dh, dw), groups=g)
+    y.backward(torch.from_numpy(dy.astype(np.float64)).permute(0, 3, 1, 2))
+    ref_dx = xt.grad.permute(0, 2, 3, 1).numpy()
+    ref_dw = wtt.grad.permute(0, 2, 3, 1).numpy()
+    terms_dx = shape[5] * shape[6] * (shape[4] // g)
+    terms_dw = dy.shape[0] * dy.shape[1] * dy.shape[2]
+    np.testing.assert_allclose(oracle.bprop_f32(dy, wt, x.shape, shape[7]), ref_dx, rtol=0,
+                               atol=terms_dx * terms_dx * 2.0 ** -24 + 1e-6)
+    np.testing.assert_allclose(oracle.grad_f32(x, dy, wt.shape, shape[7]), ref_dw, rtol=0,
+                               atol=terms_dw * terms_dw * 2.0 ** -24 + 1e-6)
