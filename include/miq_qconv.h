@@ -197,11 +197,14 @@ int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int3
                        int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
 
 /* dx = the gradient of the convolution with respect to x, for output gradient dy (NHWC,
- * n x ho x wo x k) and filter w; dx is NHWC n x h x w x c, fully overwritten.  The loop order
- * and rounding of cpu_bprop_nhwc: its result bit for bit.
+ * n x ho x wo x k) and filter w; dx is NHWC n x h x w x c, fully overwritten.  algo:
+ * MIQ_ALGO_AUTO (the MFMA implicit GEMM for stride 1, (k/groups) % 4 == 0 and 16-byte aligned
+ * dy, else direct), MIQ_ALGO_IGEMM (MIQ_ERR_UNSUPPORTED where it does not apply; agrees with
+ * cpu_bprop_nhwc within abs 1e-4 / rel 1e-3) or MIQ_ALGO_DIRECT (the loop order and rounding
+ * of cpu_bprop_nhwc: its result bit for bit).
  * Replaces launch_bprop_nhwc (/root/reference/src/cuda_kernels.cu:825-872). */
 int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, int32_t h, int32_t wdt, int32_t c,
-                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream);
+                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
 
 /* dw = the gradient with respect to the KRSC filter (k x r x s x c/groups, fully overwritten)
  * for input x and output gradient dy.  The loop order and rounding of cpu_grad_nhwc.

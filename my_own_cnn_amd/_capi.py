@@ -115,7 +115,7 @@ SIGNATURES = {
     "miq_qconv2d_nhwc_i8_dequant": (C.c_int, [C.POINTER(QConvDesc), _P, _P, _P, _P, _P, _P]),
     "miq_bmm_i32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "miq_fprop_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
-    "miq_bprop_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P]),
+    "miq_bprop_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
     "miq_grad_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P]),
 }
 

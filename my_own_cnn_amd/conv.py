@@ -237,11 +237,12 @@ def launch_fprop_nhwc(d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, 
 
 
 def launch_bprop_nhwc(d_dy: Pointer, d_w: Pointer, d_dx: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,
-                      k: int, p=None, stream=None) -> None:
-    """Mirror of launch_bprop_nhwc (conv_types.h:290-292): dx of the fp32 convolution."""
+                      k: int, p=None, algo: str = "auto", stream=None) -> None:
+    """Mirror of launch_bprop_nhwc (conv_types.h:290-292): dx of the fp32 convolution; `algo`
+    'auto', 'igemm' (MFMA, stride 1) or 'direct' (bit-exact with cpu_bprop_nhwc)."""
     params = _as_params(p)
     check(lib().miq_bprop_nhwc_f32(_addr(d_dy), _addr(d_w), _addr(d_dx), n, h, w, c, r, s, k, C.byref(params),
-                                   _stream(stream)), "launch_bprop_nhwc")
+                                   F32_ALGOS[algo], _stream(stream)), "launch_bprop_nhwc")
 
 
 def launch_grad_nhwc(d_x: Pointer, d_dy: Pointer, d_dw: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,

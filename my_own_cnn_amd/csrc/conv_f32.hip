@@ -55,6 +55,8 @@ struct F32Args {
   int nchunks;   // ceil(kdim / 16)
   int tn;        // channel tiles per group
   int tiles;     // pixel tiles * channel tiles per group
+  int ow_taps;   // transposed filter: R * S of the original filter
+  int ow_cg;     // transposed filter: channels per group of the original filter (= Kg of g)
   FastDivM fd_tn, fd_tiles;
 };
 
@@ -76,6 +78,10 @@ struct TapCursor {
   }
 };
 
+// TRANSPOSED: the filter operand is read as the bprop filter of a stride-1 convolution:
+// row j (an input channel of the original) and reduction index (r', s', ko) address
+// w[g Kg + ko][R-1-r'][S-1-s'][j] of the original KRSC filter (`ow_*` extents in F32Args).
+template <bool TRANSPOSED>
 __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a) {
   __shared__ v4f sA[2][kF32BM * 4];
   __shared__ v4f sB[2][kF32BN * 4];
@@ -118,10 +124,23 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const int bp = t & 7;
   const int brow = grp * g.Kg + min(n0 + br, g.Kg - 1);
   const float* wr = a.w + static_cast<size_t>(brow) * a.kdim;
+  // transposed filter: this thread's row is input channel bj of the original filter, its
+  // reduction values (r', s', ko), (r', s', ko + 1) of each chunk tracked by a cursor
+  const int bj = min(n0 + br, g.Kg - 1);
+  const float* wt0 = a.w + static_cast<size_t>(grp) * g.Cg * a.ow_taps * g.Kg + bj;  // (ko = 0, r = s = 0)
+  TapCursor bcur;
+  if constexpr (TRANSPOSED) {
+    const int k = 2 * bp;
+    const int tap = k / g.Cg;
+    bcur.ci = k - tap * g.Cg;
+    bcur.r = tap / g.S;
+    bcur.s = tap - bcur.r * g.S;
+  }
 
   auto load = [&](int c, v4f& va, v2f& vb, bool& oka, bool& okb) {
     if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
       cur.advance(g.Cg, g.S);
+      if constexpr (TRANSPOSED) bcur.advance(g.Cg, g.S);
       ++cur_chunk;
     }
     const int hi = hbase + cur.r * g.dh;
@@ -131,7 +150,15 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     va = *reinterpret_cast<const v4f*>(xn + xo);
     const int kb = c * kF32KC + 2 * bp;
     okb = kb < a.kdim;
-    vb = *reinterpret_cast<const v2f*>(wr + (okb ? kb : 0));
+    if constexpr (TRANSPOSED) {
+      // original filter w[ko][R-1-r'][S-1-s'][bj], ko = bcur.ci (+1); consecutive ko are
+      // a.ow_taps * a.ow_cg floats apart
+      const size_t tap = static_cast<size_t>(g.R - 1 - bcur.r) * g.S + (g.S - 1 - bcur.s);
+      const size_t o = okb ? (static_cast<size_t>(bcur.ci) * a.ow_taps + tap) * a.ow_cg : 0;
+      vb = v2f{wt0[o], wt0[o + static_cast<size_t>(okb) * a.ow_taps * a.ow_cg]};
+    } else {
+      vb = *reinterpret_cast<const v2f*>(wr + (okb ? kb : 0));
+    }
   };
   const int sa_slot = f32_slot(ar, aq);
   const int sb_slot = f32_slot(br, bp >> 1);
@@ -351,9 +378,13 @@ bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string
   return true;
 }
 
-hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {
+namespace {
+hipError_t f32_igemm_launch(const Geom& g, const float* x, const float* w, float* y, bool transposed,
+                            hipStream_t stream) {
   F32Args a;
   a.x = x; a.w = w; a.y = y; a.g = g;
+  a.ow_taps = g.R * g.S;
+  a.ow_cg = g.Kg;
   a.M = g.N * g.Ho * g.Wo;
   a.kdim = g.R * g.S * g.Cg;
   a.nchunks = (a.kdim + kF32KC - 1) / kF32KC;
@@ -362,8 +393,44 @@ hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float
   a.fd_tn = fastdiv_m(a.tn);
   a.fd_tiles = fastdiv_m(a.tiles);
   const unsigned blocks = static_cast<unsigned>(a.tiles) * static_cast<unsigned>(g.G);
-  hipLaunchKernelGGL(f32_igemm_kernel, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+  if (transposed) {
+    hipLaunchKernelGGL(f32_igemm_kernel<true>, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(f32_igemm_kernel<false>, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+  }
   return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {
+  return f32_igemm_launch(g, x, w, y, false, stream);
+}
+
+// The bprop of a stride-1 convolution g as the forward convolution of dy (N x Ho x Wo x K)
+// with the flipped, channel-transposed filter: padding dilation * (R - 1) - pad, stride 1,
+// the same dilation and groups, output N x H x W x C.
+Geom f32_bprop_as_fprop(const Geom& g) {
+  Geom b = g;
+  b.H = g.Ho; b.W = g.Wo; b.C = g.K;
+  b.Ho = g.H; b.Wo = g.W; b.K = g.C;
+  b.ph = g.dh * (g.R - 1) - g.ph;
+  b.pw = g.dw * (g.S - 1) - g.pw;
+  b.Cg = g.Kg; b.Kg = g.Cg;
+  return b;
+}
+
+bool f32_bprop_igemm_eligible(const Geom& g, const void* dy, const void* w, std::string* why) {
+  if (g.sh != 1 || g.sw != 1) {
+    if (why) *why = "fp32 bprop on MFMA needs stride 1";
+    return false;
+  }
+  return f32_igemm_eligible(f32_bprop_as_fprop(g), dy, w, why);
+}
+
+// Rows of the transposed filter are the original's input channels (b.Kg = g.Cg), its reduction
+// (r', s', ko < g.Kg = b.Cg); f32_igemm_launch takes ow_taps = R * S and ow_cg = b.Kg from b.
+hipError_t launch_f32_bprop_igemm(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream) {
+  return f32_igemm_launch(f32_bprop_as_fprop(g), dy, w, dx, true, stream);
 }
 
 hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {

@@ -308,7 +308,7 @@ int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int3
 }
 
 int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, int32_t h, int32_t wdt, int32_t c,
-                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream) {
+                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
   miq::Geom g;
   int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
   if (st != MIQ_OK) return st;
@@ -317,8 +317,20 @@ int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, in
   if (out_elems(g) > 0 && dy == nullptr) return fail(MIQ_ERR_NULL_POINTER, "dy pointer is NULL");
   if (filt_elems(g) > 0 && w == nullptr) return fail(MIQ_ERR_NULL_POINTER, "filter pointer is NULL");
   if (in_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dx has more than 2^32-256 elements");
+  std::string why;
+  bool igemm = false;
+  switch (algo) {
+    case MIQ_ALGO_AUTO: igemm = miq::f32_bprop_igemm_eligible(g, dy, w, nullptr); break;
+    case MIQ_ALGO_DIRECT: igemm = false; break;
+    case MIQ_ALGO_IGEMM:
+      if (!miq::f32_bprop_igemm_eligible(g, dy, w, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      igemm = true;
+      break;
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 bprop algo must be AUTO, DIRECT or IGEMM");
+  }
   if (in_elems(g) == 0) return MIQ_OK;
-  const hipError_t e = miq::launch_f32_bprop_direct(g, dy, w, dx, static_cast<hipStream_t>(stream));
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const hipError_t e = igemm ? miq::launch_f32_bprop_igemm(g, dy, w, dx, hs) : miq::launch_f32_bprop_direct(g, dy, w, dx, hs);
   if (e != hipSuccess) return hip_fail(e, "fp32 bprop launch");
   return MIQ_OK;
 }

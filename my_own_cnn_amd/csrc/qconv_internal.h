@@ -102,6 +102,10 @@ hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float
 hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
 // fp32 dx and dw in the reference CPU loop orders (one thread per output element).
 hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
+// fp32 dx of a stride-1 convolution on the MFMA implicit GEMM (the forward kernel over dy with
+// the flipped, channel-transposed filter): (K/groups) % 4 == 0, 16-byte aligned dy.
+bool f32_bprop_igemm_eligible(const Geom& g, const void* dy, const void* w, std::string* why);
+hipError_t launch_f32_bprop_igemm(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
 hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
 
 // int32 batched GEMM (wrap-around arithmetic) on the int8 matrix cores; extents already

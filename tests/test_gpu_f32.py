@@ -111,8 +111,31 @@ def test_fp32_bprop_and_grad_bit_exact(device, case):
     xd, wd, dyd = (torch.from_numpy(a).to(device) for a in (x, wt, dy))
     dx = torch.full(x.shape, 7.0, dtype=torch.float32, device=device)
     dw = torch.full(wt.shape, 7.0, dtype=torch.float32, device=device)
-    M.launch_bprop_nhwc(dyd, wd, dx, n, h, w, c, r, s, k, conv)
+    M.launch_bprop_nhwc(dyd, wd, dx, n, h, w, c, r, s, k, conv, algo="direct")
     M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv)
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(dx.cpu().numpy().view(np.uint32), oracle.bprop_f32(dy, wt, x.shape, conv).view(np.uint32))
+    want_dx = oracle.bprop_f32(dy, wt, x.shape, conv)
+    np.testing.assert_array_equal(dx.cpu().numpy().view(np.uint32), want_dx.view(np.uint32))
     np.testing.assert_array_equal(dw.cpu().numpy().view(np.uint32), oracle.grad_f32(x, dy, wt.shape, conv).view(np.uint32))
+    # AUTO: the MFMA implicit GEMM over dy with the flipped filter where it applies (stride 1,
+    # (k/groups) % 4 == 0), checked with the reference's verify rule
+    dx.fill_(7.0)
+    M.launch_bprop_nhwc(dyd, wd, dx, n, h, w, c, r, s, k, conv)
+    torch.cuda.synchronize()
+    got = dx.cpu().numpy()
+    assert oracle.verify_tensors(want_dx, got, 1e-4, 1e-3), float(np.abs(got - want_dx).max())
+
+
+def test_fp32_bprop_igemm_applies_at_stride_1_only(device):
+    x, wt = _data(SUITE[0], 9)
+    conv = SUITE[0][8]
+    n, h, w, c = x.shape
+    k, r, s = wt.shape[:3]
+    dy = torch.rand((n, h, w, k), device=device) * 2 - 1
+    dx = torch.empty((n, h, w, c), device=device)
+    wd = torch.from_numpy(wt).to(device)
+    M.launch_bprop_nhwc(dy, wd, dx, n, h, w, c, r, s, k, conv, algo="igemm")
+    torch.cuda.synchronize()
+    assert oracle.verify_tensors(oracle.bprop_f32(dy.cpu().numpy(), wt, x.shape, conv), dx.cpu().numpy())
+    with pytest.raises(M.MiqError, match="stride 1"):
+        M.launch_bprop_nhwc(dy, wd, dx, n, h, w, c, r, s, k, (1, 1, 2, 2, 1, 1, 1), algo="igemm")
