@@ -207,10 +207,13 @@ int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, in
                        int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
 
 /* dw = the gradient with respect to the KRSC filter (k x r x s x c/groups, fully overwritten)
- * for input x and output gradient dy.  The loop order and rounding of cpu_grad_nhwc.
+ * for input x and output gradient dy.  algo: MIQ_ALGO_AUTO / MIQ_ALGO_IGEMM (the MFMA GEMM over
+ * pixels, split over workgroups and summed with float atomics: agrees with cpu_grad_nhwc
+ * within abs 1e-4 / rel 1e-3, not bit for bit, and not run to run) or MIQ_ALGO_DIRECT (the
+ * loop order and rounding of cpu_grad_nhwc: its result bit for bit).
  * Replaces launch_grad_nhwc (/root/reference/src/cuda_kernels.cu:874-937). */
 int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
-                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream);
+                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
 
 /* ---- int32 batched matrix product -------------------------------------------------- */
 /* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and

@@ -116,7 +116,7 @@ SIGNATURES = {
     "miq_bmm_i32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "miq_fprop_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
     "miq_bprop_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
-    "miq_grad_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P]),
+    "miq_grad_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
 }
 
 _lib = None

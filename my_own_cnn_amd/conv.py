@@ -246,11 +246,12 @@ def launch_bprop_nhwc(d_dy: Pointer, d_w: Pointer, d_dx: Pointer, n: int, h: int
 
 
 def launch_grad_nhwc(d_x: Pointer, d_dy: Pointer, d_dw: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,
-                     k: int, p=None, stream=None) -> None:
-    """Mirror of launch_grad_nhwc (conv_types.h:293-295): dw of the fp32 convolution."""
+                     k: int, p=None, algo: str = "auto", stream=None) -> None:
+    """Mirror of launch_grad_nhwc (conv_types.h:293-295): dw of the fp32 convolution; `algo`
+    'auto' / 'igemm' (MFMA, split over pixels) or 'direct' (bit-exact with cpu_grad_nhwc)."""
     params = _as_params(p)
     check(lib().miq_grad_nhwc_f32(_addr(d_x), _addr(d_dy), _addr(d_dw), n, h, w, c, r, s, k, C.byref(params),
-                                  _stream(stream)), "launch_grad_nhwc")
+                                  F32_ALGOS[algo], _stream(stream)), "launch_grad_nhwc")
 
 def conv2d_nhwc_f32(x, w, *, stride=1, padding=0, dilation=1, groups=1, algo="auto", out=None, stream=None):
     """fp32 convolution of device tensors: x (N, H, W, C), w (K, R, S, C/groups) -> (N, Ho, Wo, K)."""

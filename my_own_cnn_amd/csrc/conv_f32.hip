@@ -340,7 +340,238 @@ __global__ void __launch_bounds__(kDirectThreads) f32_grad_direct_kernel(const f
   dw[e] = acc;
 }
 
+// dw on the matrix cores: dw[g Kg + k][j] = sum over pixels p of dy[p][g Kg + k] * col[p][j],
+// j = (r, s, ci) the filter column, col the implicit im2col of x.  A workgroup of 8 waves
+// computes 128 columns x 64 channels over its share of the pixels (chunks of 16), with the
+// fprop kernel's staging, fragment layout and pipeline; the pixel range is split over
+// workgroups and each adds its partial tile into dw (zeroed first) with float atomics.
+struct GradArgs {
+  const float* x;
+  const float* dy;
+  float* dw;
+  Geom g;
+  int P;       // N * Ho * Wo
+  int kdim;    // R * S * Cg
+  int tn;      // channel tiles per group
+  int tiles;   // column tiles * channel tiles per group
+  int cps;     // 16-pixel chunks per split
+  FastDivM fd_tn, fd_tiles, fd_gt;  // gt = G * tiles
+  int gt;
+};
+
+// (n, ho, wo) of pixel index p, advanced one pixel or one chunk at a time
+struct PixCursor {
+  int n, ho, wo;
+  __device__ __forceinline__ void step(const Geom& g) {
+    if (++wo == g.Wo) {
+      wo = 0;
+      if (++ho == g.Ho) {
+        ho = 0;
+        ++n;
+      }
+    }
+  }
+  __device__ __forceinline__ void advance(const Geom& g, int d) {
+    wo += d;
+    while (wo >= g.Wo) {
+      wo -= g.Wo;
+      if (++ho == g.Ho) {
+        ho = 0;
+        ++n;
+      }
+    }
+  }
+};
+
+__global__ void __launch_bounds__(64 * kF32Waves, 1) f32_grad_igemm_kernel(GradArgs a) {
+  __shared__ v4f sA[2][kF32BM * 4];
+  __shared__ v4f sB[2][kF32BN * 4];
+  const Geom& g = a.g;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+
+  const int lin = blockIdx.x;
+  const int split = fdiv(lin, a.fd_gt);
+  const int rem = lin - split * a.gt;
+  const int grp = fdiv(rem, a.fd_tiles);
+  const int rem2 = rem - grp * a.tiles;
+  const int tmi = fdiv(rem2, a.fd_tn);
+  const int tni = rem2 - tmi * a.tn;
+  const int m0 = tmi * kF32BM;
+  const int n0 = tni * kF32BN;
+  const int pb = split * a.cps * kF32KC;
+  const int pe = min(a.P, pb + a.cps * kF32KC);
+  if (pb >= pe) return;  // whole workgroup: an empty split
+  const int nch = (pe - pb + kF32KC - 1) / kF32KC;
+
+  // A: filter column ja (r, s, ci), pixels pb + 16 c + 4 aq + e of chunk c
+  const int ar = t >> 2;
+  const int aq = t & 3;
+  const int ja = min(m0 + ar, a.kdim - 1);
+  const int tap = ja / g.Cg;
+  const int aci = ja - tap * g.Cg;
+  const int ar_ = tap / g.S;
+  const int as_ = tap - ar_ * g.S;
+  const float* xg = a.x + static_cast<size_t>(grp) * g.Cg + aci;
+  PixCursor pc;
+  {
+    const int p0 = min(pb + 4 * aq, a.P - 1);
+    const int hw = g.Ho * g.Wo;
+    pc.n = p0 / hw;
+    const int r0 = p0 - pc.n * hw;
+    pc.ho = r0 / g.Wo;
+    pc.wo = r0 - pc.ho * g.Wo;
+  }
+  int cur_chunk = 0;
+  // B: channel row, pixels pb + 16 c + 2 bp + e
+  const int br = t >> 3;
+  const int bp = t & 7;
+  const int bk = grp * g.Kg + min(n0 + br, g.Kg - 1);
+  const float* dyk = a.dy + bk;
+
+  auto load = [&](int c, v4f& va, v2f& vb, unsigned& oka, bool& okb) {
+    if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
+      pc.advance(g, kF32KC);
+      ++cur_chunk;
+    }
+    PixCursor q = pc;
+    oka = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (e > 0) q.step(g);
+      const int pp = pb + c * kF32KC + 4 * aq + e;
+      const int hi = q.ho * g.sh - g.ph + ar_ * g.dh;
+      const int wi = q.wo * g.sw - g.pw + as_ * g.dw;
+      const bool ok = pp < pe && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
+      oka |= static_cast<unsigned>(ok) << e;
+      const size_t o = ok ? ((static_cast<size_t>(q.n) * g.H + hi) * g.W + wi) * g.C : 0;
+      va[e] = xg[o];
+    }
+    const int pq = pb + c * kF32KC + 2 * bp;
+    okb = pq < pe;  // pe - pb is not always even: the second pixel is checked at staging
+    const size_t ob = static_cast<size_t>(okb ? pq : pb) * g.K;
+    const bool ok2 = pq + 1 < pe;
+    vb = v2f{dyk[ob], dyk[ob + (ok2 ? g.K : 0)]};
+  };
+  const int sa_slot = f32_slot(ar, aq);
+  const int sb_slot = f32_slot(br, bp >> 1);
+  auto stage = [&](int buf, int c, const v4f& va, const v2f& vb, unsigned oka, bool live) {
+    v4f v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (live && ((oka >> e) & 1u)) ? va[e] : 0.f;
+    sA[buf][sa_slot] = v;
+    const int pq = pb + c * kF32KC + 2 * bp;
+    const v2f w2 = v2f{(live && pq < pe) ? vb[0] : 0.f, (live && pq + 1 < pe) ? vb[1] : 0.f};
+    *(reinterpret_cast<v2f*>(&sB[buf][sb_slot]) + (bp & 1)) = w2;
+  };
+
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int fb0 = f32_slot(32 * wn + (lane & 15), lane >> 4);
+  const int fb1 = f32_slot(32 * wn + 16 + (lane & 15), lane >> 4);
+  const int fa0 = f32_slot(32 * wm + (lane & 15), lane >> 4);
+  const int fa1 = f32_slot(32 * wm + 16 + (lane & 15), lane >> 4);
+  v4f acc[2][2];
+#pragma unroll
+  for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+    for (int im = 0; im < 2; ++im) acc[jn][im] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int P2 = kF32Depth;
+  const int last = nch - 1;
+  v4f va[P2];
+  v2f vb[P2];
+  unsigned oka[P2];
+  bool okb[P2];
+#pragma unroll
+  for (int j = 0; j < P2; ++j) load(min(j, last), va[j], vb[j], oka[j], okb[j]);
+  stage(0, 0, va[0], vb[0], oka[0], true);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  for (int c0 = 0; c0 < nch; c0 += P2) {
+#pragma unroll
+    for (int j = 0; j < P2; ++j) {
+      const int c = c0 + j;
+      load(min(c + P2, last), va[j], vb[j], oka[j], okb[j]);
+      const int buf = c & 1;
+      const v4f Bf[2] = {sB[buf][fb0], sB[buf][fb1]};
+      const v4f Af[2] = {sA[buf][fa0], sA[buf][fa1]};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+          for (int im = 0; im < 2; ++im)
+            acc[jn][im] = __builtin_amdgcn_mfma_f32_16x16x4f32(Bf[jn][kk], Af[im][kk], acc[jn][im], 0, 0, 0);
+      const int j1 = (j + 1) % P2;
+      stage(buf ^ 1, min(c + 1, last), va[j1], vb[j1], oka[j1], c + 1 <= last);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+  }
+
+  // lane (c = lane % 16, q = lane / 16) of tile (jn, im): column m0 + 32 wm + 16 im + c,
+  // channels n0 + 32 wn + 16 jn + 4 q .. + 3 of the group
+#pragma unroll
+  for (int jn = 0; jn < 2; ++jn) {
+#pragma unroll
+    for (int im = 0; im < 2; ++im) {
+      const int jcol = m0 + 32 * wm + 16 * im + (lane & 15);
+      const int ch = n0 + 32 * wn + 16 * jn + 4 * (lane >> 4);
+      if (jcol >= a.kdim) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (ch + i < g.Kg)
+          unsafeAtomicAdd(a.dw + static_cast<size_t>(grp * g.Kg + ch + i) * a.kdim + jcol, acc[jn][im][i]);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kDirectThreads) f32_zero_kernel(float* __restrict__ p, long long count) {
+  const long long stride = static_cast<long long>(gridDim.x) * kDirectThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x; i < count; i += stride)
+    p[i] = 0.0f;
+}
+
 }  // namespace
+
+bool f32_grad_igemm_eligible(const Geom& g, std::string* why) {
+  auto no = [&](const char* m) {
+    if (why) *why = m;
+    return false;
+  };
+  const long long px = static_cast<long long>(g.N) * g.Ho * g.Wo;
+  const long long in = static_cast<long long>(g.N) * g.H * g.W * g.C;
+  const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
+  if (px == 0 || in == 0 || kdim == 0 || g.Kg == 0) return no("fp32 grad on MFMA needs non-empty x, dy and dw");
+  if (px >= (1LL << 31) - 64 || kdim >= (1LL << 31) - kF32BM) return no("fp32 grad on MFMA extents exceed int32");
+  const long long tiles = ((kdim + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G;
+  if (tiles > (1LL << 20)) return no("fp32 grad on MFMA: more than 2^20 output tiles");
+  return true;
+}
+
+hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream) {
+  GradArgs a;
+  a.x = x; a.dy = dy; a.dw = dw; a.g = g;
+  a.P = g.N * g.Ho * g.Wo;
+  a.kdim = g.R * g.S * g.Cg;
+  a.tn = (g.Kg + kF32BN - 1) / kF32BN;
+  a.tiles = ((a.kdim + kF32BM - 1) / kF32BM) * a.tn;
+  a.gt = a.tiles * g.G;
+  // about 2048 workgroups, at least 8 chunks (128 pixels) each
+  const long long chunks = (static_cast<long long>(a.P) + kF32KC - 1) / kF32KC;
+  long long splits = std::max(1LL, std::min((2048LL + a.gt - 1) / a.gt, (chunks + 7) / 8));
+  a.cps = static_cast<int>((chunks + splits - 1) / splits);
+  splits = (chunks + a.cps - 1) / a.cps;
+  a.fd_tn = fastdiv_m(a.tn);
+  a.fd_tiles = fastdiv_m(a.tiles);
+  a.fd_gt = fastdiv_m(a.gt);
+  const long long count = static_cast<long long>(g.K) * a.kdim;
+  const unsigned zb = static_cast<unsigned>(std::min<long long>((count + kDirectThreads - 1) / kDirectThreads, 4096));
+  hipLaunchKernelGGL(f32_zero_kernel, dim3(zb), dim3(kDirectThreads), 0, stream, dw, count);
+  const unsigned blocks = static_cast<unsigned>(splits * a.gt);
+  hipLaunchKernelGGL(f32_grad_igemm_kernel, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+  return hipGetLastError();
+}
 
 hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream) {
   const long long total = static_cast<long long>(g.N) * g.H * g.W * g.C;

@@ -74,7 +74,8 @@ void launch_bprop_nhwc(const float* d_dy, const float* d_w, float* d_dx, int n, 
 void launch_grad_nhwc(const float* d_x, const float* d_dy, float* d_dw, int n, int h, int w, int c, int r, int s,
                       int k, const Conv2DParams& p) {
   const miq_conv2d_params cp = to_c(p);
-  throw_on_error(miq_grad_nhwc_f32(d_x, d_dy, d_dw, n, h, w, c, r, s, k, &cp, nullptr), "launch_grad_nhwc");
+  throw_on_error(miq_grad_nhwc_f32(d_x, d_dy, d_dw, n, h, w, c, r, s, k, &cp, MIQ_ALGO_AUTO, nullptr),
+                 "launch_grad_nhwc");
 }
 
 namespace conv_quant_detail {

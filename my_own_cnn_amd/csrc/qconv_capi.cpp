@@ -336,15 +336,27 @@ int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, in
 }
 
 int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
-                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, void* stream) {
+                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
   miq::Geom g;
   int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
   if (st != MIQ_OK) return st;
   st = check_tensors(g, filt_elems(g), x, dw, dy);
   if (st != MIQ_OK) return st;
   if (filt_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dw has more than 2^32-256 elements");
+  std::string why;
+  bool igemm = false;
+  switch (algo) {
+    case MIQ_ALGO_AUTO: igemm = miq::f32_grad_igemm_eligible(g, nullptr); break;
+    case MIQ_ALGO_DIRECT: igemm = false; break;
+    case MIQ_ALGO_IGEMM:
+      if (!miq::f32_grad_igemm_eligible(g, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      igemm = true;
+      break;
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 grad algo must be AUTO, DIRECT or IGEMM");
+  }
   if (filt_elems(g) == 0) return MIQ_OK;
-  const hipError_t e = miq::launch_f32_grad_direct(g, x, dy, dw, static_cast<hipStream_t>(stream));
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const hipError_t e = igemm ? miq::launch_f32_grad_igemm(g, x, dy, dw, hs) : miq::launch_f32_grad_direct(g, x, dy, dw, hs);
   if (e != hipSuccess) return hip_fail(e, "fp32 grad launch");
   return MIQ_OK;
 }

@@ -107,6 +107,10 @@ hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* 
 bool f32_bprop_igemm_eligible(const Geom& g, const void* dy, const void* w, std::string* why);
 hipError_t launch_f32_bprop_igemm(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
 hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
+// fp32 dw on the MFMA (pixel range split over workgroups, partial tiles added into dw with
+// float atomics after a zero fill): any non-empty shape.
+bool f32_grad_igemm_eligible(const Geom& g, std::string* why);
+hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
 
 // int32 batched GEMM (wrap-around arithmetic) on the int8 matrix cores; extents already
 // validated (>= 0), pointers non-null where the extents need them.

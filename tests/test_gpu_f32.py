@@ -112,7 +112,7 @@ def test_fp32_bprop_and_grad_bit_exact(device, case):
     dx = torch.full(x.shape, 7.0, dtype=torch.float32, device=device)
     dw = torch.full(wt.shape, 7.0, dtype=torch.float32, device=device)
     M.launch_bprop_nhwc(dyd, wd, dx, n, h, w, c, r, s, k, conv, algo="direct")
-    M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv)
+    M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv, algo="direct")
     torch.cuda.synchronize()
     want_dx = oracle.bprop_f32(dy, wt, x.shape, conv)
     np.testing.assert_array_equal(dx.cpu().numpy().view(np.uint32), want_dx.view(np.uint32))
@@ -124,6 +124,13 @@ def test_fp32_bprop_and_grad_bit_exact(device, case):
     torch.cuda.synchronize()
     got = dx.cpu().numpy()
     assert oracle.verify_tensors(want_dx, got, 1e-4, 1e-3), float(np.abs(got - want_dx).max())
+    # AUTO grad: the MFMA GEMM over pixels, split over workgroups (atomics), verify rule
+    dw.fill_(7.0)
+    M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv)
+    torch.cuda.synchronize()
+    want_dw = oracle.grad_f32(x, dy, wt.shape, conv)
+    got = dw.cpu().numpy()
+    assert oracle.verify_tensors(want_dw, got, 1e-4, 1e-3), float(np.abs(got - want_dw).max())
 
 
 def test_fp32_bprop_igemm_applies_at_stride_1_only(device):
