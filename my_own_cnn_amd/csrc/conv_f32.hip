@@ -240,17 +240,44 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
 
 constexpr int kDirectThreads = 256;
 
+// Element index -> (outer..., inner) by three launch-constant divisors; below 2^31 elements
+// with the multiply-high division (FastDivM), else in 64-bit arithmetic.
+struct Split3 {
+  FastDivM d0, d1, d2;  // innermost divisor first
+  int v0, v1, v2;
+  __device__ __forceinline__ void apply(long long e, bool small, int& i0, int& i1, int& i2, int& i3) const {
+    if (small) {
+      const int a = static_cast<int>(e);
+      const int q0 = fdiv(a, d0);
+      i0 = a - q0 * v0;
+      const int q1 = fdiv(q0, d1);
+      i1 = q0 - q1 * v1;
+      i3 = fdiv(q1, d2);
+      i2 = q1 - i3 * v2;
+    } else {
+      i0 = static_cast<int>(e % v0);
+      const long long q0 = e / v0;
+      i1 = static_cast<int>(q0 % v1);
+      const long long q1 = q0 / v1;
+      i2 = static_cast<int>(q1 % v2);
+      i3 = static_cast<int>(q1 / v2);
+    }
+  }
+};
+
+inline Split3 make_split3(int v0, int v1, int v2) {
+  return Split3{fastdiv_m(static_cast<uint32_t>(v0)), fastdiv_m(static_cast<uint32_t>(v1)),
+                fastdiv_m(static_cast<uint32_t>(v2)), v0, v1, v2};
+}
+
 __global__ void __launch_bounds__(kDirectThreads) f32_direct_kernel(const float* __restrict__ x,
                                                                     const float* __restrict__ w,
-                                                                    float* __restrict__ y, Geom g, long long total) {
+                                                                    float* __restrict__ y, Geom g, long long total,
+                                                                    Split3 sp) {
   const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
   if (e >= total) return;
-  const int k = static_cast<int>(e % g.K);
-  const long long pix = e / g.K;
-  const int wo = static_cast<int>(pix % g.Wo);
-  const long long tq = pix / g.Wo;
-  const int ho = static_cast<int>(tq % g.Ho);
-  const int n = static_cast<int>(tq / g.Ho);
+  int k, wo, ho, n;
+  sp.apply(e, total < (1LL << 31), k, wo, ho, n);
   const int grp = k / g.Kg;
   const float* wk = w + static_cast<size_t>(k) * g.R * g.S * g.Cg;
   const float* xg = x + static_cast<size_t>(n) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
@@ -275,15 +302,11 @@ __global__ void __launch_bounds__(kDirectThreads) f32_direct_kernel(const float*
 __global__ void __launch_bounds__(kDirectThreads) f32_bprop_direct_kernel(const float* __restrict__ dy,
                                                                           const float* __restrict__ w,
                                                                           float* __restrict__ dx, Geom g,
-                                                                          long long total) {
+                                                                          long long total, Split3 sp) {
   const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
   if (e >= total) return;
-  const int c = static_cast<int>(e % g.C);
-  const long long pix = e / g.C;
-  const int wi = static_cast<int>(pix % g.W);
-  const long long tq = pix / g.W;
-  const int hi = static_cast<int>(tq % g.H);
-  const int n = static_cast<int>(tq / g.H);
+  int c, wi, hi, n;
+  sp.apply(e, total < (1LL << 31), c, wi, hi, n);
   const int grp = c / g.Cg;
   const int ci = c - grp * g.Cg;
   const size_t wstride = static_cast<size_t>(g.R) * g.S * g.Cg;  // between output channels
@@ -578,7 +601,7 @@ hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* 
   if (total == 0) return hipSuccess;
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
   hipLaunchKernelGGL(f32_bprop_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream,
-                     dy, w, dx, g, total);
+                     dy, w, dx, g, total, make_split3(g.C, g.W, g.H));
   return hipGetLastError();
 }
 
@@ -669,7 +692,7 @@ hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, floa
   if (total == 0) return hipSuccess;
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
   hipLaunchKernelGGL(f32_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, x, w,
-                     y, g, total);
+                     y, g, total, make_split3(g.K, g.Wo, g.Ho));
   return hipGetLastError();
 }
 
