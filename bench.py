@@ -3,6 +3,7 @@
     python bench.py [--steps K] [--warmup W] [--config r50_3x3] [--cache cold|warm] [--all]
     python bench.py --bmm [--config r50_3x3_im2col]      # the int32 matrix product instead
     python bench.py --fp32 [--config resnet_like_56x56]  # the fp32 convolution (conv_bench suite)
+    python bench.py --qi32 [--config r50_3x3]            # the reference's float-code API
 
 One step = one fused conv + bias + requantize (+ ReLU) pass of libmiq_qconv over one batch
 of synthetic int8 input (BASELINE.json configs[1] by default: ResNet-50 conv2_x 3x3, N=32)
@@ -53,6 +54,8 @@ def parse():
                     help="measure the int32 batched matrix product (bmm_matmul_i32) instead of the convolution")
     ap.add_argument("--fp32", action="store_true",
                     help="measure the fp32 convolution (launch_fprop_nhwc) on the reference's conv_bench suite")
+    ap.add_argument("--qi32", action="store_true",
+                    help="measure the reference's float-code API (launch_fprop_nhwc_qi32, LinQuantU8) on the workloads")
     ap.add_argument("--op", choices=["fprop", "bprop", "grad"], default="fprop",
                     help="with --fp32: the pass to time (launch_fprop_nhwc / launch_bprop_nhwc / launch_grad_nhwc)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -325,6 +328,77 @@ def bench_fp32(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def bench_qi32(args) -> None:
+    """Times the reference's own entry point, launch_fprop_nhwc_qi32<LinQuantU8>, on the workloads'
+    shapes with uint8 float codes and per-sample zero points (int32 accumulators out); checks
+    image 0 of each against the oracle bit for bit; prints a table on stderr and one JSON line."""
+    import numpy as np
+    import torch
+
+    import my_own_cnn_amd as M
+    import oracle  # checker of the sampled image only
+    from my_own_cnn_amd import workloads as W
+
+    dev = torch.device("cuda:0")
+    rows = []
+    for name, wl in W.WORKLOADS.items():
+        if args.config not in (None, name):
+            continue
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(7)
+        x = torch.randint(0, 256, (wl.n, wl.h, wl.w, wl.c), device=dev, generator=gen).float()
+        w = torch.randint(0, 256, (wl.k, wl.r, wl.s, wl.c // wl.groups), device=dev, generator=gen).float()
+        zp = [int(v) for v in np.random.default_rng(5).integers(0, 256, size=wl.n)]
+        arr = M.qparams_array(M.DataType.LinQuantU8, zp)
+        in_qp = torch.from_numpy(np.frombuffer(arr.tobytes(), np.uint8).copy()).to(dev)
+        farr = M.qparams_array(M.DataType.LinQuantU8, [131])
+        f_qp = torch.from_numpy(np.frombuffer(farr.tobytes(), np.uint8).copy()).to(dev)
+        y = torch.empty((wl.n, wl.ho, wl.wo, wl.k), dtype=torch.int32, device=dev)
+        p = M.Conv2DParams(*wl.conv7)
+        stream = torch.cuda.current_stream()
+
+        def step():
+            M.launch_fprop_nhwc_qi32(M.DataType.LinQuantU8, x, w, y, wl.n, wl.h, wl.w, wl.c, wl.r, wl.s, wl.k, p,
+                                     in_qp, f_qp, stream=stream)
+
+        step()
+        torch.cuda.synchronize()
+        want = oracle.conv_qi32(x[:1].cpu().numpy(), w.cpu().numpy(), wl.conv7, zp[:1], 131)
+        ok = bool(np.array_equal(y[:1].cpu().numpy(), want))
+        for _ in range(args.warmup):
+            step()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(args.steps):
+            step()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        tops = wl.ops / (ms * 1e-3) / 1e12
+        nbytes = 4.0 * (x.numel() + w.numel() + y.numel())
+        kern = "igemm" if (wl.c // wl.groups) % 4 == 0 else "direct"
+        rows.append(dict(name=name, kernel=kern, us=round(ms * 1e3, 2), int32_tops=round(tops, 2),
+                         gbs=round(nbytes / (ms * 1e-3) / 1e9, 1), frac_mfma=round(tops / (PEAK_INT8_TOPS / 16), 4),
+                         verified_image0=ok))
+        del x, w, y
+        torch.cuda.empty_cache()
+    print(f"{'config':10s} {'kernel':7s} {'us':>9s} {'TOPS':>8s} {'GB/s':>8s} {'frac':>6s} exact", file=sys.stderr)
+    for r in rows:
+        print(f"{r['name']:10s} {r['kernel']:7s} {r['us']:9.2f} {r['int32_tops']:8.2f} {r['gbs']:8.1f} "
+              f"{r['frac_mfma']:6.3f} {r['verified_image0']}", file=sys.stderr)
+    head = rows[0]
+    print(json.dumps({
+        "metric": "float-code qi32 conv TOPS (launch_fprop_nhwc_qi32<LinQuantU8>, int32 accumulators)",
+        "value": head["int32_tops"], "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int32", "data": "synthetic",
+        "config": {"workload": head["name"], "kernel": head["kernel"], "timing": "eager back-to-back", "cache": "warm"},
+        "roofline": {"bound": "mfma", "achieved": head["int32_tops"], "peak": PEAK_INT8_TOPS / 16, "unit": "TOPS",
+                     "frac": head["frac_mfma"], "traffic": None},
+        "shapes": rows}), flush=True)
+
+
 def cpu_model() -> str:
     try:
         for ln in open("/proc/cpuinfo"):
@@ -386,6 +460,9 @@ def main():
         return
     if args.fp32:
         bench_fp32(args)
+        return
+    if args.qi32:
+        bench_qi32(args)
         return
     dev = torch.device("cuda:0")
     names = [args.config or W.HEADLINE]

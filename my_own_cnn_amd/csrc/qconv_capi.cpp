@@ -92,7 +92,14 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
     return fail(MIQ_ERR_NULL_POINTER, "quantized fprop requires non-null quantization parameters");
   }
   if (out_elems(g) == 0) return MIQ_OK;
-  const hipError_t e = miq::launch_qi32_direct(g, bg, qk, x, w, y, in_qp, f_qp, static_cast<hipStream_t>(stream));
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  // one filter block (a plain KRSC filter): the MFMA implicit GEMM where it applies
+  if (bg.By == 1 && bg.Bx == 1 && miq::qi32_igemm_eligible(g, x, w, nullptr)) {
+    const hipError_t e = miq::launch_qi32_igemm(g, qk, x, w, y, in_qp, f_qp, hs);
+    if (e != hipSuccess) return hip_fail(e, "qi32 implicit GEMM launch");
+    return MIQ_OK;
+  }
+  const hipError_t e = miq::launch_qi32_direct(g, bg, qk, x, w, y, in_qp, f_qp, hs);
   if (e != hipSuccess) return hip_fail(e, "qi32 direct convolution launch");
   return MIQ_OK;
 }
