@@ -341,13 +341,18 @@ def bench_qi32(args) -> None:
 
     dev = torch.device("cuda:0")
     rows = []
-    for name, wl in W.WORKLOADS.items():
+    # the workloads, then C2 with the reference's blocked-suite filter grids (main.cpp:177-178)
+    cases = [(name, wl, (1, 1)) for name, wl in W.WORKLOADS.items()]
+    cases += [("r50_3x3_b2x2", W.WORKLOADS["r50_3x3"], (2, 2)), ("r50_3x3_b4x4", W.WORKLOADS["r50_3x3"], (4, 4))]
+    for name, wl, (by, bx) in cases:
         if args.config not in (None, name):
             continue
         gen = torch.Generator(device=dev)
         gen.manual_seed(7)
         x = torch.randint(0, 256, (wl.n, wl.h, wl.w, wl.c), device=dev, generator=gen).float()
-        w = torch.randint(0, 256, (wl.k, wl.r, wl.s, wl.c // wl.groups), device=dev, generator=gen).float()
+        wshape = (wl.k, wl.r, wl.s, wl.c // wl.groups) if (by, bx) == (1, 1) else \
+            (wl.k, by, bx, wl.r, wl.s, wl.c // wl.groups)
+        w = torch.randint(0, 256, wshape, device=dev, generator=gen).float()
         zp = [int(v) for v in np.random.default_rng(5).integers(0, 256, size=wl.n)]
         arr = M.qparams_array(M.DataType.LinQuantU8, zp)
         in_qp = torch.from_numpy(np.frombuffer(arr.tobytes(), np.uint8).copy()).to(dev)
@@ -357,13 +362,20 @@ def bench_qi32(args) -> None:
         p = M.Conv2DParams(*wl.conv7)
         stream = torch.cuda.current_stream()
 
+        bp = M.BlockConv2DParams(p, by, bx)
+
         def step():
-            M.launch_fprop_nhwc_qi32(M.DataType.LinQuantU8, x, w, y, wl.n, wl.h, wl.w, wl.c, wl.r, wl.s, wl.k, p,
-                                     in_qp, f_qp, stream=stream)
+            if (by, bx) == (1, 1):
+                M.launch_fprop_nhwc_qi32(M.DataType.LinQuantU8, x, w, y, wl.n, wl.h, wl.w, wl.c, wl.r, wl.s, wl.k, p,
+                                         in_qp, f_qp, stream=stream)
+            else:
+                M.launch_block_fprop_nhwc_qi32(M.DataType.LinQuantU8, x, w, y, wl.n, wl.h, wl.w, wl.c, wl.r, wl.s,
+                                               wl.k, bp, in_qp, f_qp, stream=stream)
 
         step()
         torch.cuda.synchronize()
-        want = oracle.conv_qi32(x[:1].cpu().numpy(), w.cpu().numpy(), wl.conv7, zp[:1], 131)
+        want = oracle.conv_qi32(x[:1].cpu().numpy(), w.cpu().numpy(), wl.conv7, zp[:1], 131,
+                                (0, 0) if (by, bx) == (1, 1) else (by, bx))
         ok = bool(np.array_equal(y[:1].cpu().numpy(), want))
         for _ in range(args.warmup):
             step()

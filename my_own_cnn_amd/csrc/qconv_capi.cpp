@@ -93,9 +93,9 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
   }
   if (out_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  // one filter block (a plain KRSC filter): the MFMA implicit GEMM where it applies
-  if (bg.By == 1 && bg.Bx == 1 && miq::qi32_igemm_eligible(g, x, w, nullptr)) {
-    const hipError_t e = miq::launch_qi32_igemm(g, qk, x, w, y, in_qp, f_qp, hs);
+  // plain or blocked filters: the MFMA implicit GEMM where it applies
+  if (miq::qi32_igemm_eligible(g, bg, x, w, nullptr)) {
+    const hipError_t e = miq::launch_qi32_igemm(g, bg, qk, x, w, y, in_qp, f_qp, hs);
     if (e != hipSuccess) return hip_fail(e, "qi32 implicit GEMM launch");
     return MIQ_OK;
   }

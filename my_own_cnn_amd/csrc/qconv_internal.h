@@ -68,10 +68,10 @@ hipError_t launch_qi32_direct(const Geom& g, const BlockGeom& bg, QpKind qp, con
                               int32_t* y, const void* in_qp, const void* f_qp, hipStream_t stream);
 
 // int32 accumulators on float codes on the int8 matrix cores (digits of the centred codes):
-// plain (unblocked) filters, (C/groups) % 4 == 0, 16-byte aligned x and w, a non-empty image.
-bool qi32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why);
-hipError_t launch_qi32_igemm(const Geom& g, QpKind qp, const float* x, const float* w, int32_t* y, const void* in_qp,
-                             const void* f_qp, hipStream_t stream);
+// plain or blocked filters, (C/groups) % 4 == 0, 16-byte aligned x and w, a non-empty image.
+bool qi32_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, std::string* why);
+hipError_t launch_qi32_igemm(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
+                             const void* in_qp, const void* f_qp, hipStream_t stream);
 
 // int8 VALU direct convolution: any geometry.
 hipError_t launch_i8_direct(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,

@@ -16,6 +16,10 @@
 //     past kdim and rows past M or Kg read a valid address and are zeroed at staging (zero's
 //     digits are zero) or never stored.
 //   - Per-sample zero points are read once per thread (its pixel's sample); the filter's once.
+//   - Blocked filters [K, By, Bx, R, S, C/groups] (launch_block_fprop_nhwc_qi32,
+//     cuda_kernels.cu:1394-1461): a workgroup's pixel tile lies inside one filter block of
+//     bho x bwo output positions (over the batch), and its filter operand is that block's
+//     slice; a plain filter is the case By = Bx = 1.
 
 #include "qconv_device.h"
 
@@ -42,7 +46,10 @@ struct Qi32Args {
   const unsigned char* f_qp;
   Geom g;
   int M, kdim, nchunks, tn, tiles;
-  FastDivM fd_tn, fd_tiles;
+  // filter blocks (By = Bx = 1: a plain KRSC filter): a workgroup's pixels lie in one block of
+  // bho x bwo output positions; M counts the pixels of one block over the batch
+  int By, Bx, bho, bwo, gt;  // gt = tiles * By * Bx
+  FastDivM fd_tn, fd_tiles, fd_gt;
 };
 
 // Per-sample zero point from the raw parameter struct: uint8 at offset 0 of a 12-byte struct
@@ -78,7 +85,7 @@ struct QTapCursor {
 };
 
 template <QpKind Q>
-__global__ void __launch_bounds__(64 * kQWaves, 1) qi32_igemm_kernel(Qi32Args a) {
+__global__ void __launch_bounds__(64 * kQWaves) __attribute__((amdgpu_waves_per_eu(4, 4))) qi32_igemm_kernel(Qi32Args a) {
   __shared__ v4i sA[2][kQBM * 4];
   __shared__ v4i sB[2][kQBN * 4];
   const Geom& g = a.g;
@@ -87,10 +94,14 @@ __global__ void __launch_bounds__(64 * kQWaves, 1) qi32_igemm_kernel(Qi32Args a)
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
 
   const int lin = blockIdx.x;
-  const int grp = fdiv(lin, a.fd_tiles);
-  const int rem = lin - grp * a.tiles;
+  const int grp = fdiv(lin, a.fd_gt);
+  const int remg = lin - grp * a.gt;
+  const int blk = fdiv(remg, a.fd_tiles);
+  const int rem = remg - blk * a.tiles;
   const int tmi = fdiv(rem, a.fd_tn);
   const int tni = rem - tmi * a.tn;
+  const int bby = blk / a.Bx;
+  const int bbx = blk - bby * a.Bx;
   const int m0 = tmi * kQBM;
   const int n0 = tni * kQBN;
 
@@ -98,11 +109,11 @@ __global__ void __launch_bounds__(64 * kQWaves, 1) qi32_igemm_kernel(Qi32Args a)
   const int ar = t >> 2;
   const int aq = t & 3;
   const int pix = min(m0 + ar, a.M - 1);
-  const int hw = g.Ho * g.Wo;
+  const int hw = a.bho * a.bwo;
   const int pn = pix / hw;
   const int prem = pix - pn * hw;
-  const int pho = prem / g.Wo;
-  const int pwo = prem - pho * g.Wo;
+  const int pho = bby * a.bho + prem / a.bwo;
+  const int pwo = bbx * a.bwo + (prem - (prem / a.bwo) * a.bwo);
   const int hbase = pho * g.sh - g.ph;
   const int wbase = pwo * g.sw - g.pw;
   const float* xn = a.x + static_cast<size_t>(pn) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
@@ -121,7 +132,7 @@ __global__ void __launch_bounds__(64 * kQWaves, 1) qi32_igemm_kernel(Qi32Args a)
   const int br = t >> 3;
   const int bp = t & 7;
   const int brow = grp * g.Kg + min(n0 + br, g.Kg - 1);
-  const float* wr = a.w + static_cast<size_t>(brow) * a.kdim;
+  const float* wr = a.w + ((static_cast<size_t>(brow) * a.By + bby) * a.Bx + bbx) * a.kdim;
 
   auto load = [&](int c, v4f& va, v2f& vb, bool& oka, bool& okb) {
     if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
@@ -220,7 +231,11 @@ __global__ void __launch_bounds__(64 * kQWaves, 1) qi32_igemm_kernel(Qi32Args a)
         r[i] = static_cast<int>(v);
       }
       if (m >= a.M) continue;
-      int32_t* yp = a.y + static_cast<size_t>(m) * g.K + static_cast<size_t>(grp) * g.Kg + ch;
+      const int mn = m / hw;
+      const int mr = m - mn * hw;
+      const int mh = mr / a.bwo;
+      const size_t opix = (static_cast<size_t>(mn) * g.Ho + bby * a.bho + mh) * g.Wo + bbx * a.bwo + (mr - mh * a.bwo);
+      int32_t* yp = a.y + opix * g.K + static_cast<size_t>(grp) * g.Kg + ch;
       if (vec && ch + 3 < g.Kg) {
         *reinterpret_cast<v4i*>(yp) = r;
         store_gap(r);
@@ -235,7 +250,7 @@ __global__ void __launch_bounds__(64 * kQWaves, 1) qi32_igemm_kernel(Qi32Args a)
 
 }  // namespace
 
-bool qi32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why) {
+bool qi32_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, std::string* why) {
   auto no = [&](const char* m) {
     if (why) *why = m;
     return false;
@@ -248,25 +263,29 @@ bool qi32_igemm_eligible(const Geom& g, const void* x, const void* w, std::strin
   const long long m = static_cast<long long>(g.N) * g.Ho * g.Wo;
   const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
   if (m >= (1LL << 31) - kQBM || kdim >= (1LL << 31) - kQKC) return no("qi32 implicit GEMM extents exceed int32");
-  const long long tiles = ((m + kQBM - 1) / kQBM) * ((g.Kg + kQBN - 1) / kQBN) * g.G;
+  const long long mb = static_cast<long long>(g.N) * bg.bho * bg.bwo;
+  const long long tiles = ((mb + kQBM - 1) / kQBM) * ((g.Kg + kQBN - 1) / kQBN) * g.G * bg.By * bg.Bx;
   if (tiles > (1LL << 22)) return no("qi32 implicit GEMM grid exceeds 2^22 workgroups");
   return true;
 }
 
-hipError_t launch_qi32_igemm(const Geom& g, QpKind qp, const float* x, const float* w, int32_t* y, const void* in_qp,
-                             const void* f_qp, hipStream_t stream) {
+hipError_t launch_qi32_igemm(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
+                             const void* in_qp, const void* f_qp, hipStream_t stream) {
   Qi32Args a;
   a.x = x; a.w = w; a.y = y; a.g = g;
   a.in_qp = static_cast<const unsigned char*>(in_qp);
   a.f_qp = static_cast<const unsigned char*>(f_qp);
-  a.M = g.N * g.Ho * g.Wo;
+  a.By = bg.By; a.Bx = bg.Bx; a.bho = bg.bho; a.bwo = bg.bwo;
+  a.M = g.N * bg.bho * bg.bwo;
   a.kdim = g.R * g.S * g.Cg;
   a.nchunks = (a.kdim + kQKC - 1) / kQKC;
   a.tn = (g.Kg + kQBN - 1) / kQBN;
   a.tiles = ((a.M + kQBM - 1) / kQBM) * a.tn;
+  a.gt = a.tiles * bg.By * bg.Bx;
   a.fd_tn = fastdiv_m(a.tn);
   a.fd_tiles = fastdiv_m(a.tiles);
-  const unsigned blocks = static_cast<unsigned>(a.tiles) * static_cast<unsigned>(g.G);
+  a.fd_gt = fastdiv_m(a.gt);
+  const unsigned blocks = static_cast<unsigned>(a.gt) * static_cast<unsigned>(g.G);
   if (qp == kQpU8) {
     hipLaunchKernelGGL(qi32_igemm_kernel<kQpU8>, dim3(blocks), dim3(64 * kQWaves), 0, stream, a);
   } else {

@@ -46,3 +46,33 @@ def test_qi32_float_codes_bit_exact(device, case):
                              in_qp, f_qp)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y.cpu().numpy(), want)
+
+
+BLOCKED = [  # kind, n, h, w, c, k, r, s, conv7, (by, bx)
+    ("u8", 2, 12, 12, 16, 32, 3, 3, (1, 1, 1, 1, 1, 1, 1), (2, 2)),
+    ("s5", 1, 16, 16, 32, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), (4, 4)),
+    ("u8", 2, 14, 10, 8, 24, 3, 3, (1, 1, 1, 1, 1, 1, 2), (2, 5)),
+    ("u8", 1, 12, 12, 64, 96, 1, 1, (0, 0, 2, 2, 1, 1, 1), (3, 2)),
+    ("s5", 3, 9, 8, 4, 20, 3, 3, (1, 1, 1, 1, 1, 1, 1), (1, 4)),
+]
+
+
+@pytest.mark.parametrize("case", BLOCKED, ids=[f"{c[0]}_b{c[9][0]}x{c[9][1]}_c{c[4]}g{c[8][6]}" for c in BLOCKED])
+def test_qi32_blocked_filters_bit_exact(device, case):
+    kind, n, h, w, c, k, r, s, conv, (by, bx) = case
+    rng = np.random.default_rng(4500 + BLOCKED.index(case))
+    g = conv[6]
+    lo, hi = (0, 255) if kind == "u8" else (-16, 15)
+    x = rng.uniform(lo, hi, size=(n, h, w, c)).astype(np.float32)
+    wt = rng.uniform(lo, hi, size=(k, by, bx, r, s, c // g)).astype(np.float32)
+    zlo, zhi = (0, 255) if kind == "u8" else (-128, 127)
+    zp = rng.integers(zlo, zhi, size=n, endpoint=True).astype(np.int32)
+    fzp = int(rng.integers(zlo, zhi, endpoint=True))
+    want = oracle.conv_qi32(x, wt, conv, zp, fzp, (by, bx))
+    tin, in_qp = qparams_dev(kind, zp, device)
+    _, f_qp = qparams_dev(kind, [fzp], device)
+    y = torch.full(want.shape, -7, dtype=torch.int32, device=device)
+    bp = M.BlockConv2DParams(M.Conv2DParams(*conv), by, bx)
+    M.launch_block_fprop_nhwc_qi32(tin, dev(x, device), dev(wt, device), y, n, h, w, c, r, s, k, bp, in_qp, f_qp)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), want)
