@@ -389,7 +389,7 @@ def bench_qi32(args) -> None:
         ms = t0.elapsed_time(t1) / args.steps
         tops = wl.ops / (ms * 1e-3) / 1e12
         nbytes = 4.0 * (x.numel() + w.numel() + y.numel())
-        kern = "igemm" if (wl.c // wl.groups) % 4 == 0 else "direct"
+        kern = "igemm" if (wl.c // wl.groups) % 4 == 0 else "igemm-scalar"
         rows.append(dict(name=name, kernel=kern, us=round(ms * 1e3, 2), int32_tops=round(tops, 2),
                          gbs=round(nbytes / (ms * 1e-3) / 1e9, 1), frac_mfma=round(tops / (PEAK_INT8_TOPS / 16), 4),
                          verified_image0=ok))

@@ -68,7 +68,7 @@ hipError_t launch_qi32_direct(const Geom& g, const BlockGeom& bg, QpKind qp, con
                               int32_t* y, const void* in_qp, const void* f_qp, hipStream_t stream);
 
 // int32 accumulators on float codes on the int8 matrix cores (digits of the centred codes):
-// plain or blocked filters, (C/groups) % 4 == 0, 16-byte aligned x and w, a non-empty image.
+// plain or blocked filters, any C/groups, 4-byte aligned x and w, a non-empty image.
 bool qi32_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, std::string* why);
 hipError_t launch_qi32_igemm(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
                              const void* in_qp, const void* f_qp, hipStream_t stream);

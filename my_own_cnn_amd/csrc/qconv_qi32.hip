@@ -7,7 +7,8 @@
 //
 // qi32_igemm_kernel: an implicit GEMM whose staging is that of the fp32 implicit GEMM (rows:
 // output pixels and one group's output channels; reduction over (r, s, ci) in chunks of 16,
-// gathered as float4 of 4 channels of one tap, C/groups % 4 == 0) and whose arithmetic is that
+// gathered as float4 of 4 channels of one tap where C/groups % 4 == 0, else value by value) and
+// whose arithmetic is that
 // of the int32 batched GEMM: every centred code is split into balanced base-256 digits
 // (w = (u + 0x808080) ^ 0x808080), and four shift groups of v_mfma_i32_16x16x64_i8 over the
 // digit bytes (the filter's byte-reversed and shifted) give the exact wrapped sums.
@@ -72,6 +73,15 @@ __device__ __forceinline__ int q_slot(int row, int g) { return 4 * row + (g ^ ((
 
 struct QTapCursor {
   int r, s, ci;
+  __device__ __forceinline__ void step(int Cg, int S) {
+    if (++ci == Cg) {
+      ci = 0;
+      if (++s == S) {
+        s = 0;
+        ++r;
+      }
+    }
+  }
   __device__ __forceinline__ void advance(int Cg, int S) {
     ci += kQKC;
     while (ci >= Cg) {
@@ -84,7 +94,10 @@ struct QTapCursor {
   }
 };
 
-template <QpKind Q>
+// V4: a thread's 4 reduction values are 4 channels of one tap, read as one float4 (C/groups % 4
+// == 0, 16-byte aligned codes); otherwise each value has its own tap and validity and is read
+// alone (any C/groups, e.g. the 3-channel stem), as are the filter's two.
+template <QpKind Q, bool V4>
 __global__ void __launch_bounds__(64 * kQWaves) __attribute__((amdgpu_waves_per_eu(4, 4))) qi32_igemm_kernel(Qi32Args a) {
   __shared__ v4i sA[2][kQBM * 4];
   __shared__ v4i sB[2][kQBN * 4];
@@ -134,30 +147,52 @@ __global__ void __launch_bounds__(64 * kQWaves) __attribute__((amdgpu_waves_per_
   const int brow = grp * g.Kg + min(n0 + br, g.Kg - 1);
   const float* wr = a.w + ((static_cast<size_t>(brow) * a.By + bby) * a.Bx + bbx) * a.kdim;
 
-  auto load = [&](int c, v4f& va, v2f& vb, bool& oka, bool& okb) {
+  // oka / okb: validity bits of the 4 / 2 values (V4: all four share one bit)
+  auto load = [&](int c, v4f& va, v2f& vb, unsigned& oka, unsigned& okb) {
     if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
       cur.advance(g.Cg, g.S);
       ++cur_chunk;
     }
-    const int hi = hbase + cur.r * g.dh;
-    const int wi = wbase + cur.s * g.dw;
-    oka = cur.r < g.R && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
-    const size_t xo = oka ? (static_cast<size_t>(hi) * g.W + wi) * g.C + cur.ci : 0;
-    va = *reinterpret_cast<const v4f*>(xn + xo);
+    if constexpr (V4) {
+      const int hi = hbase + cur.r * g.dh;
+      const int wi = wbase + cur.s * g.dw;
+      const bool ok = cur.r < g.R && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
+      oka = ok ? 0xFu : 0u;
+      const size_t xo = ok ? (static_cast<size_t>(hi) * g.W + wi) * g.C + cur.ci : 0;
+      va = *reinterpret_cast<const v4f*>(xn + xo);
+    } else {
+      QTapCursor q = cur;
+      oka = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (e > 0) q.step(g.Cg, g.S);
+        const int hi = hbase + q.r * g.dh;
+        const int wi = wbase + q.s * g.dw;
+        const bool ok = q.r < g.R && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
+        oka |= static_cast<unsigned>(ok) << e;
+        va[e] = xn[ok ? (static_cast<size_t>(hi) * g.W + wi) * g.C + q.ci : 0];
+      }
+    }
     const int kb = c * kQKC + 2 * bp;
-    okb = kb < a.kdim;
-    vb = *reinterpret_cast<const v2f*>(wr + (okb ? kb : 0));
+    if constexpr (V4) {
+      okb = kb < a.kdim ? 3u : 0u;
+      vb = *reinterpret_cast<const v2f*>(wr + (kb < a.kdim ? kb : 0));
+    } else {
+      okb = static_cast<unsigned>(kb < a.kdim) | (static_cast<unsigned>(kb + 1 < a.kdim) << 1);
+      vb = v2f{wr[(okb & 1u) ? kb : 0], wr[(okb & 2u) ? kb + 1 : 0]};
+    }
   };
   const int sa_slot = q_slot(ar, aq);
   const int sb_slot = q_slot(br, bp >> 1);
-  auto stage = [&](int buf, const v4f& va, const v2f& vb, bool oka, bool okb) {
+  auto stage = [&](int buf, const v4f& va, const v2f& vb, unsigned oka, unsigned okb) {
     v4i da;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) da[e] = oka ? static_cast<int>(centred_digits(va[e], zx)) : 0;
+    for (int e = 0; e < 4; ++e) da[e] = ((oka >> e) & 1u) ? static_cast<int>(centred_digits(va[e], zx)) : 0;
     sA[buf][sa_slot] = da;
-    const v2i db = okb ? v2i{static_cast<int>(__builtin_bswap32(centred_digits(vb[0], zw))),
-                             static_cast<int>(__builtin_bswap32(centred_digits(vb[1], zw)))}
-                       : v2i{0, 0};
+    v2i db;
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      db[e] = ((okb >> e) & 1u) ? static_cast<int>(__builtin_bswap32(centred_digits(vb[e], zw))) : 0;
     *(reinterpret_cast<v2i*>(&sB[buf][sb_slot]) + (bp & 1)) = db;
   };
 
@@ -181,7 +216,7 @@ __global__ void __launch_bounds__(64 * kQWaves) __attribute__((amdgpu_waves_per_
     const int last = nch - 1;
     v4f va[P];
     v2f vb[P];
-    bool oka[P], okb[P];
+    unsigned oka[P], okb[P];
 #pragma unroll
     for (int j = 0; j < P; ++j) load(min(j, last), va[j], vb[j], oka[j], okb[j]);
     stage(0, va[0], vb[0], oka[0], okb[0]);
@@ -207,7 +242,7 @@ __global__ void __launch_bounds__(64 * kQWaves) __attribute__((amdgpu_waves_per_
         }
         const int j1 = (j + 1) % P;
         const bool live = c + 1 <= last;
-        stage(buf ^ 1, va[j1], vb[j1], live && oka[j1], live && okb[j1]);
+        stage(buf ^ 1, va[j1], vb[j1], live ? oka[j1] : 0u, live ? okb[j1] : 0u);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       }
     }
@@ -255,10 +290,9 @@ bool qi32_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* x, cons
     if (why) *why = m;
     return false;
   };
-  if (g.Cg % 4 != 0) return no("qi32 implicit GEMM needs (c/groups) % 4 == 0");
-  if (g.H == 0 || g.W == 0) return no("qi32 implicit GEMM needs a non-empty input image");
-  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(w) & 15u) != 0) {
-    return no("qi32 implicit GEMM needs 16-byte aligned x and w");
+  if (g.H == 0 || g.W == 0 || g.Cg == 0) return no("qi32 implicit GEMM needs a non-empty input image");
+  if ((reinterpret_cast<uintptr_t>(x) & 3u) != 0 || (reinterpret_cast<uintptr_t>(w) & 3u) != 0) {
+    return no("qi32 implicit GEMM needs 4-byte aligned x and w");
   }
   const long long m = static_cast<long long>(g.N) * g.Ho * g.Wo;
   const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
@@ -286,10 +320,15 @@ hipError_t launch_qi32_igemm(const Geom& g, const BlockGeom& bg, QpKind qp, cons
   a.fd_tiles = fastdiv_m(a.tiles);
   a.fd_gt = fastdiv_m(a.gt);
   const unsigned blocks = static_cast<unsigned>(a.gt) * static_cast<unsigned>(g.G);
+  const bool v4 = g.Cg % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+  const dim3 grid(blocks), block(64 * kQWaves);
   if (qp == kQpU8) {
-    hipLaunchKernelGGL(qi32_igemm_kernel<kQpU8>, dim3(blocks), dim3(64 * kQWaves), 0, stream, a);
+    if (v4) hipLaunchKernelGGL((qi32_igemm_kernel<kQpU8, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((qi32_igemm_kernel<kQpU8, false>), grid, block, 0, stream, a);
   } else {
-    hipLaunchKernelGGL(qi32_igemm_kernel<kQpS5>, dim3(blocks), dim3(64 * kQWaves), 0, stream, a);
+    if (v4) hipLaunchKernelGGL((qi32_igemm_kernel<kQpS5, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((qi32_igemm_kernel<kQpS5, false>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }

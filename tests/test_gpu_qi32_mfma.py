@@ -3,8 +3,8 @@ API) on its MFMA implicit GEMM (digits of the centred codes, exact int32 wrap-ar
 the oracle's orc_conv_qi32, which the reference's cpu_fprop_nhwc_qi32 pins bit for bit:
 U8 and S5 parameter layouts, per-sample zero points, fractional codes (truncation), codes far
 outside 8 bits (every digit used, sums wrapping past 2^31), groups, stride, dilation,
-padding, partial tiles, and a shape the MFMA path does not take (c/groups % 4 != 0) served by
-the direct kernel.  Integer results bit-exact."""
+padding, partial tiles, and c/groups % 4 != 0 (the value-by-value gather, as for the 3-channel
+stem).  Integer results bit-exact."""
 import numpy as np
 import pytest
 import torch
@@ -24,7 +24,7 @@ CASES = [
     ("s5", 1, 20, 17, 4, 64, 7, 7, (3, 3, 2, 2, 1, 1, 1), (-16, 15)),
     ("u8", 1, 6, 7, 12, 20, 5, 3, (4, 2, 1, 1, 1, 1, 1), (-3000, 70000)),      # wide codes
     ("u8", 2, 10, 10, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), (-2.0e8, 2.0e8)),   # wrap-around sums
-    ("u8", 1, 9, 9, 6, 8, 3, 3, (1, 1, 1, 1, 1, 1, 1), (0, 255)),              # c % 4 != 0: direct
+    ("u8", 1, 9, 9, 6, 8, 3, 3, (1, 1, 1, 1, 1, 1, 1), (0, 255)),              # c % 4 != 0: value-by-value gather
 ]
 
 
@@ -54,6 +54,7 @@ BLOCKED = [  # kind, n, h, w, c, k, r, s, conv7, (by, bx)
     ("u8", 2, 14, 10, 8, 24, 3, 3, (1, 1, 1, 1, 1, 1, 2), (2, 5)),
     ("u8", 1, 12, 12, 64, 96, 1, 1, (0, 0, 2, 2, 1, 1, 1), (3, 2)),
     ("s5", 3, 9, 8, 4, 20, 3, 3, (1, 1, 1, 1, 1, 1, 1), (1, 4)),
+    ("u8", 2, 16, 16, 3, 64, 7, 7, (3, 3, 2, 2, 1, 1, 1), (2, 2)),   # 3 channels, blocked
 ]
 
 
