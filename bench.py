@@ -279,6 +279,7 @@ def bench_fp32(args) -> None:
         gbs = nbytes / (ms * 1e-3) / 1e9
         frac = tf / PEAK_FP32_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
         algo = ("igemm" if (c // g) % 4 == 0 and args.op == "fprop" else
+                "depthwise" if c == g == k and c % 4 == 0 and args.op == "fprop" else
                 "igemm" if (k // g) % 4 == 0 and sh == sw == 1 and args.op == "bprop" else
                 "igemm" if args.op == "grad" else "direct")
         rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, kernel=algo,

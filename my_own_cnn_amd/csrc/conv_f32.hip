@@ -296,6 +296,50 @@ __global__ void __launch_bounds__(kDirectThreads) f32_direct_kernel(const float*
   y[e] = acc;
 }
 
+// Depthwise fp32 convolution (C/groups == K/groups == 1, C % 4 == 0): one thread per output
+// pixel and 4 consecutive channels, one float4 of the input per tap; the filter is staged in
+// LDS transposed to [tap][channel], so a tap's 4 weights are one 16-byte LDS read.  Each
+// channel's sum runs over (r, s) in the reference loop's order with one multiply and one add
+// per tap, so the result is cpu_fprop_nhwc's bit for bit.
+constexpr int kDwLdsFloats = 8192;  // R * S * C staged per workgroup (32 KB)
+
+__global__ void __launch_bounds__(kDirectThreads) f32_depthwise_kernel(const float* __restrict__ x,
+                                                                       const float* __restrict__ w,
+                                                                       float* __restrict__ y, Geom g, long long total,
+                                                                       Split3 sp) {
+  __shared__ v4f wl[kDwLdsFloats / 4];
+  const int taps = g.R * g.S;
+  float* wf = reinterpret_cast<float*>(wl);
+  for (int i = threadIdx.x; i < taps * g.C; i += kDirectThreads) {  // w[c][t] -> wl[t][c]
+    const int c = i / taps;
+    const int t = i - c * taps;
+    wf[t * g.C + c] = w[i];
+  }
+  __syncthreads();
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;  // after the only barrier
+  int c4, wo, ho, n;
+  sp.apply(e, total < (1LL << 31), c4, wo, ho, n);
+  const int c = 4 * c4;
+  const float* xn = x + static_cast<size_t>(n) * g.H * g.W * g.C + c;
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < g.R; ++r) {
+    const int hi = ho * g.sh - g.ph + r * g.dh;
+    if (hi < 0 || hi >= g.H) continue;
+    for (int s = 0; s < g.S; ++s) {
+      const int wi = wo * g.sw - g.pw + s * g.dw;
+      if (wi < 0 || wi >= g.W) continue;
+      const v4f xv = *reinterpret_cast<const v4f*>(xn + (static_cast<size_t>(hi) * g.W + wi) * g.C);
+      const v4f wv = wl[((r * g.S + s) * g.C + c) >> 2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(xv[j], wv[j]));
+    }
+  }
+  const size_t pix = (static_cast<size_t>(n) * g.Ho + ho) * g.Wo + wo;
+  *reinterpret_cast<v4f*>(y + pix * g.K + c) = acc;
+  store_gap(acc);
+}
+
 // dx of the convolution, the reference's cpu_bprop_nhwc order (cpu_ref.cpp:150-190): one
 // thread per dx element; for each tap (r, s) whose output position ho = (hi + ph - r dh) / sh
 // is whole and in range (likewise wo), acc += dy * w over the group's output channels.
@@ -593,6 +637,20 @@ hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy,
   hipLaunchKernelGGL(f32_zero_kernel, dim3(zb), dim3(kDirectThreads), 0, stream, dw, count);
   const unsigned blocks = static_cast<unsigned>(splits * a.gt);
   hipLaunchKernelGGL(f32_grad_igemm_kernel, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+  return hipGetLastError();
+}
+
+bool f32_depthwise_eligible(const Geom& g, const void* x, const void* y) {
+  return g.Cg == 1 && g.Kg == 1 && g.C % 4 == 0 && static_cast<long long>(g.R) * g.S * g.C <= kDwLdsFloats &&
+         (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+}
+
+hipError_t launch_f32_depthwise(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {
+  const long long total = static_cast<long long>(g.N) * g.Ho * g.Wo * (g.C / 4);
+  if (total == 0) return hipSuccess;
+  const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
+  hipLaunchKernelGGL(f32_depthwise_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, x, w,
+                     y, g, total, make_split3(g.C / 4, g.Wo, g.Ho));
   return hipGetLastError();
 }
 

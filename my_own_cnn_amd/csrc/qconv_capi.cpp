@@ -309,7 +309,14 @@ int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int3
   }
   if (out_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  const hipError_t e = igemm ? miq::launch_f32_igemm(g, x, w, y, hs) : miq::launch_f32_direct(g, x, w, y, hs);
+  hipError_t e;
+  if (igemm) {
+    e = miq::launch_f32_igemm(g, x, w, y, hs);
+  } else if (algo == MIQ_ALGO_AUTO && miq::f32_depthwise_eligible(g, x, y)) {
+    e = miq::launch_f32_depthwise(g, x, w, y, hs);
+  } else {
+    e = miq::launch_f32_direct(g, x, w, y, hs);
+  }
   if (e != hipSuccess) return hip_fail(e, "fp32 convolution launch");
   return MIQ_OK;
 }

@@ -106,6 +106,10 @@ hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t*
 bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why);
 hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
 hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
+// fp32 depthwise (C/groups == K/groups == 1, C % 4 == 0, R*S*C <= 8192, 16-byte aligned x and y),
+// four channels per thread in the reference loop's order: bit-exact like the direct kernel.
+bool f32_depthwise_eligible(const Geom& g, const void* x, const void* y);
+hipError_t launch_f32_depthwise(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
 // fp32 dx and dw in the reference CPU loop orders (one thread per output element).
 hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
 // fp32 dx of a stride-1 convolution on the MFMA implicit GEMM (the forward kernel over dy with

@@ -35,6 +35,7 @@ EDGE = [
     ("7x7_s2_c4", 2, 30, 30, 4, 64, 7, 7, (3, 3, 2, 2, 1, 1, 1)),
     ("k_odd_scalar_store", 1, 10, 10, 8, 30, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
     ("groups3_kg5", 1, 8, 9, 12, 15, 1, 3, (0, 1, 1, 1, 1, 1, 3)),
+    ("depthwise_s2_d2", 2, 15, 13, 36, 36, 3, 5, (2, 3, 2, 1, 2, 1, 36)),
 ]
 CASES = SUITE + EDGE
 
@@ -62,6 +63,8 @@ def test_fp32_conv_matches_reference_cpu(device, case):
     want = oracle.conv_f32(x, wt, conv)
     got = _run(device, x, wt, conv, "auto")
     assert oracle.verify_tensors(want, got, 1e-4, 1e-3), float(np.abs(got - want).max())
+    if conv[6] == case[4] == case[5]:  # depthwise: AUTO's 4-channel kernel keeps the reference order
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
     direct = _run(device, x, wt, conv, "direct")
     np.testing.assert_array_equal(direct.view(np.uint32), want.view(np.uint32))
 
