@@ -456,7 +456,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding of the convolution is described in DESIGN.md, not benchmarked", file=sys.stderr)
+              "the convolution shards on the batch dimension with no exchange; that split is designed, not benchmarked", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
