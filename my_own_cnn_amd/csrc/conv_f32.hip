@@ -81,10 +81,15 @@ struct TapCursor {
 // TRANSPOSED: the filter operand is read as the bprop filter of a stride-1 convolution:
 // row j (an input channel of the original) and reduction index (r', s', ko) address
 // w[g Kg + ko][R-1-r'][S-1-s'][j] of the original KRSC filter (`ow_*` extents in F32Args).
-template <bool TRANSPOSED>
+// BN: channels per workgroup, 64 (128 pixels, waves 4 x 2) or 32 for groups of at most 32
+// output channels (256 pixels, waves 8 x 1; each thread stages two pixel rows, and the waves
+// of threads 256.. load filter rows again without staging them).
+template <bool TRANSPOSED, int BN>
 __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a) {
-  __shared__ v4f sA[2][kF32BM * 4];
-  __shared__ v4f sB[2][kF32BN * 4];
+  constexpr int BM = BN == 64 ? 128 : 256;
+  constexpr int NA = BM / 128;  // pixel rows per thread
+  __shared__ v4f sA[2][BM * 4];
+  __shared__ v4f sB[2][BN * 4];
   const Geom& g = a.g;
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -95,21 +100,26 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const int rem = lin - grp * a.tiles;
   const int tmi = fdiv(rem, a.fd_tn);
   const int tni = rem - tmi * a.tn;
-  const int m0 = tmi * kF32BM;
-  const int n0 = tni * kF32BN;
+  const int m0 = tmi * BM;
+  const int n0 = tni * BN;
 
-  // A: pixel row ar, reduction values 4 aq .. 4 aq + 3 of each chunk
+  // A: pixel rows ar + 128 i, reduction values 4 aq .. 4 aq + 3 of each chunk
   const int ar = t >> 2;
   const int aq = t & 3;
-  const int pix = min(m0 + ar, a.M - 1);
-  const int hw = g.Ho * g.Wo;
-  const int pn = pix / hw;
-  const int prem = pix - pn * hw;
-  const int pho = prem / g.Wo;
-  const int pwo = prem - pho * g.Wo;
-  const int hbase = pho * g.sh - g.ph;
-  const int wbase = pwo * g.sw - g.pw;
-  const float* xn = a.x + static_cast<size_t>(pn) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
+  int hbase[NA], wbase[NA];
+  const float* xn[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int pix = min(m0 + ar + 128 * i, a.M - 1);
+    const int hw = g.Ho * g.Wo;
+    const int pn = pix / hw;
+    const int prem = pix - pn * hw;
+    const int pho = prem / g.Wo;
+    const int pwo = prem - pho * g.Wo;
+    hbase[i] = pho * g.sh - g.ph;
+    wbase[i] = pwo * g.sw - g.pw;
+    xn[i] = a.x + static_cast<size_t>(pn) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
+  }
   TapCursor cur;
   {
     const int k = 4 * aq;
@@ -120,8 +130,9 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   }
   int cur_chunk = 0;
   // B: filter row br (channel of the group), reduction values 2 bp, 2 bp + 1 of each chunk
-  const int br = t >> 3;
+  const int br = (t >> 3) & (BN - 1);
   const int bp = t & 7;
+  const bool b_stager = BN == 64 || t < 8 * BN;  // whole waves
   const int brow = grp * g.Kg + min(n0 + br, g.Kg - 1);
   const float* wr = a.w + static_cast<size_t>(brow) * a.kdim;
   // transposed filter: this thread's row is input channel bj of the original filter, its
@@ -137,17 +148,22 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     bcur.s = tap - bcur.r * g.S;
   }
 
-  auto load = [&](int c, v4f& va, v2f& vb, bool& oka, bool& okb) {
+  auto load = [&](int c, v4f (&va)[NA], v2f& vb, unsigned& oka, bool& okb) {
     if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
       cur.advance(g.Cg, g.S);
       if constexpr (TRANSPOSED) bcur.advance(g.Cg, g.S);
       ++cur_chunk;
     }
-    const int hi = hbase + cur.r * g.dh;
-    const int wi = wbase + cur.s * g.dw;
-    oka = cur.r < g.R && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
-    const size_t xo = oka ? (static_cast<size_t>(hi) * g.W + wi) * g.C + cur.ci : 0;
-    va = *reinterpret_cast<const v4f*>(xn + xo);
+    oka = 0;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int hi = hbase[i] + cur.r * g.dh;
+      const int wi = wbase[i] + cur.s * g.dw;
+      const bool ok = cur.r < g.R && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
+      oka |= static_cast<unsigned>(ok) << i;
+      const size_t xo = ok ? (static_cast<size_t>(hi) * g.W + wi) * g.C + cur.ci : 0;
+      va[i] = *reinterpret_cast<const v4f*>(xn[i] + xo);
+    }
     const int kb = c * kF32KC + 2 * bp;
     okb = kb < a.kdim;
     if constexpr (TRANSPOSED) {
@@ -160,15 +176,15 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
       vb = *reinterpret_cast<const v2f*>(wr + (okb ? kb : 0));
     }
   };
-  const int sa_slot = f32_slot(ar, aq);
   const int sb_slot = f32_slot(br, bp >> 1);
-  auto stage = [&](int buf, const v4f& va, const v2f& vb, bool oka, bool okb) {
-    sA[buf][sa_slot] = oka ? va : v4f{0.f, 0.f, 0.f, 0.f};
-    *(reinterpret_cast<v2f*>(&sB[buf][sb_slot]) + (bp & 1)) = okb ? vb : v2f{0.f, 0.f};
+  auto stage = [&](int buf, const v4f (&va)[NA], const v2f& vb, unsigned oka, bool okb) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) sA[buf][f32_slot(ar + 128 * i, aq)] = ((oka >> i) & 1u) ? va[i] : v4f{0.f, 0.f, 0.f, 0.f};
+    if (b_stager) *(reinterpret_cast<v2f*>(&sB[buf][sb_slot]) + (bp & 1)) = okb ? vb : v2f{0.f, 0.f};
   };
 
-  const int wn = wave & 1;
-  const int wm = wave >> 1;
+  const int wn = BN == 64 ? (wave & 1) : 0;
+  const int wm = BN == 64 ? (wave >> 1) : wave;
   const int fb0 = f32_slot(32 * wn + (lane & 15), lane >> 4);
   const int fb1 = f32_slot(32 * wn + 16 + (lane & 15), lane >> 4);
   const int fa0 = f32_slot(32 * wm + (lane & 15), lane >> 4);
@@ -183,9 +199,10 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const int nch = a.nchunks;
   if (nch > 0) {
     const int last = nch - 1;
-    v4f va[P];
+    v4f va[P][NA];
     v2f vb[P];
-    bool oka[P], okb[P];
+    unsigned oka[P];
+    bool okb[P];
 #pragma unroll
     for (int j = 0; j < P; ++j) load(min(j, last), va[j], vb[j], oka[j], okb[j]);
     stage(0, va[0], vb[0], oka[0], okb[0]);
@@ -208,7 +225,7 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
               acc[jn][im] = __builtin_amdgcn_mfma_f32_16x16x4f32(Bf[jn][kk], Af[im][kk], acc[jn][im], 0, 0, 0);
         const int jn1 = (j + 1) % P;
         const bool live = c + 1 <= last;
-        stage(buf ^ 1, va[jn1], vb[jn1], live && oka[jn1], live && okb[jn1]);
+        stage(buf ^ 1, va[jn1], vb[jn1], live ? oka[jn1] : 0u, live && okb[jn1]);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       }
     }
@@ -700,15 +717,20 @@ hipError_t f32_igemm_launch(const Geom& g, const float* x, const float* w, float
   a.M = g.N * g.Ho * g.Wo;
   a.kdim = g.R * g.S * g.Cg;
   a.nchunks = (a.kdim + kF32KC - 1) / kF32KC;
-  a.tn = (g.Kg + kF32BN - 1) / kF32BN;
-  a.tiles = ((a.M + kF32BM - 1) / kF32BM) * a.tn;
+  const bool narrow = g.Kg <= 32;  // 256 pixels x 32 channels per workgroup
+  const int bm = narrow ? 256 : kF32BM, bn = narrow ? 32 : kF32BN;
+  a.tn = (g.Kg + bn - 1) / bn;
+  a.tiles = ((a.M + bm - 1) / bm) * a.tn;
   a.fd_tn = fastdiv_m(a.tn);
   a.fd_tiles = fastdiv_m(a.tiles);
   const unsigned blocks = static_cast<unsigned>(a.tiles) * static_cast<unsigned>(g.G);
+  const dim3 grid(blocks), block(64 * kF32Waves);
   if (transposed) {
-    hipLaunchKernelGGL(f32_igemm_kernel<true>, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+    if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<true, 32>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((f32_igemm_kernel<true, 64>), grid, block, 0, stream, a);
   } else {
-    hipLaunchKernelGGL(f32_igemm_kernel<false>, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+    if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<false, 32>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((f32_igemm_kernel<false, 64>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }
