@@ -281,6 +281,7 @@ def bench_fp32(args) -> None:
         algo = ("igemm" if (c // g) % 4 == 0 and args.op == "fprop" else
                 "depthwise" if c == g == k and c % 4 == 0 and args.op == "fprop" else
                 "igemm" if (k // g) % 4 == 0 and sh == sw == 1 and args.op == "bprop" else
+                "depthwise" if args.op == "grad" and c == g == k and c % 4 == 0 and r * s_ <= 16 else
                 "igemm" if args.op == "grad" else "direct")
         rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, kernel=algo,
                          us=round(ms * 1e3, 2), tflops=round(tf, 3), gbs=round(gbs, 1), bound=bound,

@@ -357,6 +357,63 @@ __global__ void __launch_bounds__(kDirectThreads) f32_depthwise_kernel(const flo
   store_gap(acc);
 }
 
+// Depthwise fp32 dw (C/groups == K/groups == 1, C % 4 == 0, R*S <= 16): one thread per 4
+// channels and a run of kDwGradPix consecutive output pixels, summing x * dy for all R*S taps
+// in registers (float4 reads of x and dy), then adding its partial sums into dw (zeroed first)
+// with float atomics.  The order of the sums differs from cpu_grad_nhwc's.
+constexpr int kDwGradPix = 128;
+constexpr int kDwGradTaps = 16;
+
+__global__ void __launch_bounds__(kDirectThreads) f32_depthwise_grad_kernel(const float* __restrict__ x,
+                                                                            const float* __restrict__ dy,
+                                                                            float* __restrict__ dw, Geom g, int P,
+                                                                            long long total) {
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;
+  const int c4n = g.C / 4;
+  const int c = 4 * static_cast<int>(e % c4n);
+  const int p0 = static_cast<int>(e / c4n) * kDwGradPix;
+  const int p1 = min(P, p0 + kDwGradPix);
+  const int taps = g.R * g.S;
+  v4f acc[kDwGradTaps];
+#pragma unroll
+  for (int t = 0; t < kDwGradTaps; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int hw = g.Ho * g.Wo;
+  int n = p0 / hw;
+  int ho = (p0 - n * hw) / g.Wo;
+  int wo = p0 - n * hw - ho * g.Wo;
+  for (int p = p0; p < p1; ++p) {
+    const v4f dv = *reinterpret_cast<const v4f*>(dy + static_cast<size_t>(p) * g.K + c);
+    const float* xn = x + static_cast<size_t>(n) * g.H * g.W * g.C + c;
+#pragma unroll
+    for (int t = 0; t < kDwGradTaps; ++t) {
+      if (t < taps) {
+        const int r = t / g.S;
+        const int s = t - r * g.S;
+        const int hi = ho * g.sh - g.ph + r * g.dh;
+        const int wi = wo * g.sw - g.pw + s * g.dw;
+        if (hi >= 0 && hi < g.H && wi >= 0 && wi < g.W) {
+          const v4f xv = *reinterpret_cast<const v4f*>(xn + (static_cast<size_t>(hi) * g.W + wi) * g.C);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[t][j] = __fadd_rn(acc[t][j], __fmul_rn(xv[j], dv[j]));
+        }
+      }
+    }
+    if (++wo == g.Wo) {
+      wo = 0;
+      if (++ho == g.Ho) {
+        ho = 0;
+        ++n;
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kDwGradTaps; ++t)
+    if (t < taps)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) unsafeAtomicAdd(dw + static_cast<size_t>(c + j) * taps + t, acc[t][j]);
+}
+
 // dx of the convolution, the reference's cpu_bprop_nhwc order (cpu_ref.cpp:150-190): one
 // thread per dx element; for each tap (r, s) whose output position ho = (hi + ph - r dh) / sh
 // is whole and in range (likewise wo), acc += dy * w over the group's output channels.
@@ -773,6 +830,25 @@ hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, floa
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
   hipLaunchKernelGGL(f32_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, x, w,
                      y, g, total, make_split3(g.K, g.Wo, g.Ho));
+  return hipGetLastError();
+}
+
+bool f32_depthwise_grad_eligible(const Geom& g, const void* x, const void* dy) {
+  return g.Cg == 1 && g.Kg == 1 && g.C % 4 == 0 && g.R * g.S <= kDwGradTaps && g.R * g.S > 0 && g.H > 0 &&
+         g.W > 0 && static_cast<long long>(g.N) * g.Ho * g.Wo < (1LL << 31) - kDwGradPix &&
+         (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(dy) & 15u) == 0;
+}
+
+hipError_t launch_f32_depthwise_grad(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream) {
+  const int P = g.N * g.Ho * g.Wo;
+  const long long count = static_cast<long long>(g.K) * g.R * g.S;
+  const unsigned zb = static_cast<unsigned>(std::min<long long>((count + kDirectThreads - 1) / kDirectThreads, 4096));
+  hipLaunchKernelGGL(f32_zero_kernel, dim3(zb), dim3(kDirectThreads), 0, stream, dw, count);
+  const long long total = static_cast<long long>((P + kDwGradPix - 1) / kDwGradPix) * (g.C / 4);
+  if (total == 0) return hipGetLastError();
+  const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
+  hipLaunchKernelGGL(f32_depthwise_grad_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream,
+                     x, dy, dw, g, P, total);
   return hipGetLastError();
 }
 

@@ -370,7 +370,14 @@ int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int
   }
   if (filt_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  const hipError_t e = igemm ? miq::launch_f32_grad_igemm(g, x, dy, dw, hs) : miq::launch_f32_grad_direct(g, x, dy, dw, hs);
+  hipError_t e;
+  if (algo == MIQ_ALGO_AUTO && miq::f32_depthwise_grad_eligible(g, x, dy)) {
+    e = miq::launch_f32_depthwise_grad(g, x, dy, dw, hs);
+  } else if (igemm) {
+    e = miq::launch_f32_grad_igemm(g, x, dy, dw, hs);
+  } else {
+    e = miq::launch_f32_grad_direct(g, x, dy, dw, hs);
+  }
   if (e != hipSuccess) return hip_fail(e, "fp32 grad launch");
   return MIQ_OK;
 }

@@ -120,6 +120,10 @@ hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy
 // fp32 dw on the MFMA (pixel range split over workgroups, partial tiles added into dw with
 // float atomics after a zero fill): any non-empty shape.
 bool f32_grad_igemm_eligible(const Geom& g, std::string* why);
+// fp32 depthwise dw (C/groups == K/groups == 1, C % 4 == 0, R*S <= 16, 16-byte aligned x and dy):
+// pixel runs per thread, partial sums added into dw with float atomics after a zero fill.
+bool f32_depthwise_grad_eligible(const Geom& g, const void* x, const void* dy);
+hipError_t launch_f32_depthwise_grad(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
 hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
 
 // int32 batched GEMM (wrap-around arithmetic) on the int8 matrix cores; extents already
