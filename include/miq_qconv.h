@@ -23,6 +23,7 @@
 #define MIQ_QCONV_H_
 
 #include <stdint.h>
+#include <stddef.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -48,9 +49,11 @@ typedef enum miq_algo {
   MIQ_ALGO_BAND = 4    /* int8 MFMA row-band kernel with the filter held in registers: needs
                           (c/groups) % 64 == 0, (k/groups) % 16 == 0, stride_w == 1, output width
                           <= 64, r*s*c/groups <= 576, 16-byte aligned tensors, bias and scales */,
-  MIQ_ALGO_STREAM = 5  /* int8 MFMA row-band kernel with the filter streamed through LDS: needs
+  MIQ_ALGO_STREAM = 5, /* int8 MFMA row-band kernel with the filter streamed through LDS: needs
                           (c/groups) % 64 == 0, (k/groups) % 128 == 0, stride_w <= 4, input rows of a
                           band that fit in LDS, 16-byte aligned tensors, bias and scales */
+  MIQ_ALGO_ATOMIC = 6  /* fp32 grad only: AUTO's kernels with the split partial sums added by float
+                          atomics (no workspace; the summation order varies from run to run) */
 } miq_algo;
 
 /* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */
@@ -207,13 +210,38 @@ int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, in
                        int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
 
 /* dw = the gradient with respect to the KRSC filter (k x r x s x c/groups, fully overwritten)
- * for input x and output gradient dy.  algo: MIQ_ALGO_AUTO / MIQ_ALGO_IGEMM (the MFMA GEMM over
- * pixels, split over workgroups and summed with float atomics: agrees with cpu_grad_nhwc
- * within abs 1e-4 / rel 1e-3, not bit for bit, and not run to run) or MIQ_ALGO_DIRECT (the
- * loop order and rounding of cpu_grad_nhwc: its result bit for bit).
+ * for input x and output gradient dy.  algo:
+ *   MIQ_ALGO_AUTO: the depthwise kernel (c/groups == k/groups == 1, c % 4 == 0, r*s <= 16,
+ *     16-byte aligned x and dy), else the MFMA GEMM over pixels; both split the pixels over
+ *     workgroups and add the split partial sums in a fixed order, so every call gives the same
+ *     bits (as the reference's ordered GEMM does);
+ *   MIQ_ALGO_IGEMM: the MFMA GEMM, ordered (MIQ_ERR_UNSUPPORTED where it does not apply);
+ *   MIQ_ALGO_ATOMIC: AUTO's kernel with the partial sums added into dw by float atomics: no
+ *     workspace, but the bits vary from run to run;
+ *   MIQ_ALGO_DIRECT: the loop order and rounding of cpu_grad_nhwc: its result bit for bit.
+ * The split kernels agree with cpu_grad_nhwc within abs 1e-4 / rel 1e-3, not bit for bit.
+ * The ordered sums need a device workspace: this entry point keeps one per device, allocated
+ * on first use and grown (hipMalloc; a device synchronisation before the old one is freed) as
+ * the reference's static workspace is; calls that overlap on one device share it and race.
  * Replaces launch_grad_nhwc (/root/reference/src/cuda_kernels.cu:874-937). */
 int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
+
+/* Bytes of device workspace miq_grad_nhwc_f32_ws needs for this shape and algo (0 when the
+ * kernel needs none: DIRECT, ATOMIC, or a single split).  No GPU access.  Has no reference
+ * counterpart: it sizes the caller-provided form of launch_grad_nhwc's workspace. */
+int miq_grad_nhwc_f32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                                     const miq_conv2d_params* p, int32_t algo, size_t* bytes);
+
+/* miq_grad_nhwc_f32 with a caller-provided device workspace of at least
+ * miq_grad_nhwc_f32_workspace_size bytes (it may be NULL when that size is 0); allocates
+ * nothing.  Same result bits as miq_grad_nhwc_f32 for the same algo.  The workspace must not
+ * be used by another call until this one's work on `stream` has finished.
+ * Replaces launch_grad_nhwc (/root/reference/src/cuda_kernels.cu:874-937) with the
+ * reference's internal workspace (:155-158, :885-891) passed in instead. */
+int miq_grad_nhwc_f32_ws(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                         int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 /* ---- int32 batched matrix product -------------------------------------------------- */
 /* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and

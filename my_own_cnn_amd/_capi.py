@@ -30,6 +30,7 @@ MIQ_ALGO_IGEMM = 2
 MIQ_ALGO_STEM = 3
 MIQ_ALGO_BAND = 4
 MIQ_ALGO_STREAM = 5
+MIQ_ALGO_ATOMIC = 6  # fp32 grad only
 ALGOS = {"auto": MIQ_ALGO_AUTO, "direct": MIQ_ALGO_DIRECT, "igemm": MIQ_ALGO_IGEMM, "stem": MIQ_ALGO_STEM,
          "band": MIQ_ALGO_BAND, "stream": MIQ_ALGO_STREAM}
 ALGO_NAMES = {v: k for k, v in ALGOS.items()}
@@ -117,6 +118,10 @@ SIGNATURES = {
     "miq_fprop_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
     "miq_bprop_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
     "miq_grad_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
+    "miq_grad_nhwc_f32_workspace_size": (
+        C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, C.POINTER(C.c_size_t)]),
+    "miq_grad_nhwc_f32_ws": (
+        C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P, C.c_size_t, _P]),
 }
 
 _lib = None

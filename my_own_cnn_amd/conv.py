@@ -224,6 +224,7 @@ def qconv2d_nhwc_i8_dequant(x, w, bias, w_scale, *, stride=1, padding=0, dilatio
 
 
 F32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2}
+F32_GRAD_ALGOS = {"auto": 0, "direct": 1, "igemm": 2, "atomic": 6}
 
 
 def launch_fprop_nhwc(d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,
@@ -246,12 +247,32 @@ def launch_bprop_nhwc(d_dy: Pointer, d_w: Pointer, d_dx: Pointer, n: int, h: int
 
 
 def launch_grad_nhwc(d_x: Pointer, d_dy: Pointer, d_dw: Pointer, n: int, h: int, w: int, c: int, r: int, s: int,
-                     k: int, p=None, algo: str = "auto", stream=None) -> None:
+                     k: int, p=None, algo: str = "auto", stream=None, workspace=None) -> None:
     """Mirror of launch_grad_nhwc (conv_types.h:293-295): dw of the fp32 convolution; `algo`
-    'auto' / 'igemm' (MFMA, split over pixels) or 'direct' (bit-exact with cpu_grad_nhwc)."""
+    'auto' / 'igemm' (split over pixels, partial sums added in a fixed order: the same bits on
+    every call), 'atomic' (float-atomic partial sums, no workspace) or 'direct' (bit-exact with
+    cpu_grad_nhwc).  `workspace`: a device buffer of at least grad_workspace_size() bytes,
+    which makes the call allocation-free (miq_grad_nhwc_f32_ws); None uses the library's
+    cached per-device workspace."""
     params = _as_params(p)
-    check(lib().miq_grad_nhwc_f32(_addr(d_x), _addr(d_dy), _addr(d_dw), n, h, w, c, r, s, k, C.byref(params),
-                                  F32_ALGOS[algo], _stream(stream)), "launch_grad_nhwc")
+    a = F32_GRAD_ALGOS[algo]
+    if workspace is None:
+        check(lib().miq_grad_nhwc_f32(_addr(d_x), _addr(d_dy), _addr(d_dw), n, h, w, c, r, s, k, C.byref(params), a,
+                                      _stream(stream)), "launch_grad_nhwc")
+        return
+    nbytes = workspace.numel() * workspace.element_size() if hasattr(workspace, "numel") else int(workspace[1])
+    ptr = _addr(workspace) if hasattr(workspace, "numel") else workspace[0]
+    check(lib().miq_grad_nhwc_f32_ws(_addr(d_x), _addr(d_dy), _addr(d_dw), n, h, w, c, r, s, k, C.byref(params), a,
+                                     ptr, nbytes, _stream(stream)), "launch_grad_nhwc")
+
+
+def grad_workspace_size(n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=None, algo: str = "auto") -> int:
+    """Bytes of device workspace launch_grad_nhwc(..., workspace=...) needs (no GPU access)."""
+    params = _as_params(p)
+    out = C.c_size_t(0)
+    check(lib().miq_grad_nhwc_f32_workspace_size(n, h, w, c, r, s, k, C.byref(params), F32_GRAD_ALGOS[algo],
+                                                 C.byref(out)), "grad_workspace_size")
+    return int(out.value)
 
 def conv2d_nhwc_f32(x, w, *, stride=1, padding=0, dilation=1, groups=1, algo="auto", out=None, stream=None):
     """fp32 convolution of device tensors: x (N, H, W, C), w (K, R, S, C/groups) -> (N, Ho, Wo, K)."""

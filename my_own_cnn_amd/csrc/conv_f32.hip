@@ -359,14 +359,18 @@ __global__ void __launch_bounds__(kDirectThreads) f32_depthwise_kernel(const flo
 
 // Depthwise fp32 dw (C/groups == K/groups == 1, C % 4 == 0, R*S <= 16): one thread per 4
 // channels and a run of kDwGradPix consecutive output pixels, summing x * dy for all R*S taps
-// in registers (float4 reads of x and dy), then adding its partial sums into dw (zeroed first)
-// with float atomics.  The order of the sums differs from cpu_grad_nhwc's.
+// in registers (float4 reads of x and dy).  With `part` the thread stores its partial sums at
+// part[run][c][tap] (every entry of every run is written) and f32_sum_parts_kernel adds the
+// runs in order: the same result on every call.  Without it they are added into dw (zeroed
+// first) with float atomics, whose order varies from run to run.  Either order differs from
+// cpu_grad_nhwc's.
 constexpr int kDwGradPix = 128;
 constexpr int kDwGradTaps = 16;
 
 __global__ void __launch_bounds__(kDirectThreads) f32_depthwise_grad_kernel(const float* __restrict__ x,
                                                                             const float* __restrict__ dy,
-                                                                            float* __restrict__ dw, Geom g, int P,
+                                                                            float* __restrict__ dw,
+                                                                            float* __restrict__ part, Geom g, int P,
                                                                             long long total) {
   const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
   if (e >= total) return;
@@ -407,11 +411,33 @@ __global__ void __launch_bounds__(kDirectThreads) f32_depthwise_grad_kernel(cons
       }
     }
   }
+  if (part != nullptr) {
+    float* pr = part + static_cast<size_t>(p0 / kDwGradPix) * g.C * taps;
+#pragma unroll
+    for (int t = 0; t < kDwGradTaps; ++t)
+      if (t < taps)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pr[static_cast<size_t>(c + j) * taps + t] = acc[t][j];
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < kDwGradTaps; ++t)
     if (t < taps)
 #pragma unroll
       for (int j = 0; j < 4; ++j) unsafeAtomicAdd(dw + static_cast<size_t>(c + j) * taps + t, acc[t][j]);
+}
+
+// dw[i] = part[0][i] + part[1][i] + ... + part[nparts - 1][i], in that order (one thread per
+// element, `count` elements per part): the deterministic sum of the split partial tiles.
+__global__ void __launch_bounds__(kDirectThreads) f32_sum_parts_kernel(const float* __restrict__ part,
+                                                                       float* __restrict__ dw, long long count,
+                                                                       int nparts) {
+  const long long stride = static_cast<long long>(gridDim.x) * kDirectThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x; i < count; i += stride) {
+    float acc = part[i];
+    for (int s = 1; s < nparts; ++s) acc = __fadd_rn(acc, part[static_cast<size_t>(s) * count + i]);
+    dw[i] = acc;
+  }
 }
 
 // dx of the convolution, the reference's cpu_bprop_nhwc order (cpu_ref.cpp:150-190): one
@@ -485,11 +511,14 @@ __global__ void __launch_bounds__(kDirectThreads) f32_grad_direct_kernel(const f
 // j = (r, s, ci) the filter column, col the implicit im2col of x.  A workgroup of 8 waves
 // computes 128 columns x 64 channels over its share of the pixels (chunks of 16), with the
 // fprop kernel's staging, fragment layout and pipeline; the pixel range is split over
-// workgroups and each adds its partial tile into dw (zeroed first) with float atomics.
+// workgroups.  With `part` a workgroup stores its partial tile at part[split] (a dw-shaped
+// slice; with one split that slice is dw itself) and f32_sum_parts_kernel adds the splits in
+// order; without it each adds its tile into dw (zeroed first) with float atomics.
 struct GradArgs {
   const float* x;
   const float* dy;
   float* dw;
+  float* part;  // split partial tiles (splits x K x kdim), or nullptr for float atomics
   Geom g;
   int P;       // N * Ho * Wo
   int kdim;    // R * S * Cg
@@ -543,7 +572,7 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_grad_igemm_kernel(GradA
   const int n0 = tni * kF32BN;
   const int pb = split * a.cps * kF32KC;
   const int pe = min(a.P, pb + a.cps * kF32KC);
-  if (pb >= pe) return;  // whole workgroup: an empty split
+  if (pb >= pe) return;  // whole workgroup: an empty split (the host plans none)
   const int nch = (pe - pb + kF32KC - 1) / kF32KC;
 
   // A: filter column ja (r, s, ci), pixels pb + 16 c + 4 aq + e of chunk c
@@ -659,10 +688,17 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_grad_igemm_kernel(GradA
       const int jcol = m0 + 32 * wm + 16 * im + (lane & 15);
       const int ch = n0 + 32 * wn + 16 * jn + 4 * (lane >> 4);
       if (jcol >= a.kdim) continue;
+      if (a.part != nullptr) {
+        float* pt = a.part + static_cast<size_t>(split) * g.K * a.kdim;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (ch + i < g.Kg)
-          unsafeAtomicAdd(a.dw + static_cast<size_t>(grp * g.Kg + ch + i) * a.kdim + jcol, acc[jn][im][i]);
+        for (int i = 0; i < 4; ++i)
+          if (ch + i < g.Kg) pt[static_cast<size_t>(grp * g.Kg + ch + i) * a.kdim + jcol] = acc[jn][im][i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (ch + i < g.Kg)
+            unsafeAtomicAdd(a.dw + static_cast<size_t>(grp * g.Kg + ch + i) * a.kdim + jcol, acc[jn][im][i]);
+      }
     }
   }
 }
@@ -690,7 +726,44 @@ bool f32_grad_igemm_eligible(const Geom& g, std::string* why) {
   return true;
 }
 
-hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream) {
+namespace {
+
+// Pixel split of the MFMA grad: about `target` workgroups, at least 8 chunks (128 pixels) each,
+// every split non-empty.  The float-atomic form aims at 2048 workgroups; the ordered form at
+// 1024, which halves its partial tiles (workspace and the summing pass).
+struct GradSplit {
+  int cps;           // 16-pixel chunks per split
+  long long splits;  // non-empty splits
+};
+GradSplit grad_split(const Geom& g, bool ordered) {
+  const long long P = static_cast<long long>(g.N) * g.Ho * g.Wo;
+  const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
+  const long long gt = ((kdim + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G;
+  const long long target = ordered ? 1024 : 2048;
+  const long long chunks = (P + kF32KC - 1) / kF32KC;
+  long long splits = std::max(1LL, std::min((target + gt - 1) / gt, (chunks + 7) / 8));
+  GradSplit s;
+  s.cps = static_cast<int>((chunks + splits - 1) / splits);
+  s.splits = (chunks + s.cps - 1) / s.cps;  // every split holds at least one chunk
+  return s;
+}
+
+void launch_sum_parts(const float* part, float* dw, long long count, long long nparts, hipStream_t stream) {
+  const unsigned blocks = static_cast<unsigned>(std::min<long long>((count + kDirectThreads - 1) / kDirectThreads, 8192));
+  hipLaunchKernelGGL(f32_sum_parts_kernel, dim3(blocks), dim3(kDirectThreads), 0, stream, part, dw, count,
+                     static_cast<int>(nparts));
+}
+
+}  // namespace
+
+size_t f32_grad_igemm_workspace(const Geom& g) {
+  const GradSplit sp = grad_split(g, true);
+  if (sp.splits <= 1) return 0;
+  return static_cast<size_t>(sp.splits) * g.K * g.R * g.S * g.Cg * sizeof(float);
+}
+
+hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, float* ws,
+                                 bool ordered, hipStream_t stream) {
   GradArgs a;
   a.x = x; a.dy = dy; a.dw = dw; a.g = g;
   a.P = g.N * g.Ho * g.Wo;
@@ -698,18 +771,23 @@ hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy,
   a.tn = (g.Kg + kF32BN - 1) / kF32BN;
   a.tiles = ((a.kdim + kF32BM - 1) / kF32BM) * a.tn;
   a.gt = a.tiles * g.G;
-  // about 2048 workgroups, at least 8 chunks (128 pixels) each
-  const long long chunks = (static_cast<long long>(a.P) + kF32KC - 1) / kF32KC;
-  long long splits = std::max(1LL, std::min((2048LL + a.gt - 1) / a.gt, (chunks + 7) / 8));
-  a.cps = static_cast<int>((chunks + splits - 1) / splits);
-  splits = (chunks + a.cps - 1) / a.cps;
+  const GradSplit sp = grad_split(g, ordered);
+  a.cps = sp.cps;
   a.fd_tn = fastdiv_m(a.tn);
   a.fd_tiles = fastdiv_m(a.tiles);
   a.fd_gt = fastdiv_m(a.gt);
   const long long count = static_cast<long long>(g.K) * a.kdim;
+  const unsigned blocks = static_cast<unsigned>(sp.splits * a.gt);
+  if (ordered) {
+    // one split writes dw directly; more write their partial tiles, summed in split order
+    a.part = sp.splits == 1 ? dw : ws;
+    hipLaunchKernelGGL(f32_grad_igemm_kernel, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
+    if (sp.splits > 1) launch_sum_parts(ws, dw, count, sp.splits, stream);
+    return hipGetLastError();
+  }
+  a.part = nullptr;
   const unsigned zb = static_cast<unsigned>(std::min<long long>((count + kDirectThreads - 1) / kDirectThreads, 4096));
   hipLaunchKernelGGL(f32_zero_kernel, dim3(zb), dim3(kDirectThreads), 0, stream, dw, count);
-  const unsigned blocks = static_cast<unsigned>(splits * a.gt);
   hipLaunchKernelGGL(f32_grad_igemm_kernel, dim3(blocks), dim3(64 * kF32Waves), 0, stream, a);
   return hipGetLastError();
 }
@@ -839,16 +917,30 @@ bool f32_depthwise_grad_eligible(const Geom& g, const void* x, const void* dy) {
          (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(dy) & 15u) == 0;
 }
 
-hipError_t launch_f32_depthwise_grad(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream) {
+size_t f32_depthwise_grad_workspace(const Geom& g) {
+  const long long P = static_cast<long long>(g.N) * g.Ho * g.Wo;
+  const long long runs = (P + kDwGradPix - 1) / kDwGradPix;
+  if (runs <= 1) return 0;
+  return static_cast<size_t>(runs) * g.K * g.R * g.S * sizeof(float);
+}
+
+hipError_t launch_f32_depthwise_grad(const Geom& g, const float* x, const float* dy, float* dw, float* ws,
+                                     bool ordered, hipStream_t stream) {
   const int P = g.N * g.Ho * g.Wo;
   const long long count = static_cast<long long>(g.K) * g.R * g.S;
-  const unsigned zb = static_cast<unsigned>(std::min<long long>((count + kDirectThreads - 1) / kDirectThreads, 4096));
-  hipLaunchKernelGGL(f32_zero_kernel, dim3(zb), dim3(kDirectThreads), 0, stream, dw, count);
-  const long long total = static_cast<long long>((P + kDwGradPix - 1) / kDwGradPix) * (g.C / 4);
+  const long long runs = (static_cast<long long>(P) + kDwGradPix - 1) / kDwGradPix;
+  const long long total = runs * (g.C / 4);
+  if (!ordered || runs == 0) {
+    const unsigned zb = static_cast<unsigned>(std::min<long long>((count + kDirectThreads - 1) / kDirectThreads, 4096));
+    hipLaunchKernelGGL(f32_zero_kernel, dim3(zb), dim3(kDirectThreads), 0, stream, dw, count);
+  }
   if (total == 0) return hipGetLastError();
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
+  // ordered: one run writes dw directly; more write their partial sums, added in run order
+  float* part = !ordered ? nullptr : (runs == 1 ? dw : ws);
   hipLaunchKernelGGL(f32_depthwise_grad_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream,
-                     x, dy, dw, g, P, total);
+                     x, dy, dw, part, g, P, total);
+  if (ordered && runs > 1) launch_sum_parts(ws, dw, count, runs, stream);
   return hipGetLastError();
 }
 

@@ -1,9 +1,11 @@
 // extern "C" entry points of libmiq_qconv: host-side validation, kernel selection and
-// error reporting.  No entry point allocates device memory or touches the GPU before its
-// arguments are validated.
+// error reporting.  No entry point touches the GPU before its arguments are validated.  The
+// only one that allocates device memory is miq_grad_nhwc_f32 (its ordered split sums keep a
+// grow-only workspace per device, as the reference's launch_grad_nhwc does).
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "miq_qconv.h"
@@ -349,37 +351,158 @@ int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, in
   return MIQ_OK;
 }
 
-int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
-                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
-  miq::Geom g;
-  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
-  if (st != MIQ_OK) return st;
-  st = check_tensors(g, filt_elems(g), x, dw, dy);
-  if (st != MIQ_OK) return st;
-  if (filt_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dw has more than 2^32-256 elements");
+}  // extern "C"
+
+namespace {
+
+// The kernel family of an fp32 grad call and the workspace bytes of its ordered sums.
+enum GradKind { kGradDirect, kGradIgemm, kGradDepthwise };
+struct GradChoice {
+  GradKind kind;
+  bool ordered;  // split sums in a fixed order (workspace); false: float atomics
+  size_t ws_bytes;
+};
+
+int grad_choose(const miq::Geom& g, const void* x, const void* dy, int32_t algo, GradChoice* ch) {
   std::string why;
-  bool igemm = false;
   switch (algo) {
-    case MIQ_ALGO_AUTO: igemm = miq::f32_grad_igemm_eligible(g, nullptr); break;
-    case MIQ_ALGO_DIRECT: igemm = false; break;
+    case MIQ_ALGO_AUTO:
+    case MIQ_ALGO_ATOMIC:
+      ch->kind = miq::f32_depthwise_grad_eligible(g, x, dy) ? kGradDepthwise
+                 : miq::f32_grad_igemm_eligible(g, nullptr) ? kGradIgemm
+                                                            : kGradDirect;
+      break;
+    case MIQ_ALGO_DIRECT: ch->kind = kGradDirect; break;
     case MIQ_ALGO_IGEMM:
       if (!miq::f32_grad_igemm_eligible(g, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
-      igemm = true;
+      ch->kind = kGradIgemm;
       break;
-    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 grad algo must be AUTO, DIRECT or IGEMM");
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 grad algo must be AUTO, DIRECT, IGEMM or ATOMIC");
   }
+  ch->ordered = algo != MIQ_ALGO_ATOMIC;
+  ch->ws_bytes = !ch->ordered || filt_elems(g) == 0 ? 0
+                 : ch->kind == kGradIgemm           ? miq::f32_grad_igemm_workspace(g)
+                 : ch->kind == kGradDepthwise       ? miq::f32_depthwise_grad_workspace(g)
+                                                    : 0;
+  return MIQ_OK;
+}
+
+int grad_validate(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                  int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, miq::Geom* g,
+                  GradChoice* ch) {
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, g);
+  if (st != MIQ_OK) return st;
+  st = check_tensors(*g, filt_elems(*g), x, dw, dy);
+  if (st != MIQ_OK) return st;
+  if (filt_elems(*g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dw has more than 2^32-256 elements");
+  return grad_choose(*g, x, dy, algo, ch);
+}
+
+int grad_launch(const miq::Geom& g, const GradChoice& ch, const float* x, const float* dy, float* dw, void* ws,
+                void* stream) {
   if (filt_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
+  float* wsf = static_cast<float*>(ws);
   hipError_t e;
-  if (algo == MIQ_ALGO_AUTO && miq::f32_depthwise_grad_eligible(g, x, dy)) {
-    e = miq::launch_f32_depthwise_grad(g, x, dy, dw, hs);
-  } else if (igemm) {
-    e = miq::launch_f32_grad_igemm(g, x, dy, dw, hs);
-  } else {
-    e = miq::launch_f32_grad_direct(g, x, dy, dw, hs);
+  switch (ch.kind) {
+    case kGradDepthwise: e = miq::launch_f32_depthwise_grad(g, x, dy, dw, wsf, ch.ordered, hs); break;
+    case kGradIgemm: e = miq::launch_f32_grad_igemm(g, x, dy, dw, wsf, ch.ordered, hs); break;
+    default: e = miq::launch_f32_grad_direct(g, x, dy, dw, hs); break;
   }
   if (e != hipSuccess) return hip_fail(e, "fp32 grad launch");
   return MIQ_OK;
+}
+
+// Grow-only device workspace per device for miq_grad_nhwc_f32 (the reference keeps one static
+// workspace for its fp32 path, cuda_kernels.cu:155-158, grown by ensure_capacity).  Growing
+// waits for the device before freeing the old buffer, which earlier launches may still read.
+// Calls that overlap on one device share it and race, as the reference's do.
+struct DeviceWorkspace {
+  std::mutex m;
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+constexpr int kMaxDevices = 64;
+DeviceWorkspace g_grad_ws[kMaxDevices];
+
+int cached_workspace(size_t bytes, void** out) {
+  *out = nullptr;
+  if (bytes == 0) return MIQ_OK;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MIQ_ERR_UNSUPPORTED, "device index beyond the workspace table");
+  DeviceWorkspace& w = g_grad_ws[dev];
+  std::lock_guard<std::mutex> lock(w.m);
+  if (w.bytes < bytes) {
+    if (w.p != nullptr) {
+      e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize before growing the grad workspace");
+      (void)hipFree(w.p);
+      w.p = nullptr;
+      w.bytes = 0;
+    }
+    e = hipMalloc(&w.p, bytes);
+    if (e != hipSuccess) {
+      w.p = nullptr;
+      return hip_fail(e, "hipMalloc of the grad workspace");
+    }
+    w.bytes = bytes;
+  }
+  *out = w.p;
+  return MIQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int miq_grad_nhwc_f32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                                     const miq_conv2d_params* p, int32_t algo, size_t* bytes) {
+  if (bytes == nullptr) return fail(MIQ_ERR_NULL_POINTER, "bytes pointer is NULL");
+  *bytes = 0;
+  miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  // the choice of kernel for AUTO also depends on the alignment of x and dy: report the
+  // larger of the aligned and unaligned choices
+  GradChoice aligned{}, unaligned{};
+  const float* a16 = reinterpret_cast<const float*>(static_cast<uintptr_t>(256));
+  const float* a4 = reinterpret_cast<const float*>(static_cast<uintptr_t>(260));
+  st = grad_choose(g, a16, a16, algo, &aligned);
+  if (st != MIQ_OK) return st;
+  st = grad_choose(g, a4, a4, algo, &unaligned);
+  if (st != MIQ_OK) return st;
+  *bytes = aligned.ws_bytes > unaligned.ws_bytes ? aligned.ws_bytes : unaligned.ws_bytes;
+  return MIQ_OK;
+}
+
+int miq_grad_nhwc_f32_ws(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                         int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  miq::Geom g;
+  GradChoice ch{};
+  int st = grad_validate(x, dy, dw, n, h, wdt, c, r, s, k, p, algo, &g, &ch);
+  if (st != MIQ_OK) return st;
+  if (ch.ws_bytes > 0 && workspace == nullptr) return fail(MIQ_ERR_NULL_POINTER, "workspace pointer is NULL");
+  if (workspace_bytes < ch.ws_bytes) {
+    return fail(MIQ_ERR_INVALID_ARGUMENT, "workspace is smaller than miq_grad_nhwc_f32_workspace_size reports");
+  }
+  return grad_launch(g, ch, x, dy, dw, workspace, stream);
+}
+
+int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                      int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
+  miq::Geom g;
+  GradChoice ch{};
+  int st = grad_validate(x, dy, dw, n, h, wdt, c, r, s, k, p, algo, &g, &ch);
+  if (st != MIQ_OK) return st;
+  void* ws = nullptr;
+  if (filt_elems(g) > 0) {
+    st = cached_workspace(ch.ws_bytes, &ws);
+    if (st != MIQ_OK) return st;
+  }
+  return grad_launch(g, ch, x, dy, dw, ws, stream);
 }
 
 int miq_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,

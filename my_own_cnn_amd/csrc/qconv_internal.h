@@ -117,14 +117,21 @@ hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* 
 bool f32_bprop_igemm_eligible(const Geom& g, const void* dy, const void* w, std::string* why);
 hipError_t launch_f32_bprop_igemm(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
 hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
-// fp32 dw on the MFMA (pixel range split over workgroups, partial tiles added into dw with
-// float atomics after a zero fill): any non-empty shape.
+// fp32 dw on the MFMA (pixel range split over workgroups): any non-empty shape.  ordered: the
+// splits' partial tiles go to `ws` (f32_grad_igemm_workspace bytes, none for one split) and
+// are summed in split order, the same result on every call; otherwise they are added into dw
+// with float atomics after a zero fill (ws unused), whose order varies from run to run.
 bool f32_grad_igemm_eligible(const Geom& g, std::string* why);
+size_t f32_grad_igemm_workspace(const Geom& g);
+hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, float* ws,
+                                 bool ordered, hipStream_t stream);
 // fp32 depthwise dw (C/groups == K/groups == 1, C % 4 == 0, R*S <= 16, 16-byte aligned x and dy):
-// pixel runs per thread, partial sums added into dw with float atomics after a zero fill.
+// pixel runs per thread; ordered: partial sums of every run to `ws`
+// (f32_depthwise_grad_workspace bytes) summed in run order; otherwise float atomics into dw.
 bool f32_depthwise_grad_eligible(const Geom& g, const void* x, const void* dy);
-hipError_t launch_f32_depthwise_grad(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
-hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
+size_t f32_depthwise_grad_workspace(const Geom& g);
+hipError_t launch_f32_depthwise_grad(const Geom& g, const float* x, const float* dy, float* dw, float* ws,
+                                     bool ordered, hipStream_t stream);
 
 // int32 batched GEMM (wrap-around arithmetic) on the int8 matrix cores; extents already
 // validated (>= 0), pointers non-null where the extents need them.

@@ -383,6 +383,9 @@ bool stream_plan(const Geom& g, Epi epi, StreamPlan* p, std::string* why) {
   if (g.Cg % 64 != 0) return no("stream kernel needs (c/groups) % 64 == 0");
   if (g.Kg % 128 != 0) return no("stream kernel needs (k/groups) % 128 == 0");
   if (g.R < 1 || g.S < 1) return no("stream kernel needs a non-empty filter");
+  // the tap walk divides s * dilation_w by the stride and indexes LDS rows with r * dilation_h
+  if (g.sh < 1 || g.sw < 1 || g.dh < 1 || g.dw < 1) return no("stream kernel needs stride and dilation >= 1");
+  if (g.ph < 0 || g.pw < 0) return no("stream kernel needs non-negative padding");
   if (g.sw > 4 || (g.S - 1) * g.dw / g.sw > 16) return no("stream kernel needs stride_w <= 4 and a narrow dilated filter");
   const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
   if (static_cast<long long>(g.H) * g.W * g.C >= (1LL << 30)) return no("stream kernel needs images below 2^30 bytes");

@@ -177,6 +177,22 @@ def test_plan_of_the_workloads(name, algo):
     assert M.plan(d) == algo
 
 
+@pytest.mark.parametrize("dil", [(-1, -1), (1, -1), (-1, 1), (0, 1), (1, 0)])
+def test_plan_never_sends_nonpositive_dilation_to_mfma_kernels(dil):
+    """infer_conv_shape accepts dilation <= 0 (as the reference's does); only the direct
+    kernel walks such taps, so AUTO must resolve there and the MFMA kernels must refuse."""
+    x_shape, w_shape = (1, 8, 8, 64), (128, 3, 3, 64)
+    try:
+        d = M.make_desc(x_shape, w_shape, padding=1, dilation=dil)
+        auto = M.plan(d)
+    except M.MiqError:
+        return  # the shape itself is rejected: nothing runs
+    assert auto == "direct", (dil, auto)
+    for algo in ("band", "stream", "igemm", "stem"):
+        with pytest.raises(M.MiqError):
+            M.plan(M.make_desc(x_shape, w_shape, padding=1, dilation=dil, algo=algo))
+
+
 def test_qparams_byte_layout():
     a = M.qparams_array(M.DataType.LinQuantU8, [37, 66], [0.25, 0.35])
     raw = a.tobytes()
@@ -275,3 +291,28 @@ def test_fp32_conv_dropin_and_validation():
     assert lib.miq_fprop_nhwc_f32(None, p, None, 0, 5, 5, 4, 3, 3, 4, C.byref(ok), 0, None) == _capi.MIQ_OK  # n == 0
     with pytest.raises(M.MiqError, match="stride must be > 0"):
         M.launch_fprop_nhwc(256, 256, 256, 1, 5, 5, 4, 3, 3, 4, (1, 1, 0, 1, 1, 1, 1), stream=0)
+
+
+def test_fp32_grad_workspace_query_and_validation():
+    lib = M.lib()
+    ok = _capi.Conv2DParams(1, 1, 1, 1, 1, 1, 1)
+    out = C.c_size_t(123)
+    # the ordered MFMA grad of the conv_bench 56x56 shape splits its 100352 pixels: a workspace
+    assert lib.miq_grad_nhwc_f32_workspace_size(32, 56, 56, 64, 3, 3, 64, C.byref(ok), 0, C.byref(out)) == 0
+    assert out.value > 0 and out.value % (64 * 576 * 4) == 0
+    for algo in ("atomic", "direct"):  # no partial tiles kept
+        assert M.grad_workspace_size(32, 56, 56, 64, 3, 3, 64, (1, 1, 1, 1, 1, 1, 1), algo) == 0
+    assert M.grad_workspace_size(1, 4, 4, 4, 1, 1, 4, (0, 0, 1, 1, 1, 1, 1)) == 0  # one split writes dw
+    assert lib.miq_grad_nhwc_f32_workspace_size(1, 5, 5, 4, 3, 3, 4, C.byref(ok), 0, None) == _capi.MIQ_ERR_NULL_POINTER
+    assert lib.miq_grad_nhwc_f32_workspace_size(1, 5, 5, 4, 3, 3, 4, C.byref(ok), 9, C.byref(out)) == \
+        _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert b"ATOMIC" in lib.miq_last_error_message()
+    # the caller-workspace form validates before touching the GPU
+    p = C.c_void_p(256)
+    need = M.grad_workspace_size(32, 56, 56, 64, 3, 3, 64, (1, 1, 1, 1, 1, 1, 1))
+    assert lib.miq_grad_nhwc_f32_ws(p, p, p, 32, 56, 56, 64, 3, 3, 64, C.byref(ok), 0, None, need, None) == \
+        _capi.MIQ_ERR_NULL_POINTER
+    assert lib.miq_grad_nhwc_f32_ws(p, p, p, 32, 56, 56, 64, 3, 3, 64, C.byref(ok), 0, p, need - 4, None) == \
+        _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert b"smaller" in lib.miq_last_error_message()
+    assert lib.miq_grad_nhwc_f32_ws(p, p, None, 1, 5, 5, 4, 3, 3, 0, C.byref(ok), 0, None, 0, None) == _capi.MIQ_OK  # k == 0

@@ -149,3 +149,47 @@ def test_fp32_bprop_igemm_applies_at_stride_1_only(device):
     assert oracle.verify_tensors(oracle.bprop_f32(dy.cpu().numpy(), wt, x.shape, conv), dx.cpu().numpy())
     with pytest.raises(M.MiqError, match="stride 1"):
         M.launch_bprop_nhwc(dy, wd, dx, n, h, w, c, r, s, k, (1, 1, 2, 2, 1, 1, 1), algo="igemm")
+
+
+# Shapes with many pixel splits (the MFMA GEMM: several column tiles; depthwise: many runs)
+# so that the ordered sums add hundreds of partial tiles.
+DETERMINISTIC = [
+    ("igemm_56x56_n4", 4, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
+    ("igemm_grouped_g4", 2, 28, 28, 64, 32, 3, 3, (1, 1, 2, 2, 1, 1, 4)),
+    ("depthwise_n4", 4, 56, 56, 128, 128, 3, 3, (1, 1, 1, 1, 1, 1, 128)),
+]
+
+
+@pytest.mark.parametrize("case", DETERMINISTIC, ids=[c[0] for c in DETERMINISTIC])
+def test_fp32_grad_auto_is_deterministic(device, case):
+    """AUTO grad adds the split partial sums in a fixed order: two calls give the same bits,
+    and the caller-workspace form gives those bits too; the float-atomic opt-in stays within
+    the reference's verify rule.  All three agree with cpu_grad_nhwc within that rule."""
+    name, n, h, w, c, k, r, s, conv = case
+    x, wt = _data(case, 900 + DETERMINISTIC.index(case))
+    ho, wo = oracle.conv_output_shape(n, h, w, c, r, s, k, conv)
+    dy = np.random.default_rng(950 + DETERMINISTIC.index(case)).uniform(-1, 1, size=(n, ho, wo, k)).astype(np.float32)
+    xd, dyd = (torch.from_numpy(a).to(device) for a in (x, dy))
+    want = oracle.grad_f32(x, dy, wt.shape, conv)
+    nbytes = M.grad_workspace_size(n, h, w, c, r, s, k, conv)
+    assert nbytes > 0, f"{name}: expected a multi-split shape"
+    outs = []
+    for _ in range(2):
+        dw = torch.full(wt.shape, 7.0, dtype=torch.float32, device=device)
+        M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv)
+        torch.cuda.synchronize()
+        outs.append(dw.cpu().numpy())
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32), err_msg=f"{name}: AUTO twice")
+    assert oracle.verify_tensors(want, outs[0], 1e-4, 1e-3), float(np.abs(outs[0] - want).max())
+    ws = torch.full((nbytes // 4 + 3,), float("nan"), dtype=torch.float32, device=device)
+    dw = torch.full(wt.shape, 7.0, dtype=torch.float32, device=device)
+    M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv, workspace=ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dw.cpu().numpy().view(np.uint32), outs[0].view(np.uint32), err_msg=f"{name}: ws")
+    with pytest.raises(M.MiqError, match="smaller"):
+        M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv, workspace=ws[: nbytes // 8])
+    dw.fill_(7.0)
+    M.launch_grad_nhwc(xd, dyd, dw, n, h, w, c, r, s, k, conv, algo="atomic")
+    torch.cuda.synchronize()
+    got = dw.cpu().numpy()
+    assert oracle.verify_tensors(want, got, 1e-4, 1e-3), float(np.abs(got - want).max())

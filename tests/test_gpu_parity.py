@@ -210,6 +210,19 @@ def test_unaligned_tensors_fall_back_exactly(device):
         M.qconv2d_nhwc_i8_acc32(xv, wd, padding=1, algo="igemm")
 
 
+@pytest.mark.parametrize("dil", [(-1, -1), (1, -1), (-1, 1)])
+def test_nonpositive_dilation_auto_matches_oracle(device, dil):
+    """Negative dilation walks the taps backwards; the reference's CPU definition and
+    infer_conv_shape accept it, so AUTO (which resolves to the direct kernel) must agree."""
+    x = W.fill_i8_uniform(1 * 8 * 8 * 64, 71, -128, 127).reshape(1, 8, 8, 64)
+    w = W.fill_i8_uniform(128 * 3 * 3 * 64, 72, -127, 127).reshape(128, 3, 3, 64)
+    conv = (1, 1, 1, 1, dil[0], dil[1], 1)
+    want = oracle.conv_i8_acc(x, w, conv)
+    y = M.qconv2d_nhwc_i8_acc32(dev(x, device), dev(w, device), **conv_kwargs(conv))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), want)
+
+
 def test_empty_batch(device):
     x = torch.zeros((0, 8, 8, 32), dtype=torch.int8, device=device)
     w = torch.zeros((16, 3, 3, 32), dtype=torch.int8, device=device)

@@ -108,6 +108,30 @@ def test_stride_is_subsampled_stride_one():
     np.testing.assert_array_equal(s2, full[:, ::2, ::2, :])
 
 
+@pytest.mark.parametrize("dil", [(-1, -1), (1, -1), (-1, 1), (-2, 1)])
+def test_negative_dilation_is_flipped_filter(dil):
+    """dilation -d on an axis walks the taps backwards: hi = ho*sh - ph - d*r.  Flipping the
+    filter along that axis and padding by ph + d*(R-1) gives the same taps with dilation +d
+    (and the same output extent), which the float64 convolution pins."""
+    rng = np.random.default_rng(12)
+    x = rng.integers(-128, 128, size=(2, 7, 9, 6)).astype(np.int8)
+    wt = rng.integers(-128, 128, size=(5, 3, 2, 6)).astype(np.int8)
+    dh, dw = dil
+    ph, pw = 1, 1
+    got = oracle.conv_i8_acc(x, wt, (ph, pw, 1, 1, dh, dw, 1))
+    wf = wt[:, ::-1] if dh < 0 else wt
+    wf = wf[:, :, ::-1] if dw < 0 else wf
+    ph2 = ph + (-dh) * (wt.shape[1] - 1) if dh < 0 else ph
+    pw2 = pw + (-dw) * (wt.shape[2] - 1) if dw < 0 else pw
+    want = torch_conv_f64(x, np.ascontiguousarray(wf), (ph2, pw2, 1, 1, abs(dh), abs(dw), 1))
+    # torch pads symmetrically: keep the first Ho x Wo outputs (those hi = ho - ph2 + ...)
+    np.testing.assert_array_equal(got, want[:, :got.shape[1], :got.shape[2]].astype(np.int64))
+    if oracle.ref() is not None:
+        xf, wff = x.astype(np.float32), wt.astype(np.float32)
+        ref, _ = oracle.ref_conv_qi32("s5", xf, wff, (ph, pw, 1, 1, dh, dw, 1), np.zeros(2, np.int32), 0)
+        np.testing.assert_array_equal(got, ref)
+
+
 def test_padding_equals_explicit_zero_border():
     rng = np.random.default_rng(5)
     x = rng.integers(-128, 128, size=(1, 7, 9, 4)).astype(np.int8)
