@@ -243,6 +243,18 @@ int miq_grad_nhwc_f32_ws(const float* x, const float* dy, float* dw, int32_t n, 
                          int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* miq_grad_nhwc_f32 (same algo values, same result bits) without any device allocation: the
+ * ordered split partial sums live in a file-scope device array of the library, 32 MiB per
+ * device, held from the first call on a device until the process ends.  Shapes whose partial
+ * sums need more (miq_grad_nhwc_f32_workspace_size > 33554432 bytes) are rejected with
+ * MIQ_ERR_UNSUPPORTED before anything is enqueued.  Calls that overlap on one device (other
+ * streams or threads) share the array and race.  No reference counterpart: it exists for
+ * callers that cannot allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc). */
+int miq_grad_nhwc_f32_noalloc(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt,
+                              int32_t c, int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo,
+                              void* stream);
+
 /* ---- int32 batched matrix product -------------------------------------------------- */
 /* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and
  * sums, exact for every int32 input.  Row-major, batch strides M*K, K*N and M*N:

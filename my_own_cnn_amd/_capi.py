@@ -120,6 +120,7 @@ SIGNATURES = {
     "miq_grad_nhwc_f32": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
     "miq_grad_nhwc_f32_workspace_size": (
         C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, C.POINTER(C.c_size_t)]),
+    "miq_grad_nhwc_f32_noalloc": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
     "miq_grad_nhwc_f32_ws": (
         C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P, C.c_size_t, _P]),
 }

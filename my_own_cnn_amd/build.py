@@ -32,6 +32,7 @@ SOURCES = [
     "qconv_stream.hip",
     "gemm_i32.hip",
     "conv_f32.hip",
+    "grad_noalloc.hip",
     "qconv_qi32.hip",
     "conv_quant_host.cpp",
     "verify.cpp",

@@ -457,6 +457,25 @@ int cached_workspace(size_t bytes, void** out) {
 
 extern "C" {
 
+}  // extern "C"
+
+namespace miq {
+
+int report_error(int status, const std::string& msg) { return fail(status, msg); }
+
+int grad_f32_check(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r,
+                   int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, size_t* ws_bytes) {
+  miq::Geom g;
+  GradChoice ch{};
+  const int st = grad_validate(x, dy, dw, n, h, wdt, c, r, s, k, p, algo, &g, &ch);
+  *ws_bytes = st == MIQ_OK ? ch.ws_bytes : 0;
+  return st;
+}
+
+}  // namespace miq
+
+extern "C" {
+
 int miq_grad_nhwc_f32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
                                      const miq_conv2d_params* p, int32_t algo, size_t* bytes) {
   if (bytes == nullptr) return fail(MIQ_ERR_NULL_POINTER, "bytes pointer is NULL");

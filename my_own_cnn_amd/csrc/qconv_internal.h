@@ -4,8 +4,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstdint>
 #include <string>
+
+struct miq_conv2d_params;  // include/miq_qconv.h
 
 namespace miq {
 
@@ -129,6 +132,12 @@ hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy,
 // pixel runs per thread; ordered: partial sums of every run to `ws`
 // (f32_depthwise_grad_workspace bytes) summed in run order; otherwise float atomics into dw.
 bool f32_depthwise_grad_eligible(const Geom& g, const void* x, const void* dy);
+// Validation of an fp32 grad call exactly as miq_grad_nhwc_f32_ws does it (status and message
+// left like an entry point's), and the workspace bytes it needs for these pointers.
+int grad_f32_check(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r,
+                   int32_t s, int32_t k, const ::miq_conv2d_params* p, int32_t algo, size_t* ws_bytes);
+// Records `msg` as the calling thread's miq_last_error_message() and returns `status`.
+int report_error(int status, const std::string& msg);
 size_t f32_depthwise_grad_workspace(const Geom& g);
 hipError_t launch_f32_depthwise_grad(const Geom& g, const float* x, const float* dy, float* dw, float* ws,
                                      bool ordered, hipStream_t stream);
