@@ -41,8 +41,8 @@ typedef enum miq_status {
 
 /* Kernel families of the int8 entry points (miq_qconv_desc.algo). */
 typedef enum miq_algo {
-  MIQ_ALGO_AUTO = 0,   /* pick by shape: band kernel, else stream kernel, else implicit GEMM, else stem
-                          kernel for thin C, else direct */
+  MIQ_ALGO_AUTO = 0,   /* pick by shape: band kernel, else flat kernel, else stream kernel, else implicit
+                          GEMM, else stem kernel for thin C, else direct */
   MIQ_ALGO_DIRECT = 1, /* VALU direct convolution: any shape, bandwidth-bound fallback */
   MIQ_ALGO_IGEMM = 2,  /* int8 MFMA implicit GEMM: needs (c/groups) % 16 == 0, 16-byte aligned tensors */
   MIQ_ALGO_STEM = 3,   /* int8 MFMA thin-channel kernel: c/groups < 16, groups == 1 */
@@ -52,8 +52,12 @@ typedef enum miq_algo {
   MIQ_ALGO_STREAM = 5, /* int8 MFMA row-band kernel with the filter streamed through LDS: needs
                           (c/groups) % 64 == 0, (k/groups) % 128 == 0, stride_w <= 4, input rows of a
                           band that fit in LDS, 16-byte aligned tensors, bias and scales */
-  MIQ_ALGO_ATOMIC = 6  /* fp32 grad only: AUTO's kernels with the split partial sums added by float
+  MIQ_ALGO_ATOMIC = 6, /* fp32 grad only: AUTO's kernels with the split partial sums added by float
                           atomics (no workspace; the summation order varies from run to run) */
+  MIQ_ALGO_FLAT = 7    /* int8 MFMA row-band kernel over virtual pixels (rows padded to the input
+                          halo's width), filter held in registers: needs stride 1, (c/groups) % 64
+                          == 0, (k/groups) % 64 == 0, r*s*c/groups <= 576, a band's input rows that
+                          fit in LDS, 16-byte aligned tensors, bias and scales */
 } miq_algo;
 
 /* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */

@@ -31,8 +31,9 @@ MIQ_ALGO_STEM = 3
 MIQ_ALGO_BAND = 4
 MIQ_ALGO_STREAM = 5
 MIQ_ALGO_ATOMIC = 6  # fp32 grad only
+MIQ_ALGO_FLAT = 7
 ALGOS = {"auto": MIQ_ALGO_AUTO, "direct": MIQ_ALGO_DIRECT, "igemm": MIQ_ALGO_IGEMM, "stem": MIQ_ALGO_STEM,
-         "band": MIQ_ALGO_BAND, "stream": MIQ_ALGO_STREAM}
+         "band": MIQ_ALGO_BAND, "stream": MIQ_ALGO_STREAM, "flat": MIQ_ALGO_FLAT}
 ALGO_NAMES = {v: k for k, v in ALGOS.items()}
 
 

@@ -30,6 +30,7 @@ SOURCES = [
     "qconv_stem.hip",
     "qconv_band.hip",
     "qconv_stream.hip",
+    "qconv_flat.hip",
     "gemm_i32.hip",
     "conv_f32.hip",
     "grad_noalloc.hip",

@@ -174,7 +174,7 @@ def make_desc(x_shape, w_shape, *, stride=1, padding=0, dilation=1, groups=1, re
 
 
 def plan(desc: QConvDesc) -> str:
-    """Kernel family ('band', 'igemm', 'stem' or 'direct') the int8 entry points will run."""
+    """Kernel family ('flat', 'band', 'stream', 'igemm', 'stem' or 'direct') the int8 entry points will run."""
     a = C.c_int32()
     check(lib().miq_qconv2d_plan(C.byref(desc), C.byref(a)), "plan")
     return ALGO_NAMES[a.value]

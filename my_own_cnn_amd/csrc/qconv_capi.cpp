@@ -117,6 +117,8 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
     case MIQ_ALGO_AUTO:
       if (miq::band_eligible(*g, x, w, y, rq, epi, nullptr)) {
         *algo = MIQ_ALGO_BAND;
+      } else if (miq::flat_eligible(*g, x, w, y, rq, epi, nullptr)) {
+        *algo = MIQ_ALGO_FLAT;
       } else if (miq::stream_eligible(*g, x, w, y, rq, epi, nullptr)) {
         *algo = MIQ_ALGO_STREAM;
       } else if (miq::igemm_eligible(*g, x, w, y, epi, nullptr)) {
@@ -145,6 +147,10 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
     case MIQ_ALGO_STREAM:
       if (!miq::stream_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       *algo = MIQ_ALGO_STREAM;
+      break;
+    case MIQ_ALGO_FLAT:
+      if (!miq::flat_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_FLAT;
       break;
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
@@ -176,6 +182,7 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
     case MIQ_ALGO_STEM: e = miq::launch_i8_stem(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_BAND: e = miq::launch_i8_band(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_STREAM: e = miq::launch_i8_stream(g, epi, x, w, y, rq, s); break;
+    case MIQ_ALGO_FLAT: e = miq::launch_i8_flat(g, epi, x, w, y, rq, s); break;
     default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");

@@ -40,6 +40,22 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
   return xcd * q + min(xcd, r) + pos;
 }
 
+// s_waitcnt vmcnt(n) for a wave-uniform 0 <= n <= 63 (the counter's full 6 bits: bits 3:0 and
+// 15:14 of the immediate); counts above 63 wait for 63, which is always correct.
+__device__ __forceinline__ void wait_vmcnt63(int n) {
+#define MIQ_VMCNT_CASE(k) \
+  case k: __builtin_amdgcn_s_waitcnt(0xF70 | ((k) & 15) | (((k) >> 4) << 14)); break;
+#define MIQ_VMCNT_CASE8(k) MIQ_VMCNT_CASE(k) MIQ_VMCNT_CASE(k + 1) MIQ_VMCNT_CASE(k + 2) MIQ_VMCNT_CASE(k + 3) \
+  MIQ_VMCNT_CASE(k + 4) MIQ_VMCNT_CASE(k + 5) MIQ_VMCNT_CASE(k + 6) MIQ_VMCNT_CASE(k + 7)
+  switch (n <= 0 ? 0 : (n >= 63 ? 63 : n)) {
+    MIQ_VMCNT_CASE8(0) MIQ_VMCNT_CASE8(8) MIQ_VMCNT_CASE8(16) MIQ_VMCNT_CASE8(24)
+    MIQ_VMCNT_CASE8(32) MIQ_VMCNT_CASE8(40) MIQ_VMCNT_CASE8(48) MIQ_VMCNT_CASE8(56)
+    default: break;
+  }
+#undef MIQ_VMCNT_CASE8
+#undef MIQ_VMCNT_CASE
+}
+
 // s_waitcnt vmcnt(n) for a wave-uniform n; counts above 15 wait for 15 (waiting for more
 // completions than needed is always correct).
 __device__ __forceinline__ void wait_vmcnt(int n) {

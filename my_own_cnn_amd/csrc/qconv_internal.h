@@ -92,6 +92,13 @@ bool band_eligible(const Geom& g, const void* x, const void* w, const void* y, c
 hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
 
+// int8 MFMA row-band kernel over virtual pixels (stride 1), filter in registers:
+// (C/groups) % 64 == 0, (K/groups) % 64 == 0, R*S*C/groups <= 576.
+bool flat_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                   std::string* why);
+hipError_t launch_i8_flat(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                          hipStream_t stream);
+
 // int8 MFMA kernel with the filter streamed through LDS: (C/groups) % 64 == 0,
 // (K/groups) % 128 == 0, stride_w <= 4.
 bool stream_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
