@@ -6,15 +6,20 @@
     python bench.py --qi32 [--config r50_3x3]            # the reference's float-code API
 
 One step = one fused conv + bias + requantize (+ ReLU) pass of libmiq_qconv over one batch
-of synthetic int8 input (BASELINE.json configs[1] by default: ResNet-50 conv2_x 3x3, N=32)
-with inputs already resident in HBM.  Prints ONE JSON line (the driver's contract).
+of synthetic int8 input, with inputs already resident in HBM.  Every BASELINE.json config is
+timed; the headline (configs[1]: ResNet-50 conv2_x 3x3, N=32) is the line's `value`, the
+others are in its "configs" block.  Prints ONE JSON line (the driver's contract).
 
 Timing: W untimed warmup steps, then exactly K steps bracketed by device synchronisation,
 timed with HIP events on the stream the kernels run on.  The K launches are recorded once
 into a HIP graph and replayed, so host launch cost does not gap the GPU; `--eager` times
-plain back-to-back launches instead.  With --cache cold (default) every step reads and
-writes a different buffer set, rotating over more than 256 MB so that the Infinity Cache
-(MALL) holds no step's inputs; --cache warm reuses one set.
+plain back-to-back launches instead.  A bounded spin kernel queued before the start event
+holds the GPU while the host submits the replay, so the region times the K steps' execution
+and not the replay's submission latency (a fixed ~30 us that would otherwise be spread over
+the K steps and dominate at small K).  With --cache cold (default) every timed step reads and
+writes its own buffer set (a pooled buffer of up to 4 GiB, filled by one copy kernel), and a
+512 MiB read just before the timed region leaves no step's data in L2 or the 256 MiB
+Infinity Cache (MALL); --cache warm reuses one set.
 
 cpu_baseline: the reference's own CPU path (cpu_ref.cpp compiled in oracle/_ref, -O3, one
 thread, float codes as the reference stores them) on the full workload, else this
@@ -37,6 +42,8 @@ METRIC = "int8 conv TOPS + % of MI355X int8 MFMA peak, ResNet-50 3x3 layer N=32"
 PEAK_INT8_TOPS = 5000.0   # dense int8 MFMA, MI355X
 PEAK_HBM_GBS = 8000.0
 MALL_BYTES = 256 << 20
+FLUSH_BYTES = 2 * MALL_BYTES   # read before each timed region (cold)
+POOL_BYTES = 4 << 30           # cold buffer pool per config: one input/output set per timed step up to this
 
 
 def parse():
@@ -48,7 +55,7 @@ def parse():
     ap.add_argument("--cache", choices=["cold", "warm"], default="cold")
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--algo", default="auto")
-    ap.add_argument("--all", action="store_true", help="also print a per-config table on stderr")
+    ap.add_argument("--all", action="store_true", help="(kept for old command lines: every config is timed by default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--bmm", action="store_true",
                     help="measure the int32 batched matrix product (bmm_matmul_i32) instead of the convolution")
@@ -61,6 +68,34 @@ def parse():
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB (counter calibration)")
     return ap.parse_args()
+
+
+_SLEEP_CYCLES_PER_US = None
+
+
+def gpu_hold(us: float) -> None:
+    """Queue a spin kernel of about `us` microseconds on the current stream (torch's bounded
+    clock loop).  Queued just before a timed region's start event, it keeps the GPU busy
+    while the host submits the region's launches (a graph replay, or eager launches), so the
+    start event is reached with those launches already queued: the region then measures the
+    GPU's back-to-back execution of the K steps, not the host's submission latency."""
+    import torch
+
+    global _SLEEP_CYCLES_PER_US
+    if _SLEEP_CYCLES_PER_US is None:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1 << 16)  # first call loads the kernel
+        a.record()
+        torch.cuda._sleep(1 << 22)
+        b.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_US = (1 << 22) / max(a.elapsed_time(b) * 1e3, 1.0)
+    torch.cuda._sleep(int(us * _SLEEP_CYCLES_PER_US))
+
+
+def hold_us(steps: int, per_step_us: float) -> float:
+    """Hold long enough for the host to submit `steps` launches, at most 50 ms."""
+    return min(100.0 + per_step_us * steps, 50_000.0)
 
 
 def copy_calibration(mib: int) -> None:
@@ -145,6 +180,7 @@ def bench_bmm(args) -> None:
             step()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        gpu_hold(hold_us(args.steps, 25.0))
         t0.record(stream)
         for _ in range(args.steps):
             step()
@@ -253,10 +289,13 @@ def bench_fp32(args) -> None:
         else:
             dy = torch.rand(y.shape, device=dev, generator=gen) * 2 - 1
             dw = torch.empty_like(wt)
-            M.launch_grad_nhwc(x[:1], dy[:1], dw, 1, h, w, c, r, s_, k, conv, stream=stream)  # one-image check
+            # the timed problem itself (all n images) checked against the direct kernel, which
+            # is bit-exact with cpu_grad_nhwc, under the reference's verify rule
+            M.launch_grad_nhwc(x, dy, dw, n, h, w, c, r, s_, k, conv, stream=stream)
+            dw_ref = torch.empty_like(wt)
+            M.launch_grad_nhwc(x, dy, dw_ref, n, h, w, c, r, s_, k, conv, algo="direct", stream=stream)
             torch.cuda.synchronize()
-            want = oracle.grad_f32(x[:1].cpu().numpy(), dy[:1].cpu().numpy(), tuple(wt.shape), conv)
-            ok = oracle.verify_tensors(want, dw.cpu().numpy(), 1e-4, 1e-3)
+            ok = oracle.verify_tensors(dw_ref.cpu().numpy(), dw.cpu().numpy(), 1e-4, 1e-3)
 
             def step():
                 M.launch_grad_nhwc(x, dy, dw, n, h, w, c, r, s_, k, conv, stream=stream)
@@ -264,6 +303,7 @@ def bench_fp32(args) -> None:
             step()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        gpu_hold(hold_us(args.steps, 25.0))
         t0.record(stream)
         for _ in range(args.steps):
             step()
@@ -278,14 +318,11 @@ def bench_fp32(args) -> None:
         tf = flops / (ms * 1e-3) / 1e12
         gbs = nbytes / (ms * 1e-3) / 1e9
         frac = tf / PEAK_FP32_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
-        algo = ("igemm" if (c // g) % 4 == 0 and args.op == "fprop" else
-                "depthwise" if c == g == k and c % 4 == 0 and args.op == "fprop" else
-                "igemm" if (k // g) % 4 == 0 and sh == sw == 1 and args.op == "bprop" else
-                "depthwise" if args.op == "grad" and c == g == k and c % 4 == 0 and r * s_ <= 16 else
-                "igemm" if args.op == "grad" else "direct")
+        algo = M.plan_f32(args.op, n, h, w, c, r, s_, k, M.Conv2DParams(*conv))  # what the library dispatches
         rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, kernel=algo,
                          us=round(ms * 1e3, 2), tflops=round(tf, 3), gbs=round(gbs, 1), bound=bound,
-                         frac=round(frac, 4), verified_image0=ok))
+                         frac=round(frac, 4), verified=ok,
+                         verified_on="all images vs the direct kernel" if args.op == "grad" else "image 0 vs the oracle"))
         del x, wt, y
         torch.cuda.empty_cache()
     if not rows:
@@ -295,7 +332,7 @@ def bench_fp32(args) -> None:
           file=sys.stderr)
     for r in rows:
         print(f"{r['name']:20s} {r['kernel']:7s} {r['us']:10.2f} {r['tflops']:8.2f} {r['gbs']:8.1f} {r['bound']:5s} "
-              f"{r['frac']:6.3f} {r['verified_image0']}", file=sys.stderr)
+              f"{r['frac']:6.3f} {r['verified']}", file=sys.stderr)
     head = rows[0]
     line = {
         "metric": f"fp32 conv {args.op} TFLOP/s, conv_bench default suite (src/main.cpp:163-174)",
@@ -383,6 +420,7 @@ def bench_qi32(args) -> None:
             step()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        gpu_hold(hold_us(args.steps, 25.0))
         t0.record(stream)
         for _ in range(args.steps):
             step()
@@ -447,6 +485,7 @@ def cpu_baseline(wl):
         "kind": kind,
         "sample": f"full {wl.name} batch (N={wl.n}, {wl.ops / 1e9:.2f} Gop int32 accumulation) in {secs:.2f} s; "
                   f"{what}; 1 thread on {cpu_model()}",
+        "workload": wl.name,
     }
 
 
@@ -479,9 +518,16 @@ def main():
         bench_qi32(args)
         return
     dev = torch.device("cuda:0")
-    names = [args.config or W.HEADLINE]
-    if args.all:
-        names = [W.HEADLINE] + [n for n in W.WORKLOADS if n != W.HEADLINE]
+    # every BASELINE config by default (the headline first: its line is `value`); --config
+    # times one
+    names = [args.config] if args.config else [W.HEADLINE] + [n for n in W.WORKLOADS if n != W.HEADLINE]
+    flush = torch.empty((FLUSH_BYTES // 4,), dtype=torch.float32, device=dev).fill_(1.0)
+
+    def flush_caches():
+        # a read of 2x the Infinity Cache (MALL) and every L2: evicts earlier steps' data and
+        # leaves no dirty lines behind, so nothing is written back during the timed region
+        torch.sum(flush)
+        torch.cuda.synchronize()
 
     results = {}
     for name in names:
@@ -491,24 +537,28 @@ def main():
         bias = torch.from_numpy(inp["bias"]).to(dev)
         ws = torch.from_numpy(inp["w_scale"]).to(dev)
         set_bytes = wl.x_bytes + wl.y_bytes
-        nsets = 1 if args.cache == "warm" else max(2, -(-2 * MALL_BYTES // set_bytes))
+        # cold: one pooled buffer of input/output sets, one per timed step up to POOL_BYTES
+        # (then reused in rotation, POOL_BYTES >> MALL apart), filled by one copy kernel; every
+        # timed step reads a set that nothing has touched since the flush before the timed region
+        nsets = 1 if args.cache == "warm" else max(1, min(args.steps, POOL_BYTES // set_bytes))
         x0 = torch.from_numpy(inp["x"]).to(dev)
-        xs = [x0] + [x0.clone() for _ in range(nsets - 1)]
-        ys = [torch.empty((wl.n, wl.ho, wl.wo, wl.k), dtype=torch.int8, device=dev) for _ in range(nsets)]
+        xpool = torch.empty((nsets,) + tuple(x0.shape), dtype=torch.int8, device=dev)
+        xpool.copy_(x0.unsqueeze(0).expand_as(xpool))
+        ypool = torch.empty((nsets, wl.n, wl.ho, wl.wo, wl.k), dtype=torch.int8, device=dev)
         kw = dict(stride=wl.stride, padding=wl.pad, relu=wl.relu, in_scale=wl.in_scale, out_scale=wl.out_scale,
                   algo=args.algo)
         algo = M.plan(M.make_desc(x0.shape, w.shape, stride=wl.stride, padding=wl.pad, algo=args.algo))
 
         def step(i, stream=None):
-            M.qconv2d_nhwc_i8(xs[i % nsets], w, bias, ws, out=ys[i % nsets], stream=stream, **kw)
+            M.qconv2d_nhwc_i8(xpool[i % nsets], w, bias, ws, out=ypool[i % nsets], stream=stream, **kw)
 
-        # correctness gate before timing: int8 output of set 0 against the oracle's epilogue
+        # correctness gate before timing: the int8 output of set 0 against the oracle's epilogue
         import oracle
         step(0)
         torch.cuda.synchronize()
         acc = oracle.conv_i8_acc(inp["x"], inp["w"], wl.conv7)
         want = oracle.requant_i8(acc, inp["bias"], inp["w_scale"], wl.in_scale, wl.out_scale, wl.relu)
-        verified = bool(np.array_equal(ys[0].cpu().numpy(), want))
+        verified = bool(np.array_equal(ypool[0].cpu().numpy(), want))
 
         for i in range(args.warmup):
             step(i)
@@ -534,8 +584,11 @@ def main():
                 graph = None
 
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if args.cache == "cold":
+            flush_caches()
         torch.cuda.synchronize()
         wall0 = time.perf_counter()
+        gpu_hold(hold_us(args.steps, 3.0 if graph is not None else 25.0))
         t0.record(stream)
         if graph is not None:
             graph.replay()
@@ -553,6 +606,8 @@ def main():
         # beside the back-to-back figure, never as `value`
         nper = min(args.steps, 200)
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nper)]
+        if args.cache == "cold":
+            flush_caches()
         for i, (ea, eb) in enumerate(evs):
             ea.record(stream)
             step(i)
@@ -565,9 +620,11 @@ def main():
         t_mfma = wl.ops / (PEAK_INT8_TOPS * 1e12)
         t_hbm = wl.bytes / (PEAK_HBM_GBS * 1e9)
         bound = "mfma" if t_mfma >= t_hbm else "hbm"
+        touched = min(args.steps, nsets) * set_bytes
+        cache = "warm" if args.cache == "warm" else "cold"
         results[name] = dict(ms=ms, tops=tops, gbs=gbs, bound=bound, verified=verified, algo=algo, mode=mode,
-                             nsets=nsets, wall=wall, wl=wl, per_launch=per_launch)
-        del xs, ys, graph
+                             nsets=nsets, touched=touched, cache=cache, wall=wall, wl=wl, per_launch=per_launch)
+        del xpool, ypool, graph
         torch.cuda.empty_cache()
 
     head = results[names[0]]
@@ -602,7 +659,8 @@ def main():
         "config": {
             "workload": wl.name, "N": wl.n, "H": wl.h, "W": wl.w, "C": wl.c, "K": wl.k, "R": wl.r, "S": wl.s,
             "stride": wl.stride, "pad": wl.pad, "relu": wl.relu, "epilogue": "bias+requant+int8 saturate",
-            "kernel": head["algo"], "cache": args.cache, "buffer_sets": head["nsets"], "timing": head["mode"],
+            "kernel": head["algo"], "cache": head["cache"], "buffer_sets": head["nsets"],
+            "bytes_touched": head["touched"], "timing": head["mode"],
         },
         "mfma_peak_frac": round(head["tops"] / PEAK_INT8_TOPS, 4),
         "gbs": round(head["gbs"], 2),
@@ -610,16 +668,32 @@ def main():
         "roofline": roof,
         "per_launch": head["per_launch"],
     }
+    # every config measured in this run (BASELINE.json configs[0..4]), same timing and cache
+    # rules as the headline; `value` stays the headline's
+    per_cfg = {}
+    for name, r in results.items():
+        frac = r["tops"] / PEAK_INT8_TOPS if r["bound"] == "mfma" else r["gbs"] / PEAK_HBM_GBS
+        traffic = None
+        tf = ROOT / "profiles" / f"traffic_{name}.json"
+        if tf.exists():
+            try:
+                traffic = json.loads(tf.read_text()).get("bytes_per_launch")
+            except (ValueError, OSError):
+                traffic = None
+        per_cfg[name] = {"us": round(r["ms"] * 1e3, 3), "tops": round(r["tops"], 2), "gbs": round(r["gbs"], 1),
+                         "bound": r["bound"], "frac": round(frac, 4), "mfma_peak_frac": round(r["tops"] / PEAK_INT8_TOPS, 4),
+                         "kernel": r["algo"], "verified_bit_exact": r["verified"], "cache": r["cache"],
+                         "bytes_touched": r["touched"], "traffic": traffic,
+                         "median_us": r["per_launch"]["median_us"], "p90_us": r["per_launch"]["p90_us"]}
+    line["configs"] = per_cfg
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(wl)
-    if args.all:
-        print(f"{'config':10s} {'kernel':7s} {'us':>9s} {'TOPS':>8s} {'GB/s':>8s} {'bound':5s} {'frac':>6s} exact"
-              f" {'med us':>7s} {'p90 us':>7s}", file=sys.stderr)
-        for name, r in results.items():
-            frac = r["tops"] / PEAK_INT8_TOPS if r["bound"] == "mfma" else r["gbs"] / PEAK_HBM_GBS
-            print(f"{name:10s} {r['algo']:7s} {r['ms'] * 1e3:9.2f} {r['tops']:8.1f} {r['gbs']:8.1f} {r['bound']:5s} "
-                  f"{frac:6.3f} {str(r['verified']):5s} {r['per_launch']['median_us']:7.2f} {r['per_launch']['p90_us']:7.2f}",
-                  file=sys.stderr)
+    print(f"{'config':10s} {'kernel':7s} {'us':>9s} {'TOPS':>8s} {'GB/s':>8s} {'bound':5s} {'frac':>6s} exact"
+          f" {'med us':>7s} {'p90 us':>7s}", file=sys.stderr)
+    for name, r in per_cfg.items():
+        print(f"{name:10s} {r['kernel']:7s} {r['us']:9.2f} {r['tops']:8.1f} {r['gbs']:8.1f} {r['bound']:5s} "
+              f"{r['frac']:6.3f} {str(r['verified_bit_exact']):5s} {r['median_us']:7.2f} {r['p90_us']:7.2f}",
+              file=sys.stderr)
     print(json.dumps(line), flush=True)
     os.sys.stdout.flush()
 

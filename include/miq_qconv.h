@@ -259,6 +259,24 @@ int miq_grad_nhwc_f32_noalloc(const float* x, const float* dy, float* dw, int32_
                               int32_t c, int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo,
                               void* stream);
 
+/* Kernel families of the fp32 passes (miq_plan_f32). */
+typedef enum miq_f32_kernel {
+  MIQ_F32_DIRECT = 0,          /* one thread per output element, the reference CPU loop's order */
+  MIQ_F32_IGEMM = 1,           /* fp32 MFMA implicit GEMM, 128 pixels x 64 channels per workgroup */
+  MIQ_F32_IGEMM32 = 2,         /* the same with 256 pixels x 32 channels (groups of <= 32 channels) */
+  MIQ_F32_DEPTHWISE = 3,       /* depthwise fprop, 4 channels per thread */
+  MIQ_F32_BPROP_IGEMM = 4,     /* stride-1 dx as the forward implicit GEMM over dy */
+  MIQ_F32_GRAD_IGEMM = 5,      /* dw as a GEMM over pixels split across workgroups */
+  MIQ_F32_GRAD_DEPTHWISE = 6   /* depthwise dw, pixel runs per thread */
+} miq_f32_kernel;
+
+/* The kernel family an fp32 pass (op 0 fprop, 1 bprop, 2 grad) would run for this problem and
+ * algo, with 16-byte aligned tensors; the same validation as the entry point.  No GPU access.
+ * No reference counterpart: it names what launch_fprop_nhwc / launch_bprop_nhwc /
+ * launch_grad_nhwc run for benchmark tables and tests. */
+int miq_plan_f32(int32_t op, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                 const miq_conv2d_params* p, int32_t algo, int32_t* kernel);
+
 /* ---- int32 batched matrix product -------------------------------------------------- */
 /* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and
  * sums, exact for every int32 input.  Row-major, batch strides M*K, K*N and M*N:

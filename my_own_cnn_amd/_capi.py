@@ -32,6 +32,10 @@ MIQ_ALGO_BAND = 4
 MIQ_ALGO_STREAM = 5
 MIQ_ALGO_ATOMIC = 6  # fp32 grad only
 MIQ_ALGO_FLAT = 7
+
+# miq_f32_kernel: the fp32 passes' kernel families (miq_plan_f32)
+F32_KERNEL_NAMES = {0: "direct", 1: "igemm", 2: "igemm32", 3: "depthwise", 4: "bprop_igemm", 5: "grad_igemm",
+                    6: "grad_depthwise"}
 ALGOS = {"auto": MIQ_ALGO_AUTO, "direct": MIQ_ALGO_DIRECT, "igemm": MIQ_ALGO_IGEMM, "stem": MIQ_ALGO_STEM,
          "band": MIQ_ALGO_BAND, "stream": MIQ_ALGO_STREAM, "flat": MIQ_ALGO_FLAT}
 ALGO_NAMES = {v: k for k, v in ALGOS.items()}
@@ -106,6 +110,7 @@ SIGNATURES = {
     "miq_block_conv2d_output_shape": (
         C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(BlockConv2DParams), _PI, _PI, _PI, _PI]),
     "miq_qconv2d_plan": (C.c_int, [C.POINTER(QConvDesc), _PI]),
+    "miq_plan_f32": (C.c_int, [_I, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _PI]),
     "miq_fprop_nhwc_qi32_u8": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P, _P, _P]),
     "miq_fprop_nhwc_qi32_s5": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P, _P, _P]),
     "miq_block_fprop_nhwc_qi32_u8": (

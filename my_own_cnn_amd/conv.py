@@ -17,7 +17,7 @@ from typing import Optional, Sequence, Tuple, Union
 import numpy as np
 
 from . import _capi
-from ._capi import (ALGO_NAMES, ALGOS, BlockConv2DParams, Conv2DParams, MiqError, QConvDesc, QParamsS5,
+from ._capi import (ALGO_NAMES, ALGOS, F32_KERNEL_NAMES, BlockConv2DParams, Conv2DParams, MiqError, QConvDesc, QParamsS5,
                     QParamsU8, check, lib)
 
 try:
@@ -274,6 +274,21 @@ def grad_workspace_size(n: int, h: int, w: int, c: int, r: int, s: int, k: int, 
                                                  C.byref(out)), "grad_workspace_size")
     return int(out.value)
 
+def plan_f32(op: str, n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=None, algo: str = "auto") -> str:
+    """Kernel family an fp32 pass ('fprop', 'bprop' or 'grad') runs for this problem with aligned
+    tensors: the library's own dispatch (miq_plan_f32), no GPU access."""
+    params = _as_params(p)
+    ops = {"fprop": 0, "bprop": 1, "grad": 2}
+    algos = F32_GRAD_ALGOS if op == "grad" else F32_ALGOS
+    if op not in ops:
+        raise ValueError(f"op must be one of {sorted(ops)}, got {op!r}")
+    if algo not in algos:
+        raise ValueError(f"algo for {op} must be one of {sorted(algos)}, got {algo!r}")
+    out = C.c_int32()
+    check(lib().miq_plan_f32(ops[op], n, h, w, c, r, s, k, C.byref(params), algos[algo], C.byref(out)), "plan_f32")
+    return F32_KERNEL_NAMES[out.value]
+
+
 def conv2d_nhwc_f32(x, w, *, stride=1, padding=0, dilation=1, groups=1, algo="auto", out=None, stream=None):
     """fp32 convolution of device tensors: x (N, H, W, C), w (K, R, S, C/groups) -> (N, Ho, Wo, K)."""
     if x.dtype != torch.float32 or w.dtype != torch.float32:
@@ -329,7 +344,7 @@ __all__ = [
     "bmm_i32", "bmm_matmul_i32", "conv2d_nhwc_f32", "launch_fprop_nhwc", "launch_bprop_nhwc", "launch_grad_nhwc",
     "DataType", "Conv2DParams", "BlockConv2DParams", "QParamsU8", "QParamsS5", "QConvDesc", "MiqError",
     "qparams_array", "infer_conv_shape", "infer_block_conv_shape", "launch_fprop_nhwc_qi32",
-    "launch_block_fprop_nhwc_qi32", "make_desc", "plan", "qconv2d_nhwc_i8", "qconv2d_nhwc_i8_acc32",
+    "launch_block_fprop_nhwc_qi32", "make_desc", "plan", "plan_f32", "qconv2d_nhwc_i8", "qconv2d_nhwc_i8_acc32",
     "qconv2d_nhwc_i8_dequant",
 ]
 _ = _capi

@@ -531,6 +531,54 @@ int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int
   return grad_launch(g, ch, x, dy, dw, ws, stream);
 }
 
+int miq_plan_f32(int32_t op, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                 const miq_conv2d_params* p, int32_t algo, int32_t* kernel) {
+  if (kernel == nullptr) return fail(MIQ_ERR_NULL_POINTER, "kernel pointer is NULL");
+  miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  static const float kAligned[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const void* al = static_cast<const void*>(kAligned);
+  std::string why;
+  switch (op) {
+    case 0:  // fprop: the order of miq_fprop_nhwc_f32
+      switch (algo) {
+        case MIQ_ALGO_AUTO:
+          *kernel = miq::f32_igemm_eligible(g, al, al, nullptr) ? (g.Kg <= 32 ? MIQ_F32_IGEMM32 : MIQ_F32_IGEMM)
+                    : miq::f32_depthwise_eligible(g, al, al)     ? MIQ_F32_DEPTHWISE
+                                                                  : MIQ_F32_DIRECT;
+          return MIQ_OK;
+        case MIQ_ALGO_DIRECT: *kernel = MIQ_F32_DIRECT; return MIQ_OK;
+        case MIQ_ALGO_IGEMM:
+          if (!miq::f32_igemm_eligible(g, al, al, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+          *kernel = g.Kg <= 32 ? MIQ_F32_IGEMM32 : MIQ_F32_IGEMM;
+          return MIQ_OK;
+        default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 convolution algo must be AUTO, DIRECT or IGEMM");
+      }
+    case 1:  // bprop: the order of miq_bprop_nhwc_f32
+      switch (algo) {
+        case MIQ_ALGO_AUTO:
+          *kernel = miq::f32_bprop_igemm_eligible(g, al, al, nullptr) ? MIQ_F32_BPROP_IGEMM : MIQ_F32_DIRECT;
+          return MIQ_OK;
+        case MIQ_ALGO_DIRECT: *kernel = MIQ_F32_DIRECT; return MIQ_OK;
+        case MIQ_ALGO_IGEMM:
+          if (!miq::f32_bprop_igemm_eligible(g, al, al, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+          *kernel = MIQ_F32_BPROP_IGEMM;
+          return MIQ_OK;
+        default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 bprop algo must be AUTO, DIRECT or IGEMM");
+      }
+    case 2: {  // grad: grad_choose, as miq_grad_nhwc_f32
+      GradChoice ch;
+      st = grad_choose(g, al, al, algo, &ch);
+      if (st != MIQ_OK) return st;
+      *kernel = ch.kind == kGradDepthwise ? MIQ_F32_GRAD_DEPTHWISE : ch.kind == kGradIgemm ? MIQ_F32_GRAD_IGEMM
+                                                                                          : MIQ_F32_DIRECT;
+      return MIQ_OK;
+    }
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "op must be 0 (fprop), 1 (bprop) or 2 (grad)");
+  }
+}
+
 int miq_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,
                 int32_t trans_a, int32_t trans_b, void* stream) {
   if (batch < 0 || M < 0 || N < 0 || K < 0) return fail(MIQ_ERR_INVALID_ARGUMENT, "bmm extents must be >= 0");

@@ -316,3 +316,32 @@ def test_fp32_grad_workspace_query_and_validation():
         _capi.MIQ_ERR_INVALID_ARGUMENT
     assert b"smaller" in lib.miq_last_error_message()
     assert lib.miq_grad_nhwc_f32_ws(p, p, None, 1, 5, 5, 4, 3, 3, 0, C.byref(ok), 0, None, 0, None) == _capi.MIQ_OK  # k == 0
+
+
+def test_plan_f32_names_the_kernel_each_pass_runs():
+    # the fp32 passes' dispatch, answered by the library without touching the GPU
+    r50 = (32, 56, 56, 64, 3, 3, 64)
+    dw = _capi.Conv2DParams(1, 1, 1, 1, 1, 1, 64)  # depthwise: groups = C = K
+    assert M.plan_f32("fprop", *r50) == "igemm"
+    assert M.plan_f32("fprop", 8, 28, 28, 64, 3, 3, 32) == "igemm32"  # K per group <= 32
+    assert M.plan_f32("fprop", *r50, dw) == "depthwise"
+    assert M.plan_f32("fprop", *r50, algo="direct") == "direct"
+    assert M.plan_f32("bprop", *r50) == "bprop_igemm"
+    assert M.plan_f32("bprop", *r50, dw) == "direct"
+    assert M.plan_f32("grad", *r50) == "grad_igemm"
+    assert M.plan_f32("grad", *r50, dw) == "grad_depthwise"
+    assert M.plan_f32("grad", *r50, algo="direct") == "direct"
+    lib = M.lib()
+    ok = _capi.Conv2DParams(1, 1, 1, 1, 1, 1, 1)
+    out = C.c_int32(-1)
+    assert lib.miq_plan_f32(3, *r50, C.byref(ok), 0, C.byref(out)) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert lib.miq_plan_f32(0, *r50, C.byref(ok), _capi.MIQ_ALGO_STREAM, C.byref(out)) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert lib.miq_plan_f32(0, *r50, C.byref(ok), 0, None) == _capi.MIQ_ERR_NULL_POINTER
+    bad = _capi.Conv2DParams(1, 1, 0, 1, 1, 1, 1)  # stride 0: the shape check rejects it
+    assert lib.miq_plan_f32(0, *r50, C.byref(bad), 0, C.byref(out)) != _capi.MIQ_OK
+    with pytest.raises(ValueError, match="algo"):
+        M.plan_f32("fprop", *r50, algo="stream")
+    with pytest.raises(ValueError, match="op"):
+        M.plan_f32("wgrad", *r50)
+    with pytest.raises(M.MiqError):
+        M.plan_f32("fprop", 1, 2, 2, 16, 3, 3, 16, _capi.Conv2DParams(0, 0, 1, 1, 1, 1, 1))  # no output pixels
