@@ -1,0 +1,426 @@
+// Hardware probes of one MI355X (gfx950) behind the kernel design choices (TEST
+// INFRASTRUCTURE ONLY; not linked into libmiq_qconv).  Built by __graft_entry__.build() into
+// tests/hw/bin/hw_probes; tests/test_gpu_hw_probes.py runs it and checks what the design
+// relies on.  Subcommands (each prints one line per measurement):
+//
+//   launch  empty-kernel cost per launch, back to back, eager and replayed from a HIP graph
+//   ingest  per-CU global->LDS rates of buffer_load_dwordx4 ... lds, from L2 and from HBM
+//   lds     ds_read_b128 throughput per CU, and the lane-to-cycle rule for bank conflicts
+//           fitted over fixed and random lane address patterns
+//   mfma    v_mfma_i32_16x16x64_i8 / 32x32x32_i8 issue rates, alone and mixed with VALU and
+//           ds_read work
+//
+// Every kernel is bounded: fixed trip counts, in-bounds LDS and buffer accesses (buffer
+// loads also carry a record count), no waits on other waves beyond __syncthreads.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <random>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+#define CK(x)                                                                               \
+  do {                                                                                      \
+    hipError_t e_ = (x);                                                                    \
+    if (e_ != hipSuccess) {                                                                 \
+      std::printf("HIP error %s at line %d: %s\n", hipGetErrorString(e_), __LINE__, #x);    \
+      std::exit(1);                                                                         \
+    }                                                                                       \
+  } while (0)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+namespace {
+
+constexpr int kCUs = 256;
+
+float time_us(const std::function<void()>& fn, int reps, hipStream_t st) {
+  hipEvent_t a, b;
+  CK(hipEventCreate(&a));
+  CK(hipEventCreate(&b));
+  fn();
+  CK(hipStreamSynchronize(st));
+  CK(hipEventRecord(a, st));
+  for (int i = 0; i < reps; ++i) fn();
+  CK(hipEventRecord(b, st));
+  CK(hipEventSynchronize(b));
+  float ms = 0.0f;
+  CK(hipEventElapsedTime(&ms, a, b));
+  CK(hipEventDestroy(a));
+  CK(hipEventDestroy(b));
+  return ms * 1000.0f / reps;
+}
+
+// ---------------------------------------------------------------- launch
+__global__ void empty_kernel() {}
+
+void probe_launch(hipStream_t st) {
+  for (int block : {64, 512}) {
+    for (int grid : {1, 256, 1024}) {
+      const float eager =
+          time_us([&] { hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(block), 0, st); }, 2000, st);
+      hipGraph_t g;
+      hipGraphExec_t ge;
+      constexpr int kNodes = 400;
+      CK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+      for (int i = 0; i < kNodes; ++i) hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(block), 0, st);
+      CK(hipStreamEndCapture(st, &g));
+      CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      const float graph = time_us([&] { CK(hipGraphLaunch(ge, st)); }, 5, st) / kNodes;
+      std::printf("launch grid %d block %d eager_us %.3f graph_us %.3f\n", grid, block, eager, graph);
+      CK(hipGraphExecDestroy(ge));
+      CK(hipGraphDestroy(g));
+    }
+  }
+}
+
+// ---------------------------------------------------------------- ingest
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), num_records, 0x00020000);
+}
+
+// Each workgroup loads nkb KB into LDS, 1 KB per buffer_load_dwordx4 ... lds (64 lanes x 16 B),
+// the instructions spread over its waves; the source is shared by all workgroups (L2 after the
+// first touch) or distinct per workgroup (HBM after a flush).  Thread 0 stamps the 100 MHz
+// clock at entry and after the workgroup's loads have landed.
+__global__ void __launch_bounds__(512) ingest_kernel(const char* src, int nkb, int distinct, long long* stamps,
+                                                     int* out) {
+  extern __shared__ v4i lds[];
+  const long long t0 = __builtin_amdgcn_s_memrealtime();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const char* base = src + (distinct ? static_cast<size_t>(blockIdx.x) * nkb * 1024 : 0);
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(base, nkb * 1024);
+  for (int f = wave; f < nkb; f += nw)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(lds + f * 64), 16, 16u * lane, f * 1024u, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+  __syncthreads();
+  const long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    stamps[2 * blockIdx.x] = t0;
+    stamps[2 * blockIdx.x + 1] = t1;
+  }
+  out[blockIdx.x * blockDim.x + threadIdx.x] = lds[(threadIdx.x * 7) % (nkb * 64)][0];
+}
+
+// Reads `n` float4 (grid-stride) and writes one partial sum per thread: evicts L2 and the
+// Infinity Cache without leaving dirty lines whose write-back would load the next kernel.
+__global__ void __launch_bounds__(256) flush_read_kernel(const float4* __restrict__ p, size_t n, float* out) {
+  const size_t tid = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  float s = 0.0f;
+  for (size_t i = tid; i < n; i += stride) {
+    const float4 v = p[i];
+    s += v.x + v.y + v.z + v.w;
+  }
+  out[tid] = s;
+}
+
+void probe_ingest(hipStream_t st) {
+  constexpr int kMaxKB = 144;
+  const size_t src_bytes = size_t(kCUs) * kMaxKB * 1024;
+  const size_t flush_bytes = size_t(512) << 20;
+  char *src = nullptr, *flush = nullptr;
+  long long* stamps = nullptr;
+  int* out = nullptr;
+  CK(hipMalloc(&src, src_bytes));
+  CK(hipMalloc(&flush, flush_bytes));
+  CK(hipMalloc(&stamps, kCUs * 2 * sizeof(long long)));
+  CK(hipMalloc(&out, kCUs * 512 * sizeof(int)));
+  CK(hipMemset(src, 1, src_bytes));
+  CK(hipMemset(flush, 0, flush_bytes));
+  constexpr int kFlushGrid = 2048, kFlushBlock = 256;
+  float* flush_out = nullptr;
+  CK(hipMalloc(&flush_out, size_t(kFlushGrid) * kFlushBlock * sizeof(float)));
+  const int lds_bytes = 150 * 1024;  // one workgroup per CU, room for 144 KB
+  CK(hipFuncSetAttribute((const void*)ingest_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
+  std::vector<long long> hs(2 * kCUs);
+  for (int distinct = 0; distinct < 2; ++distinct) {
+    for (int nkb : {8, 36, 72, kMaxKB}) {
+      for (int block : {256, 512}) {
+        double wg_us = 0, span_us = 0;
+        constexpr int kReps = 5;
+        for (int rep = 0; rep < kReps; ++rep) {
+          hipLaunchKernelGGL(flush_read_kernel, dim3(kFlushGrid), dim3(kFlushBlock), 0, st,
+                             reinterpret_cast<const float4*>(flush), flush_bytes / sizeof(float4), flush_out);
+          if (!distinct)  // the shared source: one warm-up pass puts it in L2
+            hipLaunchKernelGGL(ingest_kernel, dim3(kCUs), dim3(block), lds_bytes, st, src, nkb, 0, stamps, out);
+          hipLaunchKernelGGL(ingest_kernel, dim3(kCUs), dim3(block), lds_bytes, st, src, nkb, distinct, stamps, out);
+          CK(hipGetLastError());
+          CK(hipStreamSynchronize(st));
+          CK(hipMemcpy(hs.data(), stamps, hs.size() * sizeof(long long), hipMemcpyDeviceToHost));
+          long long mn = hs[0], mx = hs[1];
+          double s = 0;
+          for (int w = 0; w < kCUs; ++w) {
+            mn = std::min(mn, hs[2 * w]);
+            mx = std::max(mx, hs[2 * w + 1]);
+            s += (hs[2 * w + 1] - hs[2 * w]) * 0.01;
+          }
+          wg_us += s / kCUs;
+          span_us += (mx - mn) * 0.01;
+        }
+        wg_us /= kReps;
+        span_us /= kReps;
+        std::printf("ingest source %s kb %d waves %d wg_us %.3f gbs_per_cu %.1f span_us %.3f chip_tbs %.2f\n",
+                    distinct ? "hbm" : "l2", nkb, block / 64, wg_us, nkb * 1.024 / wg_us, span_us,
+                    kCUs * nkb * 1.024e-3 / span_us);
+      }
+    }
+  }
+  CK(hipFree(src));
+  CK(hipFree(flush));
+  CK(hipFree(flush_out));
+  CK(hipFree(stamps));
+  CK(hipFree(out));
+}
+
+// ---------------------------------------------------------------- lds
+// Every wave of every workgroup issues `iters` x 8 ds_read_b128, lane l reading the 16-byte
+// slot slots[l] (0..63) of a 1 KB LDS window; the lane pattern alone sets the bank conflicts.
+__global__ void __launch_bounds__(1024) lds_kernel(const int* __restrict__ slots, int iters, int* out) {
+  extern __shared__ v4i lds[];
+  for (int i = threadIdx.x; i < 64; i += blockDim.x) lds[i] = v4i{i, 2 * i, 3 * i, 4 * i};
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const unsigned addr = static_cast<unsigned>(slots[lane] & 63) * 16u;
+  v4i acc = {0, 0, 0, 0};
+  for (int i = 0; i < iters; ++i) {
+    v4i r0, r1, r2, r3, r4, r5, r6, r7;
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %8\n"
+        "ds_read_b128 %2, %8\n"
+        "ds_read_b128 %3, %8\n"
+        "ds_read_b128 %4, %8\n"
+        "ds_read_b128 %5, %8\n"
+        "ds_read_b128 %6, %8\n"
+        "ds_read_b128 %7, %8\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+        : "v"(addr)
+        : "memory");
+    acc ^= r0 ^ r1 ^ r2 ^ r3 ^ r4 ^ r5 ^ r6 ^ r7;
+  }
+  out[blockIdx.x * blockDim.x + threadIdx.x] = acc[0] + acc[1] + acc[2] + acc[3];
+}
+
+// Cycles one ds_read_b128 takes under a grouping of the 64 lanes into 4 groups of 16: per
+// group, the largest number of distinct 16-byte slots sharing one slot class (slot mod 16:
+// 64 banks x 4 bytes = 16 slots); lanes reading one address are served together.
+int predicted_cycles(const std::vector<int>& slot, const std::function<int(int)>& group_of) {
+  int total = 0;
+  for (int gi = 0; gi < 4; ++gi) {
+    int worst = 0;
+    for (int cls = 0; cls < 16; ++cls) {
+      std::vector<int> seen;
+      for (int l = 0; l < 64; ++l)
+        if (group_of(l) == gi && (slot[l] & 15) == cls && std::find(seen.begin(), seen.end(), slot[l]) == seen.end())
+          seen.push_back(slot[l]);
+      worst = std::max<int>(worst, static_cast<int>(seen.size()));
+    }
+    total += worst;
+  }
+  return total;
+}
+
+// The rule used by the kernels: a cycle serves one half-wave (lanes 0-31 or 32-63) and within
+// it the lane quads 4q..4q+3 (q = 0..7) of one popcount parity of q.
+int group_parity(int l) {
+  const int q = (l >> 2) & 7;
+  return 2 * (l >> 5) + (__builtin_popcount(q) & 1);
+}
+// The naive alternative: lanes 0-15, 16-31, 32-47, 48-63.
+int group_consecutive(int l) { return l >> 4; }
+
+void probe_lds(hipStream_t st) {
+  int *d_slots = nullptr, *out = nullptr;
+  CK(hipMalloc(&d_slots, 64 * sizeof(int)));
+  CK(hipMalloc(&out, kCUs * 1024 * sizeof(int)));
+  const int lds_bytes = 96 * 1024;  // one workgroup per CU
+  CK(hipFuncSetAttribute((const void*)lds_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
+  auto run = [&](const std::vector<int>& slot, int waves, int iters) {
+    CK(hipMemcpy(d_slots, slot.data(), 64 * sizeof(int), hipMemcpyHostToDevice));
+    return time_us([&] { hipLaunchKernelGGL(lds_kernel, dim3(kCUs), dim3(64 * waves), lds_bytes, st, d_slots, iters,
+                                            out); },
+                   3, st);
+  };
+  std::vector<int> linear(64);
+  for (int l = 0; l < 64; ++l) linear[l] = l;
+  int clock_khz = 0;
+  CK(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeClockRate, 0));
+  const double ghz = clock_khz * 1e-6;
+  // throughput of conflict-free reads against the number of waves per CU
+  for (int waves : {1, 2, 4, 8, 16}) {
+    const int iters = 4000;
+    const float us = run(linear, waves, iters);
+    const double bytes_per_cu = double(waves) * iters * 8 * 1024;
+    std::printf("lds_rate waves %d us %.1f bytes_per_clk_per_cu %.1f at %.2f GHz\n", waves, us,
+                bytes_per_cu / (us * 1e3 * ghz), ghz);
+  }
+  // the bank rule: fixed patterns, then random ones; time relative to the linear pattern
+  std::vector<std::pair<std::string, std::vector<int>>> pats;
+  auto add = [&](const std::string& name, const std::function<int(int)>& f) {
+    std::vector<int> s(64);
+    for (int l = 0; l < 64; ++l) s[l] = f(l) & 63;
+    pats.emplace_back(name, s);
+  };
+  add("linear", [](int l) { return l; });
+  add("broadcast", [](int) { return 5; });
+  add("stride2", [](int l) { return 2 * l; });
+  add("stride4", [](int l) { return 4 * l; });
+  add("stride16", [](int l) { return 16 * l + (l >> 2); });
+  add("half_swap", [](int l) { return l ^ 32; });
+  add("l_and_l16_same_class", [](int l) { return (l & 15) + 16 * ((l >> 4) & 1) + 32 * (l >> 5); });
+  add("quads_0_1_same_class", [](int l) { return (l & 3) + 16 * ((l >> 2) & 3) + 4 * (l >> 4); });
+  add("quads_0_3_same_class", [](int l) { return (l & 3) + 16 * ((l >> 2) & 3); });
+  add("pairs_same_address", [](int l) { return l >> 1; });
+  add("rows_of_8_x_128B", [](int l) { return (l & 7) + 8 * (l >> 3); });
+  add("rows_of_16_x_64B_fragment", [](int l) { return 4 * (l & 15) + (l >> 4); });
+  std::mt19937 rng(20251202u);
+  for (int p = 0; p < 200; ++p) {
+    std::vector<int> s(64);
+    const int span = (p % 4 == 0) ? 16 : 64;  // some draws from only 16 slots: many shared addresses
+    for (int l = 0; l < 64; ++l) s[l] = static_cast<int>(rng() % span) + (span == 16 ? 16 * (rng() % 4) : 0);
+    pats.emplace_back("random" + std::to_string(p), s);
+  }
+  const int iters = 2000, waves = 8;
+  const float t_lin = run(linear, waves, iters);
+  for (const auto& [name, s] : pats) {
+    const float t = run(s, waves, iters);
+    std::printf("lds_pattern %s rel_time %.3f parity_rule %d consecutive_rule %d\n", name.c_str(), t / t_lin,
+                predicted_cycles(s, group_parity), predicted_cycles(s, group_consecutive));
+  }
+  CK(hipFree(d_slots));
+  CK(hipFree(out));
+}
+
+// ---------------------------------------------------------------- mfma
+// NACC independent accumulator chains of one MFMA shape per wave; NV VALU ops (v_mul_f32 on 8
+// registers) and ND ds_read_b128 (feeding the next iteration's B operand) per MFMA group.
+template <int SHAPE, int NACC, int NV, int ND>
+__global__ void __launch_bounds__(512) mfma_kernel(int iters, int* out) {
+  extern __shared__ v4i lds[];
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < 2048; i += blockDim.x) lds[i] = v4i{i, i + 1, i + 2, i + 3};
+  __syncthreads();
+  constexpr int NB = ND > 0 ? ND : 1;
+  const v4i a = {lane, lane + 1, lane + 2, lane + 3};
+  v4i B0[NB], B1[NB];
+  for (int d = 0; d < NB; ++d) {
+    B0[d] = v4i{lane * 3 + d, 1, 2, 3};
+    B1[d] = v4i{lane * 5 + d, 1, 2, 3};
+  }
+  float f[8];
+  for (int k = 0; k < 8; ++k) f[k] = 1.0f + 0.001f * (lane + k);
+  const float m = 1.0000001f;
+  typedef typename std::conditional<SHAPE == 16, v4i, v16i>::type acc_t;
+  acc_t acc[NACC];
+  for (int j = 0; j < NACC; ++j) acc[j] = acc_t{};
+  const unsigned base = (threadIdx.x >> 6) * 2048u;  // a 2 KB LDS window per wave (32 KB for 16 waves)
+  auto rd = [&](int d, int i) {
+    const unsigned addr = base + ((lane * 16u + d * 1024u + (i & 1) * 512u) & 2047u);
+    return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(static_cast<uintptr_t>(addr));
+  };
+  auto group = [&](v4i(&B)[NB], int i) {
+#pragma unroll
+    for (int j = 0; j < NACC; ++j) {
+      if constexpr (SHAPE == 16)
+        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[j % NB], acc[j], 0, 0, 0);
+      else
+        acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, B[j % NB], acc[j], 0, 0, 0);
+    }
+    if constexpr (ND > 0) {
+#pragma unroll
+      for (int d = 0; d < ND; ++d) B[d] = rd(d, i);
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) f[v & 7] *= m;
+  };
+  for (int i = 0; i < iters; i += 2) {
+    group(B0, i);
+    group(B1, i + 1);
+  }
+  int s = 0;
+  for (int j = 0; j < NACC; ++j) s += acc[j][0] + acc[j][1];
+  for (int k = 0; k < 8; ++k) s += static_cast<int>(f[k]);
+  for (int d = 0; d < NB; ++d) s += B0[d][0] + B1[d][1];
+  out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+template <int SHAPE, int NACC, int NV, int ND>
+void run_mfma(int waves_per_simd, int* out, hipStream_t st) {
+  const int iters = 20000;
+  const int lds_bytes = 96 * 1024;  // one workgroup per CU
+  auto k = mfma_kernel<SHAPE, NACC, NV, ND>;
+  CK(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
+  const float us =
+      time_us([&] { hipLaunchKernelGGL(k, dim3(kCUs), dim3(256 * waves_per_simd), lds_bytes, st, iters, out); }, 3,
+              st);
+  CK(hipGetLastError());
+  const double mfma_per_simd = double(iters) * NACC * waves_per_simd;
+  const double ops = double(SHAPE == 16 ? 32768 : 65536) * NACC * iters * 4 * waves_per_simd * kCUs;
+  std::printf("mfma shape %dx%d chains %d valu %d ds_read %d waves_per_simd %d ns_per_mfma %.3f tops %.1f peak_frac %.3f\n",
+              SHAPE, SHAPE, NACC, NV, ND, waves_per_simd, us * 1000.0 / mfma_per_simd, ops / us * 1e-6,
+              ops / us * 1e-6 / 5000.0);
+}
+
+void probe_mfma(hipStream_t st) {
+  int* out = nullptr;
+  CK(hipMalloc(&out, kCUs * 1024 * sizeof(int)));
+  run_mfma<16, 4, 0, 0>(1, out, st);
+  run_mfma<16, 4, 0, 0>(2, out, st);
+  run_mfma<16, 8, 0, 0>(1, out, st);
+  run_mfma<32, 2, 0, 0>(1, out, st);
+  run_mfma<32, 2, 0, 0>(2, out, st);
+  run_mfma<32, 4, 0, 0>(1, out, st);
+  run_mfma<16, 4, 4, 0>(1, out, st);
+  run_mfma<16, 4, 8, 0>(1, out, st);
+  run_mfma<16, 4, 16, 0>(1, out, st);
+  run_mfma<16, 4, 8, 0>(2, out, st);
+  run_mfma<16, 4, 0, 1>(1, out, st);
+  run_mfma<16, 4, 0, 1>(2, out, st);
+  run_mfma<16, 4, 0, 2>(1, out, st);
+  run_mfma<16, 4, 8, 1>(1, out, st);
+  run_mfma<16, 4, 8, 1>(2, out, st);
+  run_mfma<32, 2, 8, 1>(1, out, st);
+  run_mfma<32, 2, 8, 1>(2, out, st);
+  CK(hipFree(out));
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const std::string what = argc > 1 ? argv[1] : "all";
+  hipStream_t st;
+  CK(hipStreamCreate(&st));
+  hipDeviceProp_t prop;
+  CK(hipGetDeviceProperties(&prop, 0));
+  std::printf("device %s cus %d clock_khz %d l2_bytes %d\n", prop.gcnArchName, prop.multiProcessorCount,
+              prop.clockRate, prop.l2CacheSize);
+  if (prop.multiProcessorCount != kCUs) {
+    std::printf("expected %d CUs (MI355X)\n", kCUs);
+    return 2;
+  }
+  std::fflush(stdout);
+  if (what == "launch" || what == "all") probe_launch(st);
+  std::fflush(stdout);
+  if (what == "ingest" || what == "all") probe_ingest(st);
+  std::fflush(stdout);
+  if (what == "lds" || what == "all") probe_lds(st);
+  std::fflush(stdout);
+  if (what == "mfma" || what == "all") probe_mfma(st);
+  CK(hipDeviceSynchronize());
+  CK(hipStreamDestroy(st));
+  std::printf("done\n");
+  return 0;
+}
