@@ -30,12 +30,15 @@
 // read 16 consecutive columns of one chunk: their 16-byte slots are distinct modulo 16,
 // so the read is free of bank conflicts for any column shift.
 //
-// Loads.  Every load of the workgroup (filter, epilogue parameters, the band's input rows)
+// Loads.  Every load of the workgroup (the band's input rows, epilogue parameters, filter)
 // is issued at the start, spread over the 8 waves, with one buffer resource per tensor and
 // a few scalar instructions per load: scalar work is shared by the waves of a SIMD and a
 // long scalar loop delays everything behind it.  Kernel arguments are preloaded in one
-// s_load batch.  A wave waits (vmcnt) for its own loads and the barrier publishes all of
-// them; after the last barrier the phases run without synchronisation.
+// s_load batch.  The rows phase 0 reads go first (HBM latency), then the epilogue
+// parameters and the filter, then the other rows.  A wave waits (vmcnt) for all but the
+// other rows and a barrier publishes them; phase 0 copies the filter into registers a few
+// K-blocks ahead of its matrix instructions; after phase 0's MFMAs a second wait and
+// barrier publish the other rows, and the phases run without synchronisation.
 //
 // Skew.  The two waves of a SIMD (w and w + 4) are offset by one epilogue: the leading
 // wave runs MFMA(p) then epilogue(p), the trailing one epilogue(p - 1) then MFMA(p), so one
@@ -51,6 +54,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <type_traits>
 
 namespace miq {
 namespace {
@@ -133,6 +137,48 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   // turn), so the loads below use one buffer resource each and keep per-load work to a
   // few instructions.
   //
+  // Issue order: the input rows phase 0 reads (HBM, the longest latency), the epilogue
+  // parameters, the filter (L2 after the first workgroup), then the remaining rows.  A
+  // CU's vector memory path accepts about 35 bytes per clock, so what is issued first
+  // lands first.
+  //
+  // ---- every input row of the band, in row order: instruction i = (row * NQ + quad) *
+  // NPB + block goes to wave i % 8; its lane l reads column 16 * block + l % 16 - pw, chunk
+  // 4 * quad + l / 16.  One resource covers the image (group gi's channels onward); the row
+  // goes into soffset.  A column outside the image gets voffset 2^30 and a row outside it
+  // soffset 2^30: either way past num_records (< 2^30), and their sum cannot wrap.
+  const int hi0 = ho0 * a.sh - a.ph;
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(a.x + static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg,
+                a.H * a.W * a.C - gi * a.Cg);
+  const int col_lane = row_l - a.pw;
+  auto load_rows = [&](int i, int i_end) {
+    int cnt = 0;
+    for (; i < i_end; i += kBandWaves) {
+      const int hr = fdiv(i, a.fd_rowi);
+      const int rem = i - hr * row_instr;
+      const int q = fdiv(rem, a.fd_npb);
+      const int pb = rem - q * a.NPB;
+      const int hi = hi0 + hr;
+      const unsigned soff =
+          static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) ? static_cast<unsigned>(hi * a.W * a.C + 64 * q) : 0x40000000u;
+      const int col = col_lane + 16 * pb;
+      const unsigned voff =
+          static_cast<unsigned>(col) < static_cast<unsigned>(a.W) ? static_cast<unsigned>(col * a.C + 16 * grp_l) : 0x40000000u;
+      load_lds16(rx, halo + i * 64, voff, soff);
+      ++cnt;
+    }
+    return cnt;
+  };
+  load_rows(wave, a.ni0);
+  // ---- bias and per-channel scales of tile t's 64 channels (wave t), 2 KB of LDS each ----
+  if (EPI != kEpiAcc32 && wave < NT) {
+    const int kt = k0 + 64 * wave;
+    const int valid = max(0, a.Kg - kt) * 4;
+    const size_t off = static_cast<size_t>(gi) * a.Kg + min(kt, a.Kg);
+    load_lds16(make_rsrc(a.bias ? a.bias + off : nullptr, a.bias ? valid : 0), ep + 128 * wave, 16u * lane, 0);
+    load_lds16(make_rsrc(a.wscale + off, valid), ep + 128 * wave + 64, 16u * lane, 0);
+  }
   // ---- filter -> LDS, instruction f to wave f % 8.  Even KB: fragment order; fragment
   // f = 4KB*t + 4b + j (64-channel tile t, K-block b, MFMA row block j) is one
   // instruction, whose lane (row_l, grp_l) holds channel
@@ -165,61 +211,31 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
       }
     }
   }
-  // ---- bias and per-channel scales of tile t's 64 channels (wave t), 2 KB of LDS each ----
-  if (EPI != kEpiAcc32 && wave < NT) {
-    const int kt = k0 + 64 * wave;
-    const int valid = max(0, a.Kg - kt) * 4;
-    const size_t off = static_cast<size_t>(gi) * a.Kg + min(kt, a.Kg);
-    load_lds16(make_rsrc(a.bias ? a.bias + off : nullptr, a.bias ? valid : 0), ep + 128 * wave, 16u * lane, 0);
-    load_lds16(make_rsrc(a.wscale + off, valid), ep + 128 * wave + 64, 16u * lane, 0);
-  }
-  // ---- every input row of the band, in row order: instruction i = (row * NQ + quad) *
-  // NPB + block goes to wave i % 8; its lane l reads column 16 * block + l % 16 - pw, chunk
-  // 4 * quad + l / 16.  One resource covers the image (group gi's channels onward); the row
-  // goes into soffset.  A column outside the image gets voffset 2^30 and a row outside it
-  // soffset 2^30: either way past num_records (< 2^30), and their sum cannot wrap.
-  int my_loads = 0;
-  {
-    const int hi0 = ho0 * a.sh - a.ph;
-    const size_t img = static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg;
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + img, a.H * a.W * a.C - gi * a.Cg);
-    const int col_lane = row_l - a.pw;
-    for (int i = wave; i < a.ni; i += kBandWaves) {
-      const int hr = fdiv(i, a.fd_rowi);
-      const int rem = i - hr * row_instr;
-      const int q = fdiv(rem, a.fd_npb);
-      const int pb = rem - q * a.NPB;
-      const int hi = hi0 + hr;
-      const unsigned soff =
-          static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) ? static_cast<unsigned>(hi * a.W * a.C + 64 * q) : 0x40000000u;
-      const int col = col_lane + 16 * pb;
-      const unsigned voff =
-          static_cast<unsigned>(col) < static_cast<unsigned>(a.W) ? static_cast<unsigned>(col * a.C + 16 * grp_l) : 0x40000000u;
-      load_lds16(rx, halo + i * 64, voff, soff);
-      ++my_loads;
-    }
-  }
-  // filter and epilogue parameters (issued before any input row) complete; the barrier
-  // publishes every wave's part
-  wait_vmcnt(my_loads);
+  // ---- the remaining input rows (instructions ni0 .. ni - 1, wave i % 8) ----
+  const int first_rest = a.ni0 + ((wave - a.ni0) % kBandWaves + kBandWaves) % kBandWaves;
+  const int rest_loads = load_rows(first_rest, a.ni);
+  // phase 0's rows, the epilogue parameters and the filter (everything but the remaining
+  // rows) complete; the barrier publishes every wave's part
+  wait_vmcnt(rest_loads);
   barrier_only();
 
+  // The filter stays in registers: A[b][j] is K-block b, MFMA row block j.  Phase 0 reads
+  // each K-block's fragments from LDS two K-blocks ahead of its MFMAs (read_A), so the
+  // copy overlaps the first segment's matrix instructions; later phases reuse them.
   v4i A[KB][4];
-  if constexpr (KB & 1) {
-    // lane (row_l, grp_l) of fragment (b, j): channel n = 16 * (row_l / 4) + 4j + row_l % 4
-    // of the tile, 16-byte unit 4 * KB * n + 4b + grp_l, plus its block's shift
-    const v4i* ft = filt + tw * band_tile_slots(KB) + 4 * KB * (16 * (row_l >> 2) + (row_l & 3)) + grp_l +
-                    2 * (row_l >> 3);
+  // lane (row_l, grp_l) of fragment (b, j), odd KB: channel n = 16 * (row_l / 4) + 4j +
+  // row_l % 4 of the tile, 16-byte unit 4 * KB * n + 4b + grp_l, plus its block's shift
+  const v4i* ft = filt + tw * band_tile_slots(KB) + 4 * KB * (16 * (row_l >> 2) + (row_l & 3)) + grp_l +
+                  2 * (row_l >> 3);
+  auto read_A = [&](int b) {
 #pragma unroll
-    for (int b = 0; b < KB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) A[b][j] = ft[16 * KB * j + 4 * b];
-  } else {
-#pragma unroll
-    for (int b = 0; b < KB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) A[b][j] = filt[(tw * 4 * KB + b * 4 + j) * 64 + lane];
-  }
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (KB & 1)
+        A[b][j] = ft[16 * KB * j + 4 * b];
+      else
+        A[b][j] = filt[(tw * 4 * KB + b * 4 + j) * 64 + lane];
+    }
+  };
   // epilogue parameters of this lane's 16 channels kc0 + 4j + r (zero past Kg)
   const int kc0 = k0 + 64 * tw + 16 * grp_l;
   const bool ch_ok = kc0 < a.Kg;  // Kg % 16 == 0: a lane's 16 channels all exist or none does
@@ -310,7 +326,14 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
       }
     }
   };
-  auto mfma_phase = [&](unsigned rb, v4i (&acc)[4]) {
+  // first: phase 0, which also reads the filter fragments, AD K-blocks ahead
+  auto mfma_phase = [&](auto first, unsigned rb, v4i (&acc)[4]) {
+    constexpr bool FIRST = decltype(first)::value;
+    constexpr int AD = KB < 2 ? KB : 2;
+    if constexpr (FIRST) {
+#pragma unroll
+      for (int b = 0; b < AD; ++b) read_A(b);
+    }
     // input fragments are read RS K-blocks ahead: each read goes out right after the
     // MFMAs that free its register
     constexpr int RS = KB < 4 ? KB : 4;
@@ -319,6 +342,9 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
     for (int r = 0; r < RS; ++r) B[r] = lds_read16(baddr[r] + rb);
 #pragma unroll
     for (int b = 0; b < KB; ++b) {
+      if constexpr (FIRST) {
+        if (b + AD < KB) read_A(b + AD);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][j], B[b % RS], b == 0 ? bias_v[j] : acc[j], 0, 0, 0);
@@ -327,16 +353,9 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
       __builtin_amdgcn_sched_barrier(0);  // keeps each read RS K-blocks ahead of its use
     }
   };
-
-  // Phase 0 starts as soon as its own input rows are in: a wave waits for its loads among
-  // the first ni0 (exact: no store is pending yet).  The wait for the rest comes after the
-  // phase-0 MFMAs and before the first store, so it is exact too, and after its barrier
-  // nothing synchronises any more.
-  {
-    const int mine0 = a.ni0 > wave ? (a.ni0 - wave + kBandWaves - 1) / kBandWaves : 0;
-    wait_vmcnt(my_loads - mine0);
-    barrier_only();
-  }
+  // The wait for the remaining rows comes after the phase-0 MFMAs and before the first
+  // store (exact: no store is pending yet), and after its barrier nothing synchronises
+  // any more.
   auto wait_rest = [&]() {
     wait_vmcnt(0);
     barrier_only();
@@ -348,7 +367,10 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   v4i acc[4];
   if (wave < kBandWaves / 2) {
     for (int p = 0; p < nph; ++p) {
-      mfma_phase(seg_rb(), acc);
+      if (p == 0)
+        mfma_phase(std::true_type{}, seg_rb(), acc);
+      else
+        mfma_phase(std::false_type{}, seg_rb(), acc);
       if (p == 0) wait_rest();
       emit(acc, seg_soff(), seg_lane());
       seg_next();
@@ -362,7 +384,10 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
       for (int j = 0; j < 4; ++j) prev[j] = acc[j];
       if (p == 1) wait_rest();
       if (p > 0) emit(prev, soff_prev, lane_prev);
-      mfma_phase(seg_rb(), acc);
+      if (p == 0)
+        mfma_phase(std::true_type{}, seg_rb(), acc);
+      else
+        mfma_phase(std::false_type{}, seg_rb(), acc);
       soff_prev = seg_soff();
       lane_prev = seg_lane();
       seg_next();
