@@ -5,9 +5,12 @@
 // and :213-342 declare for this path, with the same names, members, defaults and
 // signatures, so that callers written against the reference (quant_conv_test.cu and the
 // verify_tensors / benchmark_cuda_op harness) compile unchanged and resolve to this
-// library's implementations.  Of the fp32 functions, launch_fprop_nhwc, launch_bprop_nhwc and
-// launch_grad_nhwc are declared; the blocked fp32 kernels and the cuDNN comparison functions
-// of the reference header are not part of this build and are not declared here.
+// library's implementations.  The fp32 launchers launch_{,block_}{fprop,bprop,grad}_nhwc and the
+// CPU functions cpu_{,block_}{fprop,bprop,grad}_nhwc are declared as the reference declares
+// them (conv_types.h:204-212, :287-304); this library defines the launchers and no CPU
+// convolution (the CPU functions are the reference's cpu_ref.cpp, or the test oracle's
+// adapter).  The cuDNN comparison functions of the reference header are not part of this
+// build and are not declared here.
 //
 // Additions beside the reference surface (nothing existing changes):
 //   * RequantParams and the native int8 launchers launch_fprop_nhwc_qi8{,_acc32,_dequant}
@@ -209,6 +212,17 @@ struct BenchResult {
   float gflops = 0.0f;
 };
 
+// fp32 CPU reference path (conv_types.h:204-212): declared for callers written against the
+// reference; defined by the reference's cpu_ref.cpp (or by this repository's test oracle).
+void cpu_fprop_nhwc(const TensorNHWC& x, const FilterKRSC& w, const Conv2DParams& p, TensorNHWC& y);
+void cpu_bprop_nhwc(const TensorNHWC& dy, const FilterKRSC& w, const Conv2DParams& p, TensorNHWC& dx);
+void cpu_grad_nhwc(const TensorNHWC& x, const TensorNHWC& dy, const Conv2DParams& p, FilterKRSC& dw);
+void cpu_block_fprop_nhwc(const TensorNHWC& x, const BlockFilterKByBxRSC& w, const BlockConv2DParams& p, TensorNHWC& y,
+                          const float* bias = nullptr, BlockBiasMode bias_mode = BlockBiasMode::PerBlock);
+void cpu_block_bprop_nhwc(const TensorNHWC& dy, const BlockFilterKByBxRSC& w, const BlockConv2DParams& p, TensorNHWC& dx);
+void cpu_block_grad_nhwc(const TensorNHWC& x, const TensorNHWC& dy, const BlockConv2DParams& p, BlockFilterKByBxRSC& dw,
+                         float* dbias = nullptr, BlockBiasMode bias_mode = BlockBiasMode::PerBlock);
+
 namespace conv_quant_detail {
 
 // CPU reference path (conv_types.h:215-230).  Defined by the reference's cpu_ref.cpp (or
@@ -352,6 +366,21 @@ void launch_bprop_nhwc(const float* d_dy, const float* d_w, float* d_dx,
 void launch_grad_nhwc(const float* d_x, const float* d_dy, float* d_dw,
                       int n, int h, int w, int c, int r, int s, int k,
                       const Conv2DParams& p);
+// The blocked fp32 convolution, its dx and its dw (+ bias gradient), the reference's
+// launch_block_{fprop,bprop,grad}_nhwc (conv_types.h:296-304, cuda_kernels.cu:939-1136): same
+// signatures, defaults and meaning.  The bias gradient is the sum of dy over every position of
+// the block, as the reference's launcher computes it, in a fixed order.
+void launch_block_fprop_nhwc(const float* d_x, const float* d_w, float* d_y,
+                             int n, int h, int w, int c, int r, int s, int k,
+                             const BlockConv2DParams& p,
+                             const float* d_bias = nullptr, BlockBiasMode bias_mode = BlockBiasMode::PerBlock);
+void launch_block_bprop_nhwc(const float* d_dy, const float* d_w, float* d_dx,
+                             int n, int h, int w, int c, int r, int s, int k,
+                             const BlockConv2DParams& p);
+void launch_block_grad_nhwc(const float* d_x, const float* d_dy, float* d_dw,
+                            int n, int h, int w, int c, int r, int s, int k,
+                            const BlockConv2DParams& p,
+                            float* d_dbias = nullptr, BlockBiasMode bias_mode = BlockBiasMode::PerBlock);
 
 // y (int8 NHWC) = requant(conv(x, w)); x int8 NHWC, w int8 KRSC, all device pointers.
 void launch_fprop_nhwc_qi8(const int8_t* d_x, const int8_t* d_w, int8_t* d_y,

@@ -259,6 +259,48 @@ int miq_grad_nhwc_f32_noalloc(const float* x, const float* dy, float* dw, int32_
                               int32_t c, int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo,
                               void* stream);
 
+/* ---- blocked (locally connected) fp32 convolution ----------------------------------- */
+/* The output grid splits into block_by x block_bx blocks of (ho / block_by) x (wo / block_bx)
+ * positions (ho and wo must divide; miq_block_conv_output_shape), each with its own filter:
+ * w is [k][block_by][block_bx][r][s][c/groups].  Bias and its gradient are k * block_by *
+ * block_bx floats indexed [k][by][bx]; with MIQ_BLOCK_BIAS_SHARED every block uses (and the
+ * gradient accumulates into) entry [k][0][0], the other entries of dbias being set to 0.
+ * Values of BlockBiasMode (/root/reference/src/conv_types.h:37-40). */
+typedef enum miq_block_bias_mode {
+  MIQ_BLOCK_BIAS_PER_BLOCK = 0,
+  MIQ_BLOCK_BIAS_SHARED = 1
+} miq_block_bias_mode;
+
+/* y = the blocked convolution of x (then + bias, one fp32 add after the tap sum, when bias is
+ * not NULL).  algo: MIQ_ALGO_AUTO (the MFMA implicit GEMM, one block per workgroup, where
+ * miq_fprop_nhwc_f32 would take it; else direct), MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT (the
+ * loop order and rounding of cpu_block_fprop_nhwc, cpu_ref.cpp:232-270: its result bit for
+ * bit).  Replaces launch_block_fprop_nhwc (/root/reference/src/cuda_kernels.cu:939-1001). */
+int miq_block_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                             int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p, const float* bias,
+                             int32_t bias_mode, int32_t algo, void* stream);
+
+/* dx of the blocked convolution (dy n x ho x wo x k; dx fully overwritten).  algo: as
+ * miq_bprop_nhwc_f32 (the MFMA form: stride 1, each dx tile reducing over the filter blocks its
+ * taps reach); MIQ_ALGO_DIRECT follows cpu_block_bprop_nhwc (cpu_ref.cpp:272-314) bit for bit.
+ * Replaces launch_block_bprop_nhwc (/root/reference/src/cuda_kernels.cu:1003-1058). */
+int miq_block_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                             int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p, int32_t algo,
+                             void* stream);
+
+/* dw ([k][by][bx][r][s][c/groups], fully overwritten) of the blocked convolution and, when
+ * dbias is not NULL, the bias gradient: the sum of dy over every output position of the block
+ * (k * by * bx floats, fully overwritten), as launch_block_grad_nhwc computes it, added in a
+ * fixed order so that every call gives the same bits (the reference's CPU form,
+ * cpu_block_grad_nhwc, counts only the positions whose (r, s) = (0, 0) tap lies inside the
+ * image: the two differ where that tap falls in the padding).  algo: as miq_grad_nhwc_f32;
+ * MIQ_ALGO_DIRECT gives cpu_block_grad_nhwc's dw (cpu_ref.cpp:316-369) bit for bit.  Keeps the
+ * grow-only per-device workspace of miq_grad_nhwc_f32.
+ * Replaces launch_block_grad_nhwc (/root/reference/src/cuda_kernels.cu:1060-1136). */
+int miq_block_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                            int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p, float* dbias,
+                            int32_t bias_mode, int32_t algo, void* stream);
+
 /* Kernel families of the fp32 passes (miq_plan_f32). */
 typedef enum miq_f32_kernel {
   MIQ_F32_DIRECT = 0,          /* one thread per output element, the reference CPU loop's order */
@@ -276,6 +318,11 @@ typedef enum miq_f32_kernel {
  * launch_grad_nhwc run for benchmark tables and tests. */
 int miq_plan_f32(int32_t op, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
                  const miq_conv2d_params* p, int32_t algo, int32_t* kernel);
+
+/* miq_plan_f32 for the blocked passes (miq_block_fprop_nhwc_f32, miq_block_bprop_nhwc_f32,
+ * miq_block_grad_nhwc_f32).  No reference counterpart. */
+int miq_plan_block_f32(int32_t op, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                       const miq_block_conv2d_params* p, int32_t algo, int32_t* kernel);
 
 /* ---- int32 batched matrix product -------------------------------------------------- */
 /* C[b] = op(A[b]) * op(B[b]) for b < batch, with int32 wrap-around (mod 2^32) products and

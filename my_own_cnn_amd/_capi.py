@@ -129,6 +129,13 @@ SIGNATURES = {
     "miq_grad_nhwc_f32_noalloc": (C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P]),
     "miq_grad_nhwc_f32_ws": (
         C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, _P, C.c_size_t, _P]),
+    "miq_block_fprop_nhwc_f32": (
+        C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(BlockConv2DParams), _P, _I, _I, _P]),
+    "miq_block_bprop_nhwc_f32": (
+        C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(BlockConv2DParams), _I, _P]),
+    "miq_block_grad_nhwc_f32": (
+        C.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(BlockConv2DParams), _P, _I, _I, _P]),
+    "miq_plan_block_f32": (C.c_int, [_I, _I, _I, _I, _I, _I, _I, _I, C.POINTER(BlockConv2DParams), _I, _PI]),
 }
 
 _lib = None

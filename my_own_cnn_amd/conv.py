@@ -289,6 +289,68 @@ def plan_f32(op: str, n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=
     return F32_KERNEL_NAMES[out.value]
 
 
+BLOCK_BIAS_MODES = {"per_block": 0, "shared": 1}
+
+
+def _bias_mode(mode) -> int:
+    if isinstance(mode, str):
+        if mode not in BLOCK_BIAS_MODES:
+            raise ValueError(f"bias_mode must be one of {sorted(BLOCK_BIAS_MODES)}, got {mode!r}")
+        return BLOCK_BIAS_MODES[mode]
+    return int(mode)
+
+
+def _check_algo(algo: str, algos) -> int:
+    if algo not in algos:
+        raise ValueError(f"algo must be one of {sorted(algos)}, got {algo!r}")
+    return algos[algo]
+
+
+def launch_block_fprop_nhwc(d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int, r: int,
+                            s: int, k: int, p: BlockConv2DParams, d_bias: Pointer = None, bias_mode="per_block",
+                            algo: str = "auto", stream=None) -> None:
+    """Mirror of launch_block_fprop_nhwc (conv_types.h:296-299, cuda_kernels.cu:939-1001): the
+    blocked fp32 convolution, filter [K, By, Bx, R, S, C/groups], optional bias [K, By, Bx]
+    (bias_mode 'per_block' or 'shared'); `algo` 'auto', 'igemm' (MFMA) or 'direct' (bit-exact
+    with cpu_block_fprop_nhwc)."""
+    check(lib().miq_block_fprop_nhwc_f32(_addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k, C.byref(p),
+                                         _addr(d_bias), _bias_mode(bias_mode), _check_algo(algo, F32_ALGOS),
+                                         _stream(stream)), "launch_block_fprop_nhwc")
+
+
+def launch_block_bprop_nhwc(d_dy: Pointer, d_w: Pointer, d_dx: Pointer, n: int, h: int, w: int, c: int, r: int,
+                            s: int, k: int, p: BlockConv2DParams, algo: str = "auto", stream=None) -> None:
+    """Mirror of launch_block_bprop_nhwc (conv_types.h:300-302, cuda_kernels.cu:1003-1058): dx of
+    the blocked fp32 convolution; `algo` 'auto', 'igemm' (MFMA, stride 1) or 'direct' (bit-exact
+    with cpu_block_bprop_nhwc)."""
+    check(lib().miq_block_bprop_nhwc_f32(_addr(d_dy), _addr(d_w), _addr(d_dx), n, h, w, c, r, s, k, C.byref(p),
+                                         _check_algo(algo, F32_ALGOS), _stream(stream)), "launch_block_bprop_nhwc")
+
+
+def launch_block_grad_nhwc(d_x: Pointer, d_dy: Pointer, d_dw: Pointer, n: int, h: int, w: int, c: int, r: int,
+                           s: int, k: int, p: BlockConv2DParams, d_dbias: Pointer = None, bias_mode="per_block",
+                           algo: str = "auto", stream=None) -> None:
+    """Mirror of launch_block_grad_nhwc (conv_types.h:303-305, cuda_kernels.cu:1060-1136): dw of
+    the blocked fp32 convolution and, with d_dbias, the bias gradient (the sum of dy over every
+    position of each block, in a fixed order); `algo` as launch_grad_nhwc ('direct' gives
+    cpu_block_grad_nhwc's dw bit for bit)."""
+    check(lib().miq_block_grad_nhwc_f32(_addr(d_x), _addr(d_dy), _addr(d_dw), n, h, w, c, r, s, k, C.byref(p),
+                                        _addr(d_dbias), _bias_mode(bias_mode), _check_algo(algo, F32_GRAD_ALGOS),
+                                        _stream(stream)), "launch_block_grad_nhwc")
+
+
+def plan_block_f32(op: str, n: int, h: int, w: int, c: int, r: int, s: int, k: int, p: BlockConv2DParams,
+                   algo: str = "auto") -> str:
+    """plan_f32 for the blocked passes (miq_plan_block_f32), no GPU access."""
+    ops = {"fprop": 0, "bprop": 1, "grad": 2}
+    if op not in ops:
+        raise ValueError(f"op must be one of {sorted(ops)}, got {op!r}")
+    a = _check_algo(algo, F32_GRAD_ALGOS if op == "grad" else F32_ALGOS)
+    out = C.c_int32()
+    check(lib().miq_plan_block_f32(ops[op], n, h, w, c, r, s, k, C.byref(p), a, C.byref(out)), "plan_block_f32")
+    return F32_KERNEL_NAMES[out.value]
+
+
 def conv2d_nhwc_f32(x, w, *, stride=1, padding=0, dilation=1, groups=1, algo="auto", out=None, stream=None):
     """fp32 convolution of device tensors: x (N, H, W, C), w (K, R, S, C/groups) -> (N, Ho, Wo, K)."""
     if x.dtype != torch.float32 or w.dtype != torch.float32:
@@ -342,6 +404,7 @@ def bmm_i32(a, b, *, trans_a=False, trans_b=False, out=None, stream=None):
 
 __all__ = [
     "bmm_i32", "bmm_matmul_i32", "conv2d_nhwc_f32", "launch_fprop_nhwc", "launch_bprop_nhwc", "launch_grad_nhwc",
+    "launch_block_fprop_nhwc", "launch_block_bprop_nhwc", "launch_block_grad_nhwc", "plan_block_f32",
     "DataType", "Conv2DParams", "BlockConv2DParams", "QParamsU8", "QParamsS5", "QConvDesc", "MiqError",
     "qparams_array", "infer_conv_shape", "infer_block_conv_shape", "launch_fprop_nhwc_qi32",
     "launch_block_fprop_nhwc_qi32", "make_desc", "plan", "plan_f32", "qconv2d_nhwc_i8", "qconv2d_nhwc_i8_acc32",

@@ -49,15 +49,25 @@ struct F32Args {
   const float* x;
   const float* w;
   float* y;
+  const float* bias;  // forward with a blocked filter: K * By * Bx floats, or nullptr
   Geom g;
-  int M;         // N * Ho * Wo
+  int M;         // pixel slots per region: N * rh * rw (the pixel-tile grid's extent)
   int kdim;      // R * S * Cg
   int nchunks;   // ceil(kdim / 16)
   int tn;        // channel tiles per group
-  int tiles;     // pixel tiles * channel tiles per group
+  int tiles;     // pixel tiles * channel tiles per region
   int ow_taps;   // transposed filter: R * S of the original filter
   int ow_cg;     // transposed filter: channels per group of the original filter (= Kg of g)
-  FastDivM fd_tn, fd_tiles;
+  // Output regions: the output grid splits into ry x rx regions of rh x rw positions, the last
+  // row and column of regions clipped to Ho x Wo; a workgroup's pixels lie in one region.
+  int ry, rx, rh, rw;
+  // Filter blocks, By x Bx of bho x bwo positions each (1 x 1 of Ho x Wo: a plain KRSC filter).
+  // Forward: the blocks are the regions and a region's pixels use its block's filter.
+  // Transposed: the blocks partition this kernel's input (dy), and each input position uses
+  // the filter of its block.
+  int By, Bx, bho, bwo;
+  int bias_mode;  // 0: bias[k][by][bx]; 1: bias[k][0][0] for every block
+  FastDivM fd_tn, fd_tiles, fd_regions, fd_rx;
 };
 
 __device__ __forceinline__ int f32_slot(int row, int g) { return 4 * row + (g ^ (((row >> 3) & 1) << 1)); }
@@ -80,7 +90,10 @@ struct TapCursor {
 
 // TRANSPOSED: the filter operand is read as the bprop filter of a stride-1 convolution:
 // row j (an input channel of the original) and reduction index (r', s', ko) address
-// w[g Kg + ko][R-1-r'][S-1-s'][j] of the original KRSC filter (`ow_*` extents in F32Args).
+// w[g Kg + ko][by][bx][R-1-r'][S-1-s'][j] of the original filter (`ow_*` extents in F32Args),
+// (by, bx) the block of the input position the tap reads.  A workgroup runs its reduction
+// once per filter block that its pixels' taps can reach (one for a plain filter, and one for a
+// pixel tile inside a block's reach), reading only the input positions of that block each time.
 // BN: channels per workgroup, 64 (128 pixels, waves 4 x 2) or 32 for groups of at most 32
 // output channels (256 pixels, waves 8 x 1; each thread stages two pixel rows, and the waves
 // of threads 256.. load filter rows again without staging them).
@@ -96,12 +109,23 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
 
   const int lin = blockIdx.x;
-  const int grp = fdiv(lin, a.fd_tiles);
-  const int rem = lin - grp * a.tiles;
+  const int gr = fdiv(lin, a.fd_tiles);  // group * regions + region
+  const int rem = lin - gr * a.tiles;
+  const int grp = fdiv(gr, a.fd_regions);
+  const int reg = gr - grp * (a.ry * a.rx);
+  const int rgy = fdiv(reg, a.fd_rx);
+  const int rgx = reg - rgy * a.rx;
   const int tmi = fdiv(rem, a.fd_tn);
   const int tni = rem - tmi * a.tn;
+  const int row0 = rgy * a.rh;
+  const int col0 = rgx * a.rw;
+  const int rows = min(a.rh, g.Ho - row0);
+  const int cols = min(a.rw, g.Wo - col0);
+  const int Mr = rows > 0 && cols > 0 ? g.N * rows * cols : 0;  // this region's pixels
+  const int rc = rows * cols;
   const int m0 = tmi * BM;
   const int n0 = tni * BN;
+  if (m0 >= Mr) return;  // whole workgroup, before any barrier: a tile past a clipped region
 
   // A: pixel rows ar + 128 i, reduction values 4 aq .. 4 aq + 3 of each chunk
   const int ar = t >> 2;
@@ -110,14 +134,13 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const float* xn[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int pix = min(m0 + ar + 128 * i, a.M - 1);
-    const int hw = g.Ho * g.Wo;
-    const int pn = pix / hw;
-    const int prem = pix - pn * hw;
-    const int pho = prem / g.Wo;
-    const int pwo = prem - pho * g.Wo;
-    hbase[i] = pho * g.sh - g.ph;
-    wbase[i] = pwo * g.sw - g.pw;
+    const int pix = min(m0 + ar + 128 * i, Mr - 1);
+    const int pn = pix / rc;
+    const int prem = pix - pn * rc;
+    const int lr = prem / cols;
+    const int lc = prem - lr * cols;
+    hbase[i] = (row0 + lr) * g.sh - g.ph;
+    wbase[i] = (col0 + lc) * g.sw - g.pw;
     xn[i] = a.x + static_cast<size_t>(pn) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
   }
   TapCursor cur;
@@ -128,17 +151,21 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     cur.r = tap / g.S;
     cur.s = tap - cur.r * g.S;
   }
+  const TapCursor cur0 = cur;
   int cur_chunk = 0;
   // B: filter row br (channel of the group), reduction values 2 bp, 2 bp + 1 of each chunk
   const int br = (t >> 3) & (BN - 1);
   const int bp = t & 7;
   const bool b_stager = BN == 64 || t < 8 * BN;  // whole waves
+  const int nblk = a.By * a.Bx;
   const int brow = grp * g.Kg + min(n0 + br, g.Kg - 1);
-  const float* wr = a.w + static_cast<size_t>(brow) * a.kdim;
+  const float* wr = a.w + (static_cast<size_t>(brow) * nblk + (TRANSPOSED ? 0 : reg)) * a.kdim;
   // transposed filter: this thread's row is input channel bj of the original filter, its
   // reduction values (r', s', ko), (r', s', ko + 1) of each chunk tracked by a cursor
   const int bj = min(n0 + br, g.Kg - 1);
-  const float* wt0 = a.w + static_cast<size_t>(grp) * g.Cg * a.ow_taps * g.Kg + bj;  // (ko = 0, r = s = 0)
+  const size_t blk_stride = static_cast<size_t>(a.ow_taps) * a.ow_cg;  // between filter blocks
+  const size_t ko_stride = blk_stride * nblk;                          // between original channels
+  const float* wt0 = a.w + static_cast<size_t>(grp) * g.Cg * ko_stride + bj;  // (ko = 0, block 0, r = s = 0)
   TapCursor bcur;
   if constexpr (TRANSPOSED) {
     const int k = 2 * bp;
@@ -147,31 +174,92 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     bcur.r = tap / g.S;
     bcur.s = tap - bcur.r * g.S;
   }
+  const TapCursor bcur0 = bcur;
+
+  // The filter blocks this tile's taps can reach (inclusive rectangle qy0..qy1 x qx0..qx1),
+  // from the tile's range of output rows and columns; a plain filter has the one block 0.
+  // Input rows read by output row y: y sh - ph + r dh, r < R (likewise columns).
+  int qy0 = 0, qy1 = 0, qx0 = 0, qx1 = 0;
+  int nrect = 1;
+  if constexpr (TRANSPOSED) {
+    const int p1 = min(m0 + BM, Mr) - 1;
+    const int pn0 = m0 / rc, pn1 = p1 / rc;
+    const int lr0 = (m0 - pn0 * rc) / cols, lr1 = (p1 - pn1 * rc) / cols;
+    int rlo = 0, rhi = rows - 1, clo = 0, chi = cols - 1;
+    if (pn0 == pn1) {
+      rlo = lr0;
+      rhi = lr1;
+      if (lr0 == lr1) {
+        clo = m0 - pn0 * rc - lr0 * cols;
+        chi = p1 - pn1 * rc - lr1 * cols;
+      }
+    }
+    const int ylo = max((row0 + rlo) * g.sh - g.ph, 0);
+    const int yhi = min((row0 + rhi) * g.sh - g.ph + (g.R - 1) * g.dh, g.H - 1);
+    const int xlo = max((col0 + clo) * g.sw - g.pw, 0);
+    const int xhi = min((col0 + chi) * g.sw - g.pw + (g.S - 1) * g.dw, g.W - 1);
+    if (ylo <= yhi && xlo <= xhi) {
+      qy0 = ylo / a.bho;
+      qy1 = yhi / a.bho;
+      qx0 = xlo / a.bwo;
+      qx1 = xhi / a.bwo;
+      nrect = (qy1 - qy0 + 1) * (qx1 - qx0 + 1);
+    } else {
+      nrect = 0;  // no tap reads the input: the tile is zero
+    }
+  }
+  // current block of the reduction and the input positions it covers
+  int qy = qy0, qx = qx0, cib = 0;
+  int ylo_b = 0, yhi_b = g.H, xlo_b = 0, xhi_b = g.W;
+  const float* wtb = wt0;
+  auto set_block = [&]() {
+    ylo_b = qy * a.bho;
+    yhi_b = min(ylo_b + a.bho, g.H);
+    xlo_b = qx * a.bwo;
+    xhi_b = min(xlo_b + a.bwo, g.W);
+    wtb = wt0 + static_cast<size_t>(qy * a.Bx + qx) * blk_stride;
+  };
+  if constexpr (TRANSPOSED) set_block();
 
   auto load = [&](int c, v4f (&va)[NA], v2f& vb, unsigned& oka, bool& okb) {
     if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
-      cur.advance(g.Cg, g.S);
-      if constexpr (TRANSPOSED) bcur.advance(g.Cg, g.S);
       ++cur_chunk;
+      if constexpr (TRANSPOSED) {
+        if (++cib == a.nchunks) {  // next block of the tile's rectangle
+          cib = 0;
+          cur = cur0;
+          bcur = bcur0;
+          if (++qx > qx1) {
+            qx = qx0;
+            ++qy;
+          }
+          set_block();
+        } else {
+          cur.advance(g.Cg, g.S);
+          bcur.advance(g.Cg, g.S);
+        }
+      } else {
+        cur.advance(g.Cg, g.S);
+        cib = cur_chunk;
+      }
     }
     oka = 0;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int hi = hbase[i] + cur.r * g.dh;
       const int wi = wbase[i] + cur.s * g.dw;
-      const bool ok = cur.r < g.R && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
+      const bool ok = cur.r < g.R && hi >= ylo_b && hi < yhi_b && wi >= xlo_b && wi < xhi_b;
       oka |= static_cast<unsigned>(ok) << i;
       const size_t xo = ok ? (static_cast<size_t>(hi) * g.W + wi) * g.C + cur.ci : 0;
       va[i] = *reinterpret_cast<const v4f*>(xn[i] + xo);
     }
-    const int kb = c * kF32KC + 2 * bp;
+    const int kb = cib * kF32KC + 2 * bp;
     okb = kb < a.kdim;
     if constexpr (TRANSPOSED) {
-      // original filter w[ko][R-1-r'][S-1-s'][bj], ko = bcur.ci (+1); consecutive ko are
-      // a.ow_taps * a.ow_cg floats apart
+      // original filter w[ko][by][bx][R-1-r'][S-1-s'][bj], ko = bcur.ci (+1)
       const size_t tap = static_cast<size_t>(g.R - 1 - bcur.r) * g.S + (g.S - 1 - bcur.s);
-      const size_t o = okb ? (static_cast<size_t>(bcur.ci) * a.ow_taps + tap) * a.ow_cg : 0;
-      vb = v2f{wt0[o], wt0[o + static_cast<size_t>(okb) * a.ow_taps * a.ow_cg]};
+      const size_t o = okb ? static_cast<size_t>(bcur.ci) * ko_stride + tap * a.ow_cg : 0;
+      vb = v2f{wtb[o], wtb[o + static_cast<size_t>(okb) * ko_stride]};
     } else {
       vb = *reinterpret_cast<const v2f*>(wr + (okb ? kb : 0));
     }
@@ -196,7 +284,7 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     for (int im = 0; im < 2; ++im) acc[jn][im] = v4f{0.f, 0.f, 0.f, 0.f};
 
   constexpr int P = kF32Depth;
-  const int nch = a.nchunks;
+  const int nch = nrect * a.nchunks;
   if (nch > 0) {
     const int last = nch - 1;
     v4f va[P][NA];
@@ -234,15 +322,30 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   // lane (c = lane % 16, q = lane / 16) of tile (jn, im): pixel m0 + 32 wm + 16 im + c,
   // channels n0 + 32 wn + 16 jn + 4 q .. + 3 of the group
   const bool vec = (g.K & 3) == 0 && (g.Kg & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0;
+  const float* bias = TRANSPOSED ? nullptr : a.bias;
+  const int bias_y = a.bias_mode == 0 ? rgy : 0;
+  const int bias_x = a.bias_mode == 0 ? rgx : 0;
 #pragma unroll
-  for (int jn = 0; jn < 2; ++jn) {
+  for (int im = 0; im < 2; ++im) {
+    const int m = m0 + 32 * wm + 16 * im + (lane & 15);
+    if (m >= Mr) continue;
+    const int pn = m / rc;
+    const int prem = m - pn * rc;
+    const int lr = prem / cols;
+    const int lc = prem - lr * cols;
+    const size_t pix = (static_cast<size_t>(pn) * g.Ho + row0 + lr) * g.Wo + col0 + lc;
 #pragma unroll
-    for (int im = 0; im < 2; ++im) {
-      const int m = m0 + 32 * wm + 16 * im + (lane & 15);
+    for (int jn = 0; jn < 2; ++jn) {
       const int ch = n0 + 32 * wn + 16 * jn + 4 * (lane >> 4);
-      if (m >= a.M) continue;
-      float* yp = a.y + static_cast<size_t>(m) * g.K + static_cast<size_t>(grp) * g.Kg + ch;
-      const v4f r = acc[jn][im];
+      float* yp = a.y + pix * g.K + static_cast<size_t>(grp) * g.Kg + ch;
+      v4f r = acc[jn][im];
+      if (bias != nullptr) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int k = grp * g.Kg + min(ch + i, g.Kg - 1);
+          r[i] = __fadd_rn(r[i], bias[(static_cast<size_t>(k) * a.By + bias_y) * a.Bx + bias_x]);
+        }
+      }
       if (vec && ch + 3 < g.Kg) {
         *reinterpret_cast<v4f*>(yp) = r;
         store_gap(r);
@@ -287,16 +390,22 @@ inline Split3 make_split3(int v0, int v1, int v2) {
                 fastdiv_m(static_cast<uint32_t>(v2)), v0, v1, v2};
 }
 
+// With a blocked filter (bg: By x Bx blocks of bho x bwo output positions) the output position
+// (ho, wo) takes the filter w[k][ho / bho][wo / bwo] and, after the tap sum, one fp32 add of
+// its bias (bias[k][by][bx], or bias[k][0][0] with bias_mode 1), as cpu_block_fprop_nhwc
+// (cpu_ref.cpp:232-270) does.
 __global__ void __launch_bounds__(kDirectThreads) f32_direct_kernel(const float* __restrict__ x,
                                                                     const float* __restrict__ w,
-                                                                    float* __restrict__ y, Geom g, long long total,
-                                                                    Split3 sp) {
+                                                                    float* __restrict__ y, Geom g, BlockGeom bg,
+                                                                    const float* __restrict__ bias, int bias_mode,
+                                                                    long long total, Split3 sp) {
   const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
   if (e >= total) return;
   int k, wo, ho, n;
   sp.apply(e, total < (1LL << 31), k, wo, ho, n);
   const int grp = k / g.Kg;
-  const float* wk = w + static_cast<size_t>(k) * g.R * g.S * g.Cg;
+  const int by = ho / bg.bho, bx = wo / bg.bwo;
+  const float* wk = w + (static_cast<size_t>(k) * bg.By * bg.Bx + by * bg.Bx + bx) * g.R * g.S * g.Cg;
   const float* xg = x + static_cast<size_t>(n) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
   float acc = 0.0f;
   for (int r = 0; r < g.R; ++r) {
@@ -309,6 +418,10 @@ __global__ void __launch_bounds__(kDirectThreads) f32_direct_kernel(const float*
       const float* wp = wk + (static_cast<size_t>(r) * g.S + s) * g.Cg;
       for (int ci = 0; ci < g.Cg; ++ci) acc = __fadd_rn(acc, __fmul_rn(xp[ci], wp[ci]));
     }
+  }
+  if (bias != nullptr) {
+    acc = __fadd_rn(acc, bias[(static_cast<size_t>(k) * bg.By + (bias_mode == 0 ? by : 0)) * bg.Bx +
+                              (bias_mode == 0 ? bx : 0)]);
   }
   y[e] = acc;
 }
@@ -442,18 +555,21 @@ __global__ void __launch_bounds__(kDirectThreads) f32_sum_parts_kernel(const flo
 
 // dx of the convolution, the reference's cpu_bprop_nhwc order (cpu_ref.cpp:150-190): one
 // thread per dx element; for each tap (r, s) whose output position ho = (hi + ph - r dh) / sh
-// is whole and in range (likewise wo), acc += dy * w over the group's output channels.
+// is whole and in range (likewise wo), acc += dy * w over the group's output channels.  With a
+// blocked filter each tap takes the filter of its output position's block, as
+// cpu_block_bprop_nhwc (cpu_ref.cpp:272-314) does.
 __global__ void __launch_bounds__(kDirectThreads) f32_bprop_direct_kernel(const float* __restrict__ dy,
                                                                           const float* __restrict__ w,
                                                                           float* __restrict__ dx, Geom g,
-                                                                          long long total, Split3 sp) {
+                                                                          BlockGeom bg, long long total, Split3 sp) {
   const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
   if (e >= total) return;
   int c, wi, hi, n;
   sp.apply(e, total < (1LL << 31), c, wi, hi, n);
   const int grp = c / g.Cg;
   const int ci = c - grp * g.Cg;
-  const size_t wstride = static_cast<size_t>(g.R) * g.S * g.Cg;  // between output channels
+  const size_t tstride = static_cast<size_t>(g.R) * g.S * g.Cg;    // between filter blocks
+  const size_t wstride = tstride * bg.By * bg.Bx;                 // between output channels
   float acc = 0.0f;
   for (int r = 0; r < g.R; ++r) {
     const int hn = hi + g.ph - r * g.dh;
@@ -466,7 +582,9 @@ __global__ void __launch_bounds__(kDirectThreads) f32_bprop_direct_kernel(const 
       const int wo = wn / g.sw;
       if (wo >= g.Wo) continue;
       const float* dyp = dy + ((static_cast<size_t>(n) * g.Ho + ho) * g.Wo + wo) * g.K + static_cast<size_t>(grp) * g.Kg;
-      const float* wp = w + static_cast<size_t>(grp) * g.Kg * wstride + (static_cast<size_t>(r) * g.S + s) * g.Cg + ci;
+      const int blk = (ho / bg.bho) * bg.Bx + wo / bg.bwo;
+      const float* wp = w + static_cast<size_t>(grp) * g.Kg * wstride + blk * tstride +
+                        (static_cast<size_t>(r) * g.S + s) * g.Cg + ci;
       for (int ko = 0; ko < g.Kg; ++ko) acc = __fadd_rn(acc, __fmul_rn(dyp[ko], wp[ko * wstride]));
     }
   }
@@ -475,10 +593,12 @@ __global__ void __launch_bounds__(kDirectThreads) f32_bprop_direct_kernel(const 
 
 // dw of the convolution, the reference's cpu_grad_nhwc order (cpu_ref.cpp:192-230): one thread
 // per dw[k][r][s][ci] element, acc += x * dy over n, ho, wo in that order (in-bounds taps).
+// With a blocked filter, per dw[k][by][bx][r][s][ci] element over n and the block's positions,
+// the order of cpu_block_grad_nhwc (cpu_ref.cpp:316-369).
 __global__ void __launch_bounds__(kDirectThreads) f32_grad_direct_kernel(const float* __restrict__ x,
                                                                          const float* __restrict__ dy,
                                                                          float* __restrict__ dw, Geom g,
-                                                                         long long total) {
+                                                                         BlockGeom bg, long long total) {
   const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
   if (e >= total) return;
   const int ci = static_cast<int>(e % g.Cg);
@@ -486,18 +606,23 @@ __global__ void __launch_bounds__(kDirectThreads) f32_grad_direct_kernel(const f
   const int s = static_cast<int>(t1 % g.S);
   const long long t2 = t1 / g.S;
   const int r = static_cast<int>(t2 % g.R);
-  const int k = static_cast<int>(t2 / g.R);
+  const long long t3 = t2 / g.R;
+  const int nblk = bg.By * bg.Bx;
+  const int blk = static_cast<int>(t3 % nblk);
+  const int k = static_cast<int>(t3 / nblk);
+  const int ho0 = (blk / bg.Bx) * bg.bho;
+  const int wo0 = (blk - (blk / bg.Bx) * bg.Bx) * bg.bwo;
   const int grp = k / g.Kg;
   const float* xc = x + static_cast<size_t>(grp) * g.Cg + ci;
   const float* dyk = dy + k;
   float acc = 0.0f;
   for (int n = 0; n < g.N; ++n) {
-    for (int ho = 0; ho < g.Ho; ++ho) {
+    for (int ho = ho0; ho < ho0 + bg.bho; ++ho) {
       const int hi = ho * g.sh - g.ph + r * g.dh;
       if (hi < 0 || hi >= g.H) continue;
       const float* xrow = xc + (static_cast<size_t>(n) * g.H + hi) * g.W * g.C;
       const float* dyrow = dyk + (static_cast<size_t>(n) * g.Ho + ho) * g.Wo * g.K;
-      for (int wo = 0; wo < g.Wo; ++wo) {
+      for (int wo = wo0; wo < wo0 + bg.bwo; ++wo) {
         const int wi = wo * g.sw - g.pw + s * g.dw;
         if (wi < 0 || wi >= g.W) continue;
         acc = __fadd_rn(acc, __fmul_rn(xrow[static_cast<size_t>(wi) * g.C], dyrow[static_cast<size_t>(wo) * g.K]));
@@ -518,34 +643,43 @@ struct GradArgs {
   const float* x;
   const float* dy;
   float* dw;
-  float* part;  // split partial tiles (splits x K x kdim), or nullptr for float atomics
+  float* part;  // split partial tiles (splits x K x By x Bx x kdim), or nullptr for float atomics
   Geom g;
-  int P;       // N * Ho * Wo
+  int P;       // pixels per filter block: N * bho * bwo
   int kdim;    // R * S * Cg
   int tn;      // channel tiles per group
   int tiles;   // column tiles * channel tiles per group
   int cps;     // 16-pixel chunks per split
-  FastDivM fd_tn, fd_tiles, fd_gt;  // gt = G * tiles
+  int By, Bx, bho, bwo;  // filter blocks (1 x 1 of Ho x Wo: a plain KRSC filter)
+  FastDivM fd_tn, fd_tiles, fd_gt, fd_g;  // gt = G * By * Bx * tiles
   int gt;
 };
 
-// (n, ho, wo) of pixel index p, advanced one pixel or one chunk at a time
+// (n, ho, wo) of pixel index p within a block of rows x cols output positions, advanced one
+// pixel or one chunk at a time
 struct PixCursor {
   int n, ho, wo;
-  __device__ __forceinline__ void step(const Geom& g) {
-    if (++wo == g.Wo) {
+  __device__ __forceinline__ void init(int p, int rows, int cols) {
+    const int rc = rows * cols;
+    n = p / rc;
+    const int r0 = p - n * rc;
+    ho = r0 / cols;
+    wo = r0 - ho * cols;
+  }
+  __device__ __forceinline__ void step(int rows, int cols) {
+    if (++wo == cols) {
       wo = 0;
-      if (++ho == g.Ho) {
+      if (++ho == rows) {
         ho = 0;
         ++n;
       }
     }
   }
-  __device__ __forceinline__ void advance(const Geom& g, int d) {
+  __device__ __forceinline__ void advance(int rows, int cols, int d) {
     wo += d;
-    while (wo >= g.Wo) {
-      wo -= g.Wo;
-      if (++ho == g.Ho) {
+    while (wo >= cols) {
+      wo -= cols;
+      if (++ho == rows) {
         ho = 0;
         ++n;
       }
@@ -564,8 +698,13 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_grad_igemm_kernel(GradA
   const int lin = blockIdx.x;
   const int split = fdiv(lin, a.fd_gt);
   const int rem = lin - split * a.gt;
-  const int grp = fdiv(rem, a.fd_tiles);
-  const int rem2 = rem - grp * a.tiles;
+  const int gb = fdiv(rem, a.fd_tiles);  // block * G + group
+  const int rem2 = rem - gb * a.tiles;
+  const int blk = fdiv(gb, a.fd_g);
+  const int grp = gb - blk * g.G;
+  const int by0 = (blk / a.Bx) * a.bho;  // the block's first output row and column
+  const int bx0 = (blk - (blk / a.Bx) * a.Bx) * a.bwo;
+  const int nblk = a.By * a.Bx;
   const int tmi = fdiv(rem2, a.fd_tn);
   const int tni = rem2 - tmi * a.tn;
   const int m0 = tmi * kF32BM;
@@ -585,34 +724,34 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_grad_igemm_kernel(GradA
   const int as_ = tap - ar_ * g.S;
   const float* xg = a.x + static_cast<size_t>(grp) * g.Cg + aci;
   PixCursor pc;
-  {
-    const int p0 = min(pb + 4 * aq, a.P - 1);
-    const int hw = g.Ho * g.Wo;
-    pc.n = p0 / hw;
-    const int r0 = p0 - pc.n * hw;
-    pc.ho = r0 / g.Wo;
-    pc.wo = r0 - pc.ho * g.Wo;
-  }
+  pc.init(min(pb + 4 * aq, a.P - 1), a.bho, a.bwo);
   int cur_chunk = 0;
   // B: channel row, pixels pb + 16 c + 2 bp + e
   const int br = t >> 3;
   const int bp = t & 7;
   const int bk = grp * g.Kg + min(n0 + br, g.Kg - 1);
   const float* dyk = a.dy + bk;
+  PixCursor bc;
+  bc.init(min(pb + 2 * bp, a.P - 1), a.bho, a.bwo);
+  auto dy_off = [&](const PixCursor& q) {
+    return ((static_cast<size_t>(q.n) * g.Ho + by0 + q.ho) * g.Wo + bx0 + q.wo) * g.K;
+  };
+  const size_t ob0 = dy_off(bc);  // a valid offset for the pixels past the split
 
   auto load = [&](int c, v4f& va, v2f& vb, unsigned& oka, bool& okb) {
     if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
-      pc.advance(g, kF32KC);
+      pc.advance(a.bho, a.bwo, kF32KC);
+      bc.advance(a.bho, a.bwo, kF32KC);
       ++cur_chunk;
     }
     PixCursor q = pc;
     oka = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      if (e > 0) q.step(g);
+      if (e > 0) q.step(a.bho, a.bwo);
       const int pp = pb + c * kF32KC + 4 * aq + e;
-      const int hi = q.ho * g.sh - g.ph + ar_ * g.dh;
-      const int wi = q.wo * g.sw - g.pw + as_ * g.dw;
+      const int hi = (by0 + q.ho) * g.sh - g.ph + ar_ * g.dh;
+      const int wi = (bx0 + q.wo) * g.sw - g.pw + as_ * g.dw;
       const bool ok = pp < pe && hi >= 0 && hi < g.H && wi >= 0 && wi < g.W;
       oka |= static_cast<unsigned>(ok) << e;
       const size_t o = ok ? ((static_cast<size_t>(q.n) * g.H + hi) * g.W + wi) * g.C : 0;
@@ -620,9 +759,12 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_grad_igemm_kernel(GradA
     }
     const int pq = pb + c * kF32KC + 2 * bp;
     okb = pq < pe;  // pe - pb is not always even: the second pixel is checked at staging
-    const size_t ob = static_cast<size_t>(okb ? pq : pb) * g.K;
     const bool ok2 = pq + 1 < pe;
-    vb = v2f{dyk[ob], dyk[ob + (ok2 ? g.K : 0)]};
+    const size_t ob = okb ? dy_off(bc) : ob0;
+    PixCursor q2 = bc;
+    q2.step(a.bho, a.bwo);
+    const size_t ob2 = ok2 ? dy_off(q2) : ob;
+    vb = v2f{dyk[ob], dyk[ob2]};
   };
   const int sa_slot = f32_slot(ar, aq);
   const int sb_slot = f32_slot(br, bp >> 1);
@@ -688,19 +830,79 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_grad_igemm_kernel(GradA
       const int jcol = m0 + 32 * wm + 16 * im + (lane & 15);
       const int ch = n0 + 32 * wn + 16 * jn + 4 * (lane >> 4);
       if (jcol >= a.kdim) continue;
+      // dw[k][by][bx][j]
       if (a.part != nullptr) {
-        float* pt = a.part + static_cast<size_t>(split) * g.K * a.kdim;
+        float* pt = a.part + static_cast<size_t>(split) * g.K * nblk * a.kdim;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (ch + i < g.Kg) pt[static_cast<size_t>(grp * g.Kg + ch + i) * a.kdim + jcol] = acc[jn][im][i];
+          if (ch + i < g.Kg)
+            pt[(static_cast<size_t>(grp * g.Kg + ch + i) * nblk + blk) * a.kdim + jcol] = acc[jn][im][i];
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (ch + i < g.Kg)
-            unsafeAtomicAdd(a.dw + static_cast<size_t>(grp * g.Kg + ch + i) * a.kdim + jcol, acc[jn][im][i]);
+            unsafeAtomicAdd(a.dw + (static_cast<size_t>(grp * g.Kg + ch + i) * nblk + blk) * a.kdim + jcol,
+                            acc[jn][im][i]);
       }
     }
   }
+}
+
+// Bias gradient of the blocked convolution, the sum of dy over every output position of a block
+// (launch_block_grad_nhwc, cuda_kernels.cu:1112-1119, adds them all with float atomics), in a
+// fixed order: f32_dbias_part_kernel sums runs of kDbiasChunk consecutive positions of a block
+// ((n, lho, lwo) order) into part[blk][chunk][k], one thread per entry; f32_dbias_sum_kernel
+// adds a slot's runs in chunk order (bias_mode 0: dbias[k][by][bx]) or every block's runs in
+// block order (bias_mode 1: dbias[k][0][0], the other slots zero), starting from 0.
+constexpr int kDbiasChunk = 256;
+
+__global__ void __launch_bounds__(kDirectThreads) f32_dbias_part_kernel(const float* __restrict__ dy,
+                                                                        float* __restrict__ part, Geom g,
+                                                                        BlockGeom bg, int chunks, long long total) {
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;
+  const int k = static_cast<int>(e % g.K);
+  const long long t1 = e / g.K;
+  const int ch = static_cast<int>(t1 % chunks);
+  const int blk = static_cast<int>(t1 / chunks);
+  const int ho0 = (blk / bg.Bx) * bg.bho;
+  const int wo0 = (blk - (blk / bg.Bx) * bg.Bx) * bg.bwo;
+  const int P = g.N * bg.bho * bg.bwo;
+  const int p0 = ch * kDbiasChunk;
+  const int p1 = min(P, p0 + kDbiasChunk);
+  const int rc = bg.bho * bg.bwo;
+  int n = p0 / rc;
+  int lho = (p0 - n * rc) / bg.bwo;
+  int lwo = p0 - n * rc - lho * bg.bwo;
+  float acc = 0.0f;
+  for (int p = p0; p < p1; ++p) {
+    acc = __fadd_rn(acc, dy[((static_cast<size_t>(n) * g.Ho + ho0 + lho) * g.Wo + wo0 + lwo) * g.K + k]);
+    if (++lwo == bg.bwo) {
+      lwo = 0;
+      if (++lho == bg.bho) {
+        lho = 0;
+        ++n;
+      }
+    }
+  }
+  part[e] = acc;
+}
+
+__global__ void __launch_bounds__(kDirectThreads) f32_dbias_sum_kernel(const float* __restrict__ part,
+                                                                       float* __restrict__ dbias, int K, int nblk,
+                                                                       int chunks, int bias_mode, long long total) {
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;
+  const int k = static_cast<int>(e / nblk);
+  const int blk = static_cast<int>(e - static_cast<long long>(k) * nblk);
+  float acc = 0.0f;
+  if (bias_mode == 0 || blk == 0) {
+    const int b0 = bias_mode == 0 ? blk : 0;
+    const int b1 = bias_mode == 0 ? blk + 1 : nblk;
+    for (int b = b0; b < b1; ++b)
+      for (int c = 0; c < chunks; ++c) acc = __fadd_rn(acc, part[(static_cast<size_t>(b) * chunks + c) * K + k]);
+  }
+  dbias[e] = acc;
 }
 
 __global__ void __launch_bounds__(kDirectThreads) f32_zero_kernel(float* __restrict__ p, long long count) {
@@ -711,17 +913,18 @@ __global__ void __launch_bounds__(kDirectThreads) f32_zero_kernel(float* __restr
 
 }  // namespace
 
-bool f32_grad_igemm_eligible(const Geom& g, std::string* why) {
+bool f32_grad_igemm_eligible(const Geom& g, const BlockGeom& bg, std::string* why) {
   auto no = [&](const char* m) {
     if (why) *why = m;
     return false;
   };
-  const long long px = static_cast<long long>(g.N) * g.Ho * g.Wo;
+  const long long px = static_cast<long long>(g.N) * bg.bho * bg.bwo;
   const long long in = static_cast<long long>(g.N) * g.H * g.W * g.C;
   const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
   if (px == 0 || in == 0 || kdim == 0 || g.Kg == 0) return no("fp32 grad on MFMA needs non-empty x, dy and dw");
   if (px >= (1LL << 31) - 64 || kdim >= (1LL << 31) - kF32BM) return no("fp32 grad on MFMA extents exceed int32");
-  const long long tiles = ((kdim + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G;
+  const long long tiles = ((kdim + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G *
+                          static_cast<long long>(bg.By) * bg.Bx;
   if (tiles > (1LL << 20)) return no("fp32 grad on MFMA: more than 2^20 output tiles");
   return true;
 }
@@ -735,10 +938,11 @@ struct GradSplit {
   int cps;           // 16-pixel chunks per split
   long long splits;  // non-empty splits
 };
-GradSplit grad_split(const Geom& g, bool ordered) {
-  const long long P = static_cast<long long>(g.N) * g.Ho * g.Wo;
+GradSplit grad_split(const Geom& g, const BlockGeom& bg, bool ordered) {
+  const long long P = static_cast<long long>(g.N) * bg.bho * bg.bwo;
   const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
-  const long long gt = ((kdim + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G;
+  const long long gt = ((kdim + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G *
+                       static_cast<long long>(bg.By) * bg.Bx;
   const long long target = ordered ? 1024 : 2048;
   const long long chunks = (P + kF32KC - 1) / kF32KC;
   long long splits = std::max(1LL, std::min((target + gt - 1) / gt, (chunks + 7) / 8));
@@ -756,27 +960,29 @@ void launch_sum_parts(const float* part, float* dw, long long count, long long n
 
 }  // namespace
 
-size_t f32_grad_igemm_workspace(const Geom& g) {
-  const GradSplit sp = grad_split(g, true);
+size_t f32_grad_igemm_workspace(const Geom& g, const BlockGeom& bg) {
+  const GradSplit sp = grad_split(g, bg, true);
   if (sp.splits <= 1) return 0;
-  return static_cast<size_t>(sp.splits) * g.K * g.R * g.S * g.Cg * sizeof(float);
+  return static_cast<size_t>(sp.splits) * g.K * bg.By * bg.Bx * g.R * g.S * g.Cg * sizeof(float);
 }
 
-hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, float* ws,
-                                 bool ordered, hipStream_t stream) {
+hipError_t launch_f32_grad_igemm(const Geom& g, const BlockGeom& bg, const float* x, const float* dy, float* dw,
+                                 float* ws, bool ordered, hipStream_t stream) {
   GradArgs a;
   a.x = x; a.dy = dy; a.dw = dw; a.g = g;
-  a.P = g.N * g.Ho * g.Wo;
+  a.By = bg.By; a.Bx = bg.Bx; a.bho = bg.bho; a.bwo = bg.bwo;
+  a.P = g.N * bg.bho * bg.bwo;
   a.kdim = g.R * g.S * g.Cg;
   a.tn = (g.Kg + kF32BN - 1) / kF32BN;
   a.tiles = ((a.kdim + kF32BM - 1) / kF32BM) * a.tn;
-  a.gt = a.tiles * g.G;
-  const GradSplit sp = grad_split(g, ordered);
+  a.gt = a.tiles * g.G * bg.By * bg.Bx;
+  const GradSplit sp = grad_split(g, bg, ordered);
   a.cps = sp.cps;
   a.fd_tn = fastdiv_m(a.tn);
   a.fd_tiles = fastdiv_m(a.tiles);
   a.fd_gt = fastdiv_m(a.gt);
-  const long long count = static_cast<long long>(g.K) * a.kdim;
+  a.fd_g = fastdiv_m(g.G);
+  const long long count = static_cast<long long>(g.K) * bg.By * bg.Bx * a.kdim;
   const unsigned blocks = static_cast<unsigned>(sp.splits * a.gt);
   if (ordered) {
     // one split writes dw directly; more write their partial tiles, summed in split order
@@ -806,25 +1012,65 @@ hipError_t launch_f32_depthwise(const Geom& g, const float* x, const float* w, f
   return hipGetLastError();
 }
 
-hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream) {
+hipError_t launch_f32_bprop_direct(const Geom& g, const BlockGeom& bg, const float* dy, const float* w, float* dx,
+                                   hipStream_t stream) {
   const long long total = static_cast<long long>(g.N) * g.H * g.W * g.C;
   if (total == 0) return hipSuccess;
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
   hipLaunchKernelGGL(f32_bprop_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream,
-                     dy, w, dx, g, total, make_split3(g.C, g.W, g.H));
+                     dy, w, dx, g, bg, total, make_split3(g.C, g.W, g.H));
   return hipGetLastError();
 }
 
-hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream) {
-  const long long total = static_cast<long long>(g.K) * g.R * g.S * g.Cg;
+hipError_t launch_f32_grad_direct(const Geom& g, const BlockGeom& bg, const float* x, const float* dy, float* dw,
+                                  hipStream_t stream) {
+  const long long total = static_cast<long long>(g.K) * bg.By * bg.Bx * g.R * g.S * g.Cg;
   if (total == 0) return hipSuccess;
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
   hipLaunchKernelGGL(f32_grad_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, x,
-                     dy, dw, g, total);
+                     dy, dw, g, bg, total);
   return hipGetLastError();
 }
 
-bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why) {
+size_t f32_block_dbias_workspace(const Geom& g, const BlockGeom& bg) {
+  const long long P = static_cast<long long>(g.N) * bg.bho * bg.bwo;
+  const long long chunks = (P + kDbiasChunk - 1) / kDbiasChunk;
+  return static_cast<size_t>(bg.By) * bg.Bx * chunks * g.K * sizeof(float);
+}
+
+hipError_t launch_f32_block_dbias(const Geom& g, const BlockGeom& bg, const float* dy, float* dbias, int bias_mode,
+                                  float* ws, hipStream_t stream) {
+  const int P = g.N * bg.bho * bg.bwo;
+  const int chunks = (P + kDbiasChunk - 1) / kDbiasChunk;
+  const long long parts = static_cast<long long>(bg.By) * bg.Bx * chunks * g.K;
+  if (parts > 0) {
+    const long long blocks = (parts + kDirectThreads - 1) / kDirectThreads;
+    hipLaunchKernelGGL(f32_dbias_part_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream,
+                       dy, ws, g, bg, chunks, parts);
+  }
+  const long long slots = static_cast<long long>(g.K) * bg.By * bg.Bx;
+  if (slots > 0) {
+    const long long blocks = (slots + kDirectThreads - 1) / kDirectThreads;
+    hipLaunchKernelGGL(f32_dbias_sum_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, ws,
+                       dbias, g.K, bg.By * bg.Bx, chunks, bias_mode, slots);
+  }
+  return hipGetLastError();
+}
+
+namespace {
+
+// Output regions of the implicit GEMM (F32Args): forward, the filter blocks themselves; the
+// transposed form, By x Bx regions of ceil(Ho / By) x ceil(Wo / Bx) positions (the last ones
+// clipped), so that most tiles reach the input positions of one filter block only.
+struct Regions {
+  int ry, rx, rh, rw;
+};
+Regions fprop_regions(const BlockGeom& bg) { return Regions{bg.By, bg.Bx, bg.bho, bg.bwo}; }
+Regions bprop_regions(const Geom& b, const BlockGeom& bg) {
+  return Regions{bg.By, bg.Bx, (b.Ho + bg.By - 1) / bg.By, (b.Wo + bg.Bx - 1) / bg.Bx};
+}
+
+bool igemm_fits(const Geom& g, const Regions& rg, const void* x, const void* w, std::string* why) {
   auto no = [&](const char* m) {
     if (why) *why = m;
     return false;
@@ -834,22 +1080,27 @@ bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(w) & 15u) != 0) {
     return no("fp32 implicit GEMM needs 16-byte aligned x and w");
   }
-  const long long m = static_cast<long long>(g.N) * g.Ho * g.Wo;
+  const long long m = static_cast<long long>(g.N) * rg.rh * rg.rw;
   const long long kdim = static_cast<long long>(g.R) * g.S * g.Cg;
-  if (m >= (1LL << 31) - kF32BM || kdim >= (1LL << 31) - kF32KC) return no("fp32 implicit GEMM extents exceed int32");
-  const long long tiles = ((m + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G;
+  if (m >= (1LL << 31) - 2 * kF32BM || kdim >= (1LL << 31) - kF32KC) {
+    return no("fp32 implicit GEMM extents exceed int32");
+  }
+  const long long tiles =
+      ((m + kF32BM - 1) / kF32BM) * ((g.Kg + kF32BN - 1) / kF32BN) * g.G * static_cast<long long>(rg.ry) * rg.rx;
   if (tiles > (1LL << 22)) return no("fp32 implicit GEMM grid exceeds 2^22 workgroups");
   return true;
 }
 
-namespace {
-hipError_t f32_igemm_launch(const Geom& g, const float* x, const float* w, float* y, bool transposed,
-                            hipStream_t stream) {
+hipError_t f32_igemm_launch(const Geom& g, const BlockGeom& bg, const Regions& rg, const float* x, const float* w,
+                            const float* bias, int bias_mode, float* y, bool transposed, hipStream_t stream) {
   F32Args a;
-  a.x = x; a.w = w; a.y = y; a.g = g;
+  a.x = x; a.w = w; a.y = y; a.bias = bias; a.g = g;
   a.ow_taps = g.R * g.S;
   a.ow_cg = g.Kg;
-  a.M = g.N * g.Ho * g.Wo;
+  a.ry = rg.ry; a.rx = rg.rx; a.rh = rg.rh; a.rw = rg.rw;
+  a.By = bg.By; a.Bx = bg.Bx; a.bho = bg.bho; a.bwo = bg.bwo;
+  a.bias_mode = bias_mode;
+  a.M = g.N * rg.rh * rg.rw;
   a.kdim = g.R * g.S * g.Cg;
   a.nchunks = (a.kdim + kF32KC - 1) / kF32KC;
   const bool narrow = g.Kg <= 32;  // 256 pixels x 32 channels per workgroup
@@ -858,7 +1109,10 @@ hipError_t f32_igemm_launch(const Geom& g, const float* x, const float* w, float
   a.tiles = ((a.M + bm - 1) / bm) * a.tn;
   a.fd_tn = fastdiv_m(a.tn);
   a.fd_tiles = fastdiv_m(a.tiles);
-  const unsigned blocks = static_cast<unsigned>(a.tiles) * static_cast<unsigned>(g.G);
+  a.fd_regions = fastdiv_m(rg.ry * rg.rx);
+  a.fd_rx = fastdiv_m(rg.rx);
+  const unsigned blocks = static_cast<unsigned>(a.tiles) * static_cast<unsigned>(g.G) *
+                          static_cast<unsigned>(rg.ry * rg.rx);
   const dim3 grid(blocks), block(64 * kF32Waves);
   if (transposed) {
     if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<true, 32>), grid, block, 0, stream, a);
@@ -871,8 +1125,13 @@ hipError_t f32_igemm_launch(const Geom& g, const float* x, const float* w, float
 }
 }  // namespace
 
-hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {
-  return f32_igemm_launch(g, x, w, y, false, stream);
+bool f32_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, std::string* why) {
+  return igemm_fits(g, fprop_regions(bg), x, w, why);
+}
+
+hipError_t launch_f32_igemm(const Geom& g, const BlockGeom& bg, const float* x, const float* w, const float* bias,
+                            int bias_mode, float* y, hipStream_t stream) {
+  return f32_igemm_launch(g, bg, fprop_regions(bg), x, w, bias, bias_mode, y, false, stream);
 }
 
 // The bprop of a stride-1 convolution g as the forward convolution of dy (N x Ho x Wo x K)
@@ -888,26 +1147,31 @@ Geom f32_bprop_as_fprop(const Geom& g) {
   return b;
 }
 
-bool f32_bprop_igemm_eligible(const Geom& g, const void* dy, const void* w, std::string* why) {
+bool f32_bprop_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* dy, const void* w, std::string* why) {
   if (g.sh != 1 || g.sw != 1) {
     if (why) *why = "fp32 bprop on MFMA needs stride 1";
     return false;
   }
-  return f32_igemm_eligible(f32_bprop_as_fprop(g), dy, w, why);
+  const Geom b = f32_bprop_as_fprop(g);
+  return igemm_fits(b, bprop_regions(b, bg), dy, w, why);
 }
 
 // Rows of the transposed filter are the original's input channels (b.Kg = g.Cg), its reduction
 // (r', s', ko < g.Kg = b.Cg); f32_igemm_launch takes ow_taps = R * S and ow_cg = b.Kg from b.
-hipError_t launch_f32_bprop_igemm(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream) {
-  return f32_igemm_launch(f32_bprop_as_fprop(g), dy, w, dx, true, stream);
+// The filter blocks partition dy (bg: blocks of the original output).
+hipError_t launch_f32_bprop_igemm(const Geom& g, const BlockGeom& bg, const float* dy, const float* w, float* dx,
+                                  hipStream_t stream) {
+  const Geom b = f32_bprop_as_fprop(g);
+  return f32_igemm_launch(b, bg, bprop_regions(b, bg), dy, w, nullptr, 0, dx, true, stream);
 }
 
-hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream) {
+hipError_t launch_f32_direct(const Geom& g, const BlockGeom& bg, const float* x, const float* w, const float* bias,
+                             int bias_mode, float* y, hipStream_t stream) {
   const long long total = static_cast<long long>(g.N) * g.Ho * g.Wo * g.K;
   if (total == 0) return hipSuccess;
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
   hipLaunchKernelGGL(f32_direct_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream, x, w,
-                     y, g, total, make_split3(g.K, g.Wo, g.Ho));
+                     y, g, bg, bias, bias_mode, total, make_split3(g.K, g.Wo, g.Ho));
   return hipGetLastError();
 }
 

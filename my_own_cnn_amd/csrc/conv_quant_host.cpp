@@ -78,6 +78,29 @@ void launch_grad_nhwc(const float* d_x, const float* d_dy, float* d_dw, int n, i
                  "launch_grad_nhwc");
 }
 
+void launch_block_fprop_nhwc(const float* d_x, const float* d_w, float* d_y, int n, int h, int w, int c, int r, int s,
+                             int k, const BlockConv2DParams& p, const float* d_bias, BlockBiasMode bias_mode) {
+  const miq_block_conv2d_params bp = to_c(p);
+  throw_on_error(miq_block_fprop_nhwc_f32(d_x, d_w, d_y, n, h, w, c, r, s, k, &bp, d_bias,
+                                          static_cast<int32_t>(bias_mode), MIQ_ALGO_AUTO, nullptr),
+                 "launch_block_fprop_nhwc");
+}
+
+void launch_block_bprop_nhwc(const float* d_dy, const float* d_w, float* d_dx, int n, int h, int w, int c, int r,
+                             int s, int k, const BlockConv2DParams& p) {
+  const miq_block_conv2d_params bp = to_c(p);
+  throw_on_error(miq_block_bprop_nhwc_f32(d_dy, d_w, d_dx, n, h, w, c, r, s, k, &bp, MIQ_ALGO_AUTO, nullptr),
+                 "launch_block_bprop_nhwc");
+}
+
+void launch_block_grad_nhwc(const float* d_x, const float* d_dy, float* d_dw, int n, int h, int w, int c, int r, int s,
+                            int k, const BlockConv2DParams& p, float* d_dbias, BlockBiasMode bias_mode) {
+  const miq_block_conv2d_params bp = to_c(p);
+  throw_on_error(miq_block_grad_nhwc_f32(d_x, d_dy, d_dw, n, h, w, c, r, s, k, &bp, d_dbias,
+                                         static_cast<int32_t>(bias_mode), MIQ_ALGO_AUTO, nullptr),
+                 "launch_block_grad_nhwc");
+}
+
 namespace conv_quant_detail {
 
 void launch_fprop_nhwc_qi32_u8(const float* d_x, const float* d_w, int32_t* d_y, int n, int h, int w, int c, int r,

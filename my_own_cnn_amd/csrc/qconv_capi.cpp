@@ -85,6 +85,66 @@ int check_tensors(const miq::Geom& g, long long filt, const void* x, const void*
   return MIQ_OK;
 }
 
+// The fp32 forward pass (miq_fprop_nhwc_f32, miq_block_fprop_nhwc_f32): bias and the
+// depthwise kernel only with a plain filter and no bias.
+int fprop_f32(const miq::Geom& g, const miq::BlockGeom& bg, const float* x, const float* w, const float* bias,
+              int32_t bias_mode, float* y, int32_t algo, void* stream) {
+  int st = check_tensors(g, filt_elems(g) * bg.By * bg.Bx, x, w, y);
+  if (st != MIQ_OK) return st;
+  if (bias_mode != 0 && bias_mode != 1) return fail(MIQ_ERR_INVALID_ARGUMENT, "bias_mode must be 0 (per block) or 1 (shared)");
+  std::string why;
+  bool igemm = false;
+  switch (algo) {
+    case MIQ_ALGO_AUTO: igemm = miq::f32_igemm_eligible(g, bg, x, w, nullptr); break;
+    case MIQ_ALGO_DIRECT: igemm = false; break;
+    case MIQ_ALGO_IGEMM:
+      if (!miq::f32_igemm_eligible(g, bg, x, w, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      igemm = true;
+      break;
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 convolution algo must be AUTO, DIRECT or IGEMM");
+  }
+  if (out_elems(g) == 0) return MIQ_OK;
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const bool dense = bg.By == 1 && bg.Bx == 1 && bias == nullptr;
+  hipError_t e;
+  if (igemm) {
+    e = miq::launch_f32_igemm(g, bg, x, w, bias, bias_mode, y, hs);
+  } else if (algo == MIQ_ALGO_AUTO && dense && miq::f32_depthwise_eligible(g, x, y)) {
+    e = miq::launch_f32_depthwise(g, x, w, y, hs);
+  } else {
+    e = miq::launch_f32_direct(g, bg, x, w, bias, bias_mode, y, hs);
+  }
+  if (e != hipSuccess) return hip_fail(e, "fp32 convolution launch");
+  return MIQ_OK;
+}
+
+// The fp32 dx pass (miq_bprop_nhwc_f32, miq_block_bprop_nhwc_f32).
+int bprop_f32(const miq::Geom& g, const miq::BlockGeom& bg, const float* dy, const float* w, float* dx, int32_t algo,
+              void* stream) {
+  // dy has the output's extent, dx the input's
+  if (in_elems(g) > 0 && dx == nullptr) return fail(MIQ_ERR_NULL_POINTER, "dx pointer is NULL");
+  if (out_elems(g) > 0 && dy == nullptr) return fail(MIQ_ERR_NULL_POINTER, "dy pointer is NULL");
+  if (filt_elems(g) * bg.By * bg.Bx > 0 && w == nullptr) return fail(MIQ_ERR_NULL_POINTER, "filter pointer is NULL");
+  if (in_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dx has more than 2^32-256 elements");
+  std::string why;
+  bool igemm = false;
+  switch (algo) {
+    case MIQ_ALGO_AUTO: igemm = miq::f32_bprop_igemm_eligible(g, bg, dy, w, nullptr); break;
+    case MIQ_ALGO_DIRECT: igemm = false; break;
+    case MIQ_ALGO_IGEMM:
+      if (!miq::f32_bprop_igemm_eligible(g, bg, dy, w, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      igemm = true;
+      break;
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 bprop algo must be AUTO, DIRECT or IGEMM");
+  }
+  if (in_elems(g) == 0) return MIQ_OK;
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const hipError_t e = igemm ? miq::launch_f32_bprop_igemm(g, bg, dy, w, dx, hs)
+                             : miq::launch_f32_bprop_direct(g, bg, dy, w, dx, hs);
+  if (e != hipSuccess) return hip_fail(e, "fp32 bprop launch");
+  return MIQ_OK;
+}
+
 int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const miq::Geom& g,
                const miq::BlockGeom& bg, const void* in_qp, const void* f_qp, void* stream) {
   const long long filt = filt_elems(g) * bg.By * bg.Bx;
@@ -301,61 +361,37 @@ int miq_qconv2d_nhwc_i8_dequant(const miq_qconv_desc* d, const int8_t* x, const 
 int miq_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
                        int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
   miq::Geom g;
-  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
   if (st != MIQ_OK) return st;
-  st = check_tensors(g, filt_elems(g), x, w, y);
+  return fprop_f32(g, miq::dense_blocks(g), x, w, nullptr, 0, y, algo, stream);
+}
+
+int miq_block_fprop_nhwc_f32(const float* x, const float* w, float* y, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                             int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p, const float* bias,
+                             int32_t bias_mode, int32_t algo, void* stream) {
+  miq::Geom g;
+  miq::BlockGeom bg;
+  const int st = infer_block_geom(n, h, wdt, c, r, s, k, p, &g, &bg);
   if (st != MIQ_OK) return st;
-  std::string why;
-  bool igemm = false;
-  switch (algo) {
-    case MIQ_ALGO_AUTO: igemm = miq::f32_igemm_eligible(g, x, w, nullptr); break;
-    case MIQ_ALGO_DIRECT: igemm = false; break;
-    case MIQ_ALGO_IGEMM:
-      if (!miq::f32_igemm_eligible(g, x, w, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
-      igemm = true;
-      break;
-    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 convolution algo must be AUTO, DIRECT or IGEMM");
-  }
-  if (out_elems(g) == 0) return MIQ_OK;
-  const hipStream_t hs = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (igemm) {
-    e = miq::launch_f32_igemm(g, x, w, y, hs);
-  } else if (algo == MIQ_ALGO_AUTO && miq::f32_depthwise_eligible(g, x, y)) {
-    e = miq::launch_f32_depthwise(g, x, w, y, hs);
-  } else {
-    e = miq::launch_f32_direct(g, x, w, y, hs);
-  }
-  if (e != hipSuccess) return hip_fail(e, "fp32 convolution launch");
-  return MIQ_OK;
+  return fprop_f32(g, bg, x, w, bias, bias_mode, y, algo, stream);
 }
 
 int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, int32_t h, int32_t wdt, int32_t c,
                        int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
   miq::Geom g;
-  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
   if (st != MIQ_OK) return st;
-  // dy has the output's extent, dx the input's
-  if (in_elems(g) > 0 && dx == nullptr) return fail(MIQ_ERR_NULL_POINTER, "dx pointer is NULL");
-  if (out_elems(g) > 0 && dy == nullptr) return fail(MIQ_ERR_NULL_POINTER, "dy pointer is NULL");
-  if (filt_elems(g) > 0 && w == nullptr) return fail(MIQ_ERR_NULL_POINTER, "filter pointer is NULL");
-  if (in_elems(g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dx has more than 2^32-256 elements");
-  std::string why;
-  bool igemm = false;
-  switch (algo) {
-    case MIQ_ALGO_AUTO: igemm = miq::f32_bprop_igemm_eligible(g, dy, w, nullptr); break;
-    case MIQ_ALGO_DIRECT: igemm = false; break;
-    case MIQ_ALGO_IGEMM:
-      if (!miq::f32_bprop_igemm_eligible(g, dy, w, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
-      igemm = true;
-      break;
-    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 bprop algo must be AUTO, DIRECT or IGEMM");
-  }
-  if (in_elems(g) == 0) return MIQ_OK;
-  const hipStream_t hs = static_cast<hipStream_t>(stream);
-  const hipError_t e = igemm ? miq::launch_f32_bprop_igemm(g, dy, w, dx, hs) : miq::launch_f32_bprop_direct(g, dy, w, dx, hs);
-  if (e != hipSuccess) return hip_fail(e, "fp32 bprop launch");
-  return MIQ_OK;
+  return bprop_f32(g, miq::dense_blocks(g), dy, w, dx, algo, stream);
+}
+
+int miq_block_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                             int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p, int32_t algo,
+                             void* stream) {
+  miq::Geom g;
+  miq::BlockGeom bg;
+  const int st = infer_block_geom(n, h, wdt, c, r, s, k, p, &g, &bg);
+  if (st != MIQ_OK) return st;
+  return bprop_f32(g, bg, dy, w, dx, algo, stream);
 }
 
 }  // extern "C"
@@ -366,64 +402,75 @@ namespace {
 enum GradKind { kGradDirect, kGradIgemm, kGradDepthwise };
 struct GradChoice {
   GradKind kind;
-  bool ordered;  // split sums in a fixed order (workspace); false: float atomics
-  size_t ws_bytes;
+  bool ordered;      // split sums in a fixed order (workspace); false: float atomics
+  size_t ws_bytes;   // dw's split sums, then (with dbias) the bias gradient's runs
+  size_t dbias_off;  // byte offset of the bias gradient's runs in the workspace
 };
 
-int grad_choose(const miq::Geom& g, const void* x, const void* dy, int32_t algo, GradChoice* ch) {
+int grad_choose(const miq::Geom& g, const miq::BlockGeom& bg, const void* x, const void* dy, int32_t algo,
+                bool with_dbias, GradChoice* ch) {
   std::string why;
+  const bool dense = bg.By == 1 && bg.Bx == 1;
   switch (algo) {
     case MIQ_ALGO_AUTO:
     case MIQ_ALGO_ATOMIC:
-      ch->kind = miq::f32_depthwise_grad_eligible(g, x, dy) ? kGradDepthwise
-                 : miq::f32_grad_igemm_eligible(g, nullptr) ? kGradIgemm
-                                                            : kGradDirect;
+      ch->kind = dense && miq::f32_depthwise_grad_eligible(g, x, dy) ? kGradDepthwise
+                 : miq::f32_grad_igemm_eligible(g, bg, nullptr)      ? kGradIgemm
+                                                                     : kGradDirect;
       break;
     case MIQ_ALGO_DIRECT: ch->kind = kGradDirect; break;
     case MIQ_ALGO_IGEMM:
-      if (!miq::f32_grad_igemm_eligible(g, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      if (!miq::f32_grad_igemm_eligible(g, bg, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       ch->kind = kGradIgemm;
       break;
     default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 grad algo must be AUTO, DIRECT, IGEMM or ATOMIC");
   }
   ch->ordered = algo != MIQ_ALGO_ATOMIC;
-  ch->ws_bytes = !ch->ordered || filt_elems(g) == 0 ? 0
-                 : ch->kind == kGradIgemm           ? miq::f32_grad_igemm_workspace(g)
-                 : ch->kind == kGradDepthwise       ? miq::f32_depthwise_grad_workspace(g)
-                                                    : 0;
+  const size_t part = !ch->ordered || filt_elems(g) == 0 ? 0
+                      : ch->kind == kGradIgemm           ? miq::f32_grad_igemm_workspace(g, bg)
+                      : ch->kind == kGradDepthwise       ? miq::f32_depthwise_grad_workspace(g)
+                                                         : 0;
+  ch->dbias_off = (part + 255) & ~static_cast<size_t>(255);
+  ch->ws_bytes = with_dbias ? ch->dbias_off + miq::f32_block_dbias_workspace(g, bg) : part;
   return MIQ_OK;
 }
 
-int grad_validate(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
-                  int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, miq::Geom* g,
-                  GradChoice* ch) {
-  int st = infer_geom(n, h, wdt, c, r, s, k, p, g);
+int grad_validate(const float* x, const float* dy, float* dw, const miq::Geom& g, const miq::BlockGeom& bg,
+                  const float* dbias, int32_t bias_mode, int32_t algo, GradChoice* ch) {
+  const long long filt = filt_elems(g) * bg.By * bg.Bx;
+  int st = check_tensors(g, filt, x, dw, dy);
   if (st != MIQ_OK) return st;
-  st = check_tensors(*g, filt_elems(*g), x, dw, dy);
-  if (st != MIQ_OK) return st;
-  if (filt_elems(*g) > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dw has more than 2^32-256 elements");
-  return grad_choose(*g, x, dy, algo, ch);
+  if (filt > kMaxDirectElems) return fail(MIQ_ERR_UNSUPPORTED, "dw has more than 2^32-256 elements");
+  if (bias_mode != 0 && bias_mode != 1) return fail(MIQ_ERR_INVALID_ARGUMENT, "bias_mode must be 0 (per block) or 1 (shared)");
+  return grad_choose(g, bg, x, dy, algo, dbias != nullptr, ch);
 }
 
-int grad_launch(const miq::Geom& g, const GradChoice& ch, const float* x, const float* dy, float* dw, void* ws,
-                void* stream) {
-  if (filt_elems(g) == 0) return MIQ_OK;
+int grad_launch(const miq::Geom& g, const miq::BlockGeom& bg, const GradChoice& ch, const float* x, const float* dy,
+                float* dw, float* dbias, int32_t bias_mode, void* ws, void* stream) {
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   float* wsf = static_cast<float*>(ws);
-  hipError_t e;
-  switch (ch.kind) {
-    case kGradDepthwise: e = miq::launch_f32_depthwise_grad(g, x, dy, dw, wsf, ch.ordered, hs); break;
-    case kGradIgemm: e = miq::launch_f32_grad_igemm(g, x, dy, dw, wsf, ch.ordered, hs); break;
-    default: e = miq::launch_f32_grad_direct(g, x, dy, dw, hs); break;
+  hipError_t e = hipSuccess;
+  if (filt_elems(g) > 0) {
+    switch (ch.kind) {
+      case kGradDepthwise: e = miq::launch_f32_depthwise_grad(g, x, dy, dw, wsf, ch.ordered, hs); break;
+      case kGradIgemm: e = miq::launch_f32_grad_igemm(g, bg, x, dy, dw, wsf, ch.ordered, hs); break;
+      default: e = miq::launch_f32_grad_direct(g, bg, x, dy, dw, hs); break;
+    }
+    if (e != hipSuccess) return hip_fail(e, "fp32 grad launch");
   }
-  if (e != hipSuccess) return hip_fail(e, "fp32 grad launch");
+  if (dbias != nullptr && static_cast<long long>(g.K) * bg.By * bg.Bx > 0) {
+    float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + ch.dbias_off);
+    e = miq::launch_f32_block_dbias(g, bg, dy, dbias, bias_mode, part, hs);
+    if (e != hipSuccess) return hip_fail(e, "fp32 bias gradient launch");
+  }
   return MIQ_OK;
 }
 
-// Grow-only device workspace per device for miq_grad_nhwc_f32 (the reference keeps one static
-// workspace for its fp32 path, cuda_kernels.cu:155-158, grown by ensure_capacity).  Growing
-// waits for the device before freeing the old buffer, which earlier launches may still read.
-// Calls that overlap on one device share it and race, as the reference's do.
+// Grow-only device workspace per device for miq_grad_nhwc_f32 and miq_block_grad_nhwc_f32
+// (the reference keeps one static workspace for its fp32 path, cuda_kernels.cu:155-158, grown
+// by ensure_capacity).  Growing waits for the device before freeing the old buffer, which
+// earlier launches may still read.  Calls that overlap on one device share it and race, as the
+// reference's do.
 struct DeviceWorkspace {
   std::mutex m;
   void* p = nullptr;
@@ -460,11 +507,52 @@ int cached_workspace(size_t bytes, void** out) {
   return MIQ_OK;
 }
 
+// The kernel family a pass runs (miq_plan_f32, miq_plan_block_f32), with 16-byte aligned tensors.
+int plan_f32(int32_t op, const miq::Geom& g, const miq::BlockGeom& bg, int32_t algo, int32_t* kernel) {
+  static const float kAligned[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const void* al = static_cast<const void*>(kAligned);
+  const bool dense = bg.By == 1 && bg.Bx == 1;
+  std::string why;
+  switch (op) {
+    case 0:  // fprop: the order of fprop_f32
+      switch (algo) {
+        case MIQ_ALGO_AUTO:
+          *kernel = miq::f32_igemm_eligible(g, bg, al, al, nullptr) ? (g.Kg <= 32 ? MIQ_F32_IGEMM32 : MIQ_F32_IGEMM)
+                    : dense && miq::f32_depthwise_eligible(g, al, al) ? MIQ_F32_DEPTHWISE
+                                                                       : MIQ_F32_DIRECT;
+          return MIQ_OK;
+        case MIQ_ALGO_DIRECT: *kernel = MIQ_F32_DIRECT; return MIQ_OK;
+        case MIQ_ALGO_IGEMM:
+          if (!miq::f32_igemm_eligible(g, bg, al, al, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+          *kernel = g.Kg <= 32 ? MIQ_F32_IGEMM32 : MIQ_F32_IGEMM;
+          return MIQ_OK;
+        default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 convolution algo must be AUTO, DIRECT or IGEMM");
+      }
+    case 1:  // bprop: the order of bprop_f32
+      switch (algo) {
+        case MIQ_ALGO_AUTO:
+          *kernel = miq::f32_bprop_igemm_eligible(g, bg, al, al, nullptr) ? MIQ_F32_BPROP_IGEMM : MIQ_F32_DIRECT;
+          return MIQ_OK;
+        case MIQ_ALGO_DIRECT: *kernel = MIQ_F32_DIRECT; return MIQ_OK;
+        case MIQ_ALGO_IGEMM:
+          if (!miq::f32_bprop_igemm_eligible(g, bg, al, al, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+          *kernel = MIQ_F32_BPROP_IGEMM;
+          return MIQ_OK;
+        default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 bprop algo must be AUTO, DIRECT or IGEMM");
+      }
+    case 2: {  // grad: grad_choose
+      GradChoice ch;
+      const int st = grad_choose(g, bg, al, al, algo, false, &ch);
+      if (st != MIQ_OK) return st;
+      *kernel = ch.kind == kGradDepthwise ? MIQ_F32_GRAD_DEPTHWISE : ch.kind == kGradIgemm ? MIQ_F32_GRAD_IGEMM
+                                                                                          : MIQ_F32_DIRECT;
+      return MIQ_OK;
+    }
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "op must be 0 (fprop), 1 (bprop) or 2 (grad)");
+  }
+}
+
 }  // namespace
-
-extern "C" {
-
-}  // extern "C"
 
 namespace miq {
 
@@ -472,9 +560,12 @@ int report_error(int status, const std::string& msg) { return fail(status, msg);
 
 int grad_f32_check(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r,
                    int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, size_t* ws_bytes) {
+  *ws_bytes = 0;
   miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
   GradChoice ch{};
-  const int st = grad_validate(x, dy, dw, n, h, wdt, c, r, s, k, p, algo, &g, &ch);
+  st = grad_validate(x, dy, dw, g, miq::dense_blocks(g), nullptr, 0, algo, &ch);
   *ws_bytes = st == MIQ_OK ? ch.ws_bytes : 0;
   return st;
 }
@@ -495,9 +586,10 @@ int miq_grad_nhwc_f32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_t 
   GradChoice aligned{}, unaligned{};
   const float* a16 = reinterpret_cast<const float*>(static_cast<uintptr_t>(256));
   const float* a4 = reinterpret_cast<const float*>(static_cast<uintptr_t>(260));
-  st = grad_choose(g, a16, a16, algo, &aligned);
+  const miq::BlockGeom bg = miq::dense_blocks(g);
+  st = grad_choose(g, bg, a16, a16, algo, false, &aligned);
   if (st != MIQ_OK) return st;
-  st = grad_choose(g, a4, a4, algo, &unaligned);
+  st = grad_choose(g, bg, a4, a4, algo, false, &unaligned);
   if (st != MIQ_OK) return st;
   *bytes = aligned.ws_bytes > unaligned.ws_bytes ? aligned.ws_bytes : unaligned.ws_bytes;
   return MIQ_OK;
@@ -507,76 +599,69 @@ int miq_grad_nhwc_f32_ws(const float* x, const float* dy, float* dw, int32_t n, 
                          int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* workspace,
                          size_t workspace_bytes, void* stream) {
   miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  const miq::BlockGeom bg = miq::dense_blocks(g);
   GradChoice ch{};
-  int st = grad_validate(x, dy, dw, n, h, wdt, c, r, s, k, p, algo, &g, &ch);
+  st = grad_validate(x, dy, dw, g, bg, nullptr, 0, algo, &ch);
   if (st != MIQ_OK) return st;
   if (ch.ws_bytes > 0 && workspace == nullptr) return fail(MIQ_ERR_NULL_POINTER, "workspace pointer is NULL");
   if (workspace_bytes < ch.ws_bytes) {
     return fail(MIQ_ERR_INVALID_ARGUMENT, "workspace is smaller than miq_grad_nhwc_f32_workspace_size reports");
   }
-  return grad_launch(g, ch, x, dy, dw, workspace, stream);
+  return grad_launch(g, bg, ch, x, dy, dw, nullptr, 0, workspace, stream);
 }
 
 int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream) {
   miq::Geom g;
+  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  const miq::BlockGeom bg = miq::dense_blocks(g);
   GradChoice ch{};
-  int st = grad_validate(x, dy, dw, n, h, wdt, c, r, s, k, p, algo, &g, &ch);
+  st = grad_validate(x, dy, dw, g, bg, nullptr, 0, algo, &ch);
   if (st != MIQ_OK) return st;
   void* ws = nullptr;
   if (filt_elems(g) > 0) {
     st = cached_workspace(ch.ws_bytes, &ws);
     if (st != MIQ_OK) return st;
   }
-  return grad_launch(g, ch, x, dy, dw, ws, stream);
+  return grad_launch(g, bg, ch, x, dy, dw, nullptr, 0, ws, stream);
+}
+
+int miq_block_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
+                            int32_t r, int32_t s, int32_t k, const miq_block_conv2d_params* p, float* dbias,
+                            int32_t bias_mode, int32_t algo, void* stream) {
+  miq::Geom g;
+  miq::BlockGeom bg;
+  int st = infer_block_geom(n, h, wdt, c, r, s, k, p, &g, &bg);
+  if (st != MIQ_OK) return st;
+  GradChoice ch{};
+  st = grad_validate(x, dy, dw, g, bg, dbias, bias_mode, algo, &ch);
+  if (st != MIQ_OK) return st;
+  void* ws = nullptr;
+  st = cached_workspace(ch.ws_bytes, &ws);
+  if (st != MIQ_OK) return st;
+  return grad_launch(g, bg, ch, x, dy, dw, dbias, bias_mode, ws, stream);
 }
 
 int miq_plan_f32(int32_t op, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
                  const miq_conv2d_params* p, int32_t algo, int32_t* kernel) {
   if (kernel == nullptr) return fail(MIQ_ERR_NULL_POINTER, "kernel pointer is NULL");
   miq::Geom g;
-  int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
   if (st != MIQ_OK) return st;
-  static const float kAligned[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  const void* al = static_cast<const void*>(kAligned);
-  std::string why;
-  switch (op) {
-    case 0:  // fprop: the order of miq_fprop_nhwc_f32
-      switch (algo) {
-        case MIQ_ALGO_AUTO:
-          *kernel = miq::f32_igemm_eligible(g, al, al, nullptr) ? (g.Kg <= 32 ? MIQ_F32_IGEMM32 : MIQ_F32_IGEMM)
-                    : miq::f32_depthwise_eligible(g, al, al)     ? MIQ_F32_DEPTHWISE
-                                                                  : MIQ_F32_DIRECT;
-          return MIQ_OK;
-        case MIQ_ALGO_DIRECT: *kernel = MIQ_F32_DIRECT; return MIQ_OK;
-        case MIQ_ALGO_IGEMM:
-          if (!miq::f32_igemm_eligible(g, al, al, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
-          *kernel = g.Kg <= 32 ? MIQ_F32_IGEMM32 : MIQ_F32_IGEMM;
-          return MIQ_OK;
-        default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 convolution algo must be AUTO, DIRECT or IGEMM");
-      }
-    case 1:  // bprop: the order of miq_bprop_nhwc_f32
-      switch (algo) {
-        case MIQ_ALGO_AUTO:
-          *kernel = miq::f32_bprop_igemm_eligible(g, al, al, nullptr) ? MIQ_F32_BPROP_IGEMM : MIQ_F32_DIRECT;
-          return MIQ_OK;
-        case MIQ_ALGO_DIRECT: *kernel = MIQ_F32_DIRECT; return MIQ_OK;
-        case MIQ_ALGO_IGEMM:
-          if (!miq::f32_bprop_igemm_eligible(g, al, al, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
-          *kernel = MIQ_F32_BPROP_IGEMM;
-          return MIQ_OK;
-        default: return fail(MIQ_ERR_INVALID_ARGUMENT, "fp32 bprop algo must be AUTO, DIRECT or IGEMM");
-      }
-    case 2: {  // grad: grad_choose, as miq_grad_nhwc_f32
-      GradChoice ch;
-      st = grad_choose(g, al, al, algo, &ch);
-      if (st != MIQ_OK) return st;
-      *kernel = ch.kind == kGradDepthwise ? MIQ_F32_GRAD_DEPTHWISE : ch.kind == kGradIgemm ? MIQ_F32_GRAD_IGEMM
-                                                                                          : MIQ_F32_DIRECT;
-      return MIQ_OK;
-    }
-    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "op must be 0 (fprop), 1 (bprop) or 2 (grad)");
-  }
+  return plan_f32(op, g, miq::dense_blocks(g), algo, kernel);
+}
+
+int miq_plan_block_f32(int32_t op, int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                       const miq_block_conv2d_params* p, int32_t algo, int32_t* kernel) {
+  if (kernel == nullptr) return fail(MIQ_ERR_NULL_POINTER, "kernel pointer is NULL");
+  miq::Geom g;
+  miq::BlockGeom bg;
+  const int st = infer_block_geom(n, h, wdt, c, r, s, k, p, &g, &bg);
+  if (st != MIQ_OK) return st;
+  return plan_f32(op, g, bg, algo, kernel);
 }
 
 int miq_bmm_i32(const int32_t* A, const int32_t* B, int32_t* C, int32_t batch, int32_t M, int32_t N, int32_t K,

@@ -113,28 +113,42 @@ hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t*
 
 // fp32 NHWC convolution: MFMA implicit GEMM for (C/groups) % 4 == 0 with 16-byte aligned x
 // and w and a non-empty image; the direct kernel (reference CPU loop order) for any shape.
-bool f32_igemm_eligible(const Geom& g, const void* x, const void* w, std::string* why);
-hipError_t launch_f32_igemm(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
-hipError_t launch_f32_direct(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
+// bg: the filter's block grid (dense_blocks(g) for a plain KRSC filter); bias (K * By * Bx
+// floats, bias_mode 0 per block or 1 shared) may be nullptr.
+inline BlockGeom dense_blocks(const Geom& g) { return BlockGeom{1, 1, g.Ho, g.Wo}; }
+bool f32_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, std::string* why);
+hipError_t launch_f32_igemm(const Geom& g, const BlockGeom& bg, const float* x, const float* w, const float* bias,
+                            int bias_mode, float* y, hipStream_t stream);
+hipError_t launch_f32_direct(const Geom& g, const BlockGeom& bg, const float* x, const float* w, const float* bias,
+                             int bias_mode, float* y, hipStream_t stream);
 // fp32 depthwise (C/groups == K/groups == 1, C % 4 == 0, R*S*C <= 8192, 16-byte aligned x and y),
 // four channels per thread in the reference loop's order: bit-exact like the direct kernel.
 bool f32_depthwise_eligible(const Geom& g, const void* x, const void* y);
 hipError_t launch_f32_depthwise(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
 // fp32 dx and dw in the reference CPU loop orders (one thread per output element).
-hipError_t launch_f32_bprop_direct(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
+hipError_t launch_f32_bprop_direct(const Geom& g, const BlockGeom& bg, const float* dy, const float* w, float* dx,
+                                   hipStream_t stream);
 // fp32 dx of a stride-1 convolution on the MFMA implicit GEMM (the forward kernel over dy with
 // the flipped, channel-transposed filter): (K/groups) % 4 == 0, 16-byte aligned dy.
-bool f32_bprop_igemm_eligible(const Geom& g, const void* dy, const void* w, std::string* why);
-hipError_t launch_f32_bprop_igemm(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
-hipError_t launch_f32_grad_direct(const Geom& g, const float* x, const float* dy, float* dw, hipStream_t stream);
+bool f32_bprop_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* dy, const void* w, std::string* why);
+hipError_t launch_f32_bprop_igemm(const Geom& g, const BlockGeom& bg, const float* dy, const float* w, float* dx,
+                                  hipStream_t stream);
+hipError_t launch_f32_grad_direct(const Geom& g, const BlockGeom& bg, const float* x, const float* dy, float* dw,
+                                  hipStream_t stream);
 // fp32 dw on the MFMA (pixel range split over workgroups): any non-empty shape.  ordered: the
 // splits' partial tiles go to `ws` (f32_grad_igemm_workspace bytes, none for one split) and
 // are summed in split order, the same result on every call; otherwise they are added into dw
 // with float atomics after a zero fill (ws unused), whose order varies from run to run.
-bool f32_grad_igemm_eligible(const Geom& g, std::string* why);
-size_t f32_grad_igemm_workspace(const Geom& g);
-hipError_t launch_f32_grad_igemm(const Geom& g, const float* x, const float* dy, float* dw, float* ws,
-                                 bool ordered, hipStream_t stream);
+bool f32_grad_igemm_eligible(const Geom& g, const BlockGeom& bg, std::string* why);
+size_t f32_grad_igemm_workspace(const Geom& g, const BlockGeom& bg);
+hipError_t launch_f32_grad_igemm(const Geom& g, const BlockGeom& bg, const float* x, const float* dy, float* dw,
+                                 float* ws, bool ordered, hipStream_t stream);
+// Bias gradient of the blocked convolution: dbias (K * By * Bx floats, bias_mode 0 per block or
+// 1 shared) = the sum of dy over every output position of each block, in a fixed order, through
+// f32_block_dbias_workspace bytes of `ws` (nonzero for any non-empty dy).
+size_t f32_block_dbias_workspace(const Geom& g, const BlockGeom& bg);
+hipError_t launch_f32_block_dbias(const Geom& g, const BlockGeom& bg, const float* dy, float* dbias, int bias_mode,
+                                  float* ws, hipStream_t stream);
 // fp32 depthwise dw (C/groups == K/groups == 1, C % 4 == 0, R*S <= 16, 16-byte aligned x and dy):
 // pixel runs per thread; ordered: partial sums of every run to `ws`
 // (f32_depthwise_grad_workspace bytes) summed in run order; otherwise float atomics into dw.

@@ -52,6 +52,10 @@ def orc() -> C.CDLL:
         h.orc_conv_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
         h.orc_bprop_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
         h.orc_grad_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _P, _I]
+        h.orc_block_conv_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P, _I, _P, _I]
+        h.orc_block_bprop_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P, _I]
+        h.orc_block_grad_f32.argtypes = [_P, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P, _P, _I, _I]
+        h.orc_block_dbias_f32.argtypes = [_P, _I, _I, _I, _I, _I, _I, _I, _I, _P]
         _orc = h
     return _orc
 
@@ -66,6 +70,7 @@ def ref() -> Optional[C.CDLL]:
                                      _P, _P, _I, C.c_int, C.c_int, _P, _P]
         h.ref_backward_f32.argtypes = [C.c_int, _P, _P] + [C.c_int] * 7 + [_P, _P, _P]
         h.ref_fprop_f32.argtypes = [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int, _P, _P, _P]
+        h.ref_block_f32.argtypes = [C.c_int, _P, _P] + [C.c_int] * 7 + [_P, C.c_int, C.c_int, _P, C.c_int, _P, _P]
         h.ref_verify_tensors.argtypes = [_P, _P, C.c_size_t, C.c_float, C.c_float, _P, _P, _P, _P, _P]
         _ref = h
     return _ref
@@ -233,6 +238,115 @@ def ref_backward_f32(op: str, a, b, x_shape, w_shape, conv) -> Tuple[np.ndarray,
                           C.byref(secs)) != 0:
         raise RuntimeError(h.ref_last_error().decode())
     return out, secs.value
+
+
+# ---- blocked fp32 ------------------------------------------------------------------------
+
+def _bias_mode(mode) -> int:
+    if mode in (0, "per_block", "PerBlock"):
+        return 0
+    if mode in (1, "shared", "Shared"):
+        return 1
+    raise ValueError(f"unknown bias mode {mode!r}")
+
+
+def _block_out_shape(n, h, w, c, r, s, k, conv, by, bx):
+    shp = conv_output_shape(n, h, w, c, r, s, k, _conv7(conv))
+    if shp is None or by <= 0 or bx <= 0 or shp[0] % by or shp[1] % bx:
+        raise ValueError("rejected shape")
+    return shp
+
+
+def block_conv_f32(x: np.ndarray, wt: np.ndarray, conv, bias=None, bias_mode=0, nthreads: int = 0) -> np.ndarray:
+    """Blocked fp32 convolution in the loop order of cpu_block_fprop_nhwc; x NHWC, wt
+    [K, By, Bx, R, S, C/groups], bias K*By*Bx floats or None."""
+    x = np.ascontiguousarray(x, np.float32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    n, h, w, c = x.shape
+    k, by, bx, r, s, _ = wt.shape
+    ho, wo = _block_out_shape(n, h, w, c, r, s, k, conv, by, bx)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32).reshape(-1)
+    if b is not None and b.size != k * by * bx:
+        raise ValueError("bias must hold k*by*bx floats")
+    y = np.empty((n, ho, wo, k), np.float32)
+    if orc().orc_block_conv_f32(_p(x), n, h, w, c, _p(wt), r, s, k, _p(_conv7(conv)), by, bx, _p(b),
+                                _bias_mode(bias_mode), _p(y), nthreads) != 0:
+        raise ValueError("rejected shape")
+    return y
+
+
+def block_bprop_f32(dy: np.ndarray, wt: np.ndarray, x_shape, conv, nthreads: int = 0) -> np.ndarray:
+    """dx (x_shape) of the blocked fp32 convolution in the loop order of cpu_block_bprop_nhwc."""
+    dy = np.ascontiguousarray(dy, np.float32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    n, h, w, c = (int(v) for v in x_shape)
+    k, by, bx, r, s, _ = wt.shape
+    _block_out_shape(n, h, w, c, r, s, k, conv, by, bx)
+    dx = np.empty((n, h, w, c), np.float32)
+    if orc().orc_block_bprop_f32(_p(dy), n, h, w, c, _p(wt), r, s, k, _p(_conv7(conv)), by, bx, _p(dx),
+                                 nthreads) != 0:
+        raise ValueError("rejected shape")
+    return dx
+
+
+def block_grad_f32(x: np.ndarray, dy: np.ndarray, w_shape, conv, with_dbias=False, bias_mode=0,
+                   nthreads: int = 0):
+    """dw ([K, By, Bx, R, S, C/groups]) of the blocked fp32 convolution in the loop order of
+    cpu_block_grad_nhwc; with with_dbias, (dw, dbias) with dbias K*By*Bx floats."""
+    x = np.ascontiguousarray(x, np.float32)
+    dy = np.ascontiguousarray(dy, np.float32)
+    n, h, w, c = x.shape
+    k, by, bx, r, s, cg = (int(v) for v in w_shape)
+    _block_out_shape(n, h, w, c, r, s, k, conv, by, bx)
+    dw = np.empty((k, by, bx, r, s, cg), np.float32)
+    db = np.empty(k * by * bx, np.float32) if with_dbias else None
+    if orc().orc_block_grad_f32(_p(x), n, h, w, c, _p(dy), r, s, k, _p(_conv7(conv)), by, bx, _p(dw), _p(db),
+                                _bias_mode(bias_mode), nthreads) != 0:
+        raise ValueError("rejected shape")
+    return (dw, db) if with_dbias else dw
+
+
+DBIAS_CHUNK = 256  # positions per run of the library's bias-gradient kernels (kDbiasChunk)
+
+
+def block_dbias_f32(dy: np.ndarray, by: int, bx: int, bias_mode=0, chunk: int = DBIAS_CHUNK) -> np.ndarray:
+    """The blocked bias gradient (K*By*Bx floats): dy summed over every position of each block,
+    in runs of `chunk` positions added in order (chunk <= 0: one sequential run), the fixed
+    order of the library's kernels for launch_block_grad_nhwc's all-positions sum."""
+    dy = np.ascontiguousarray(dy, np.float32)
+    n, ho, wo, k = dy.shape
+    out = np.empty(k * by * bx, np.float32)
+    if orc().orc_block_dbias_f32(_p(dy), n, ho, wo, k, by, bx, _bias_mode(bias_mode), chunk, _p(out)) != 0:
+        raise ValueError("rejected shape")
+    return out
+
+
+def ref_block_f32(op: str, a, b, x_shape, w_shape, conv, bias=None, bias_mode=0):
+    """(result, seconds, bias-or-dbias) of the reference's own cpu_block_fprop_nhwc ('fprop':
+    a = x, b = w, bias read), cpu_block_bprop_nhwc ('bprop': a = dy, b = w) or
+    cpu_block_grad_nhwc ('grad': a = x, b = dy, bias = a K*By*Bx float array that receives
+    dbias, or None), compiled in oracle/_ref."""
+    h = ref()
+    if h is None:
+        raise RuntimeError("oracle/_ref/libref_cpu.so was not built")
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    n, hh, w, c = (int(v) for v in x_shape)
+    k, by, bx, r, s, cg = (int(v) for v in w_shape)
+    opi = {"fprop": 0, "bprop": 1, "grad": 2}[op]
+    if opi == 0:
+        ho, wo = _block_out_shape(n, hh, w, c, r, s, k, conv, by, bx)
+        out = np.empty((n, ho, wo, k), np.float32)
+    elif opi == 1:
+        out = np.empty((n, hh, w, c), np.float32)
+    else:
+        out = np.empty((k, by, bx, r, s, cg), np.float32)
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    secs = C.c_double()
+    if h.ref_block_f32(opi, _p(a), _p(b), n, hh, w, c, r, s, k, _p(_conv7(conv)), by, bx, _p(bb),
+                       _bias_mode(bias_mode), _p(out), C.byref(secs)) != 0:
+        raise RuntimeError(h.ref_last_error().decode())
+    return out, secs.value, bb
 
 
 def verify_tensors(ref_v: np.ndarray, got: np.ndarray, abs_eps: float = 1e-4, rel_eps: float = 1e-3) -> bool:

@@ -406,3 +406,231 @@ int orc_grad_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, con
   }
   return 0;
 }
+
+/* ---- blocked fp32 convolution ---------------------------------------------------------- */
+
+/* The blocked shape rules of infer_block_conv_shape (/root/reference/src/conv_types.h:148-169):
+ * by, bx > 0 and the output extent divisible by the block grid; bho x bwo output positions
+ * per block.  Returns 0, or -1 where the reference throws. */
+static int block_shape(int32_t n, int32_t h, int32_t w, int32_t c, int32_t r, int32_t s, int32_t k,
+                       const int32_t conv[7], int32_t by, int32_t bx, int32_t* ho_n, int32_t* wo_n, int32_t* bho,
+                       int32_t* bwo) {
+  if (by <= 0 || bx <= 0) return -1;
+  if (orc_conv_output_shape(n, h, w, c, r, s, k, conv, ho_n, wo_n) != 0) return -1;
+  if (*ho_n % by != 0 || *wo_n % bx != 0) return -1;
+  *bho = *ho_n / by;
+  *bwo = *wo_n / bx;
+  return 0;
+}
+
+/* idx_block_bias (conv_types.h:184-188): mode 0 (PerBlock) indexes [k][by][bx], mode 1
+ * (Shared) the block (0, 0) entry of channel k. */
+static size_t block_bias_index(int32_t kk, int32_t byi, int32_t bxi, int32_t by, int32_t bx, int32_t mode) {
+  const int32_t yi = mode == 0 ? byi : 0, xi = mode == 0 ? bxi : 0;
+  return ((size_t)kk * by + yi) * bx + xi;
+}
+
+/* cpu_block_fprop_nhwc (cpu_ref.cpp:232-270): as cpu_fprop_nhwc, with output position
+ * (ho, wo) in block (ho / bho, wo / bwo) taking its filter from w[k][by][bx][r][s][ci]
+ * ([K, By, Bx, R, S, C/groups]); after the tap sum, acc += bias[block_bias_index] where bias
+ * is given. */
+int orc_block_conv_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r,
+                       int32_t s, int32_t k, const int32_t conv[7], int32_t by, int32_t bx, const float* bias,
+                       int32_t bias_mode, float* y, int32_t nthreads) {
+  int32_t ho_n, wo_n, bho, bwo;
+  if (block_shape(n, h, w, c, r, s, k, conv, by, bx, &ho_n, &wo_n, &bho, &bwo) != 0) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int64_t nrows = (int64_t)n * ho_n;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t row = 0; row < nrows; ++row) {
+    const int32_t ni = (int32_t)(row / ho_n);
+    const int32_t ho = (int32_t)(row % ho_n);
+    const int32_t byi = ho / bho;
+    for (int32_t wo = 0; wo < wo_n; ++wo) {
+      const int32_t bxi = wo / bwo;
+      for (int32_t g = 0; g < g_n; ++g) {
+        for (int32_t ko = 0; ko < kg; ++ko) {
+          const int32_t kk = g * kg + ko;
+          float acc = 0.0f;
+          for (int32_t rr = 0; rr < r; ++rr) {
+            const int32_t hi = ho * sh - ph + rr * dh;
+            if (hi < 0 || hi >= h) continue;
+            for (int32_t ss = 0; ss < s; ++ss) {
+              const int32_t wi = wo * sw - pw + ss * dw;
+              if (wi < 0 || wi >= w) continue;
+              const float* xp = x + (((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg;
+              const float* wp = wt + (((((size_t)kk * by + byi) * bx + bxi) * r + rr) * s + ss) * cg;
+              for (int32_t ci = 0; ci < cg; ++ci) acc += xp[ci] * wp[ci];
+            }
+          }
+          if (bias) acc += bias[block_bias_index(kk, byi, bxi, by, bx, bias_mode)];
+          y[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + kk] = acc;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* cpu_block_bprop_nhwc (cpu_ref.cpp:272-314): as cpu_bprop_nhwc, each tap's output position
+ * (ho, wo) taking the filter of its block. */
+int orc_block_bprop_f32(const float* dy, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r,
+                        int32_t s, int32_t k, const int32_t conv[7], int32_t by, int32_t bx, float* dx,
+                        int32_t nthreads) {
+  int32_t ho_n, wo_n, bho, bwo;
+  if (block_shape(n, h, w, c, r, s, k, conv, by, bx, &ho_n, &wo_n, &bho, &bwo) != 0) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int64_t nrows = (int64_t)n * h;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t row = 0; row < nrows; ++row) {
+    const int32_t ni = (int32_t)(row / h);
+    const int32_t hi = (int32_t)(row % h);
+    for (int32_t wi = 0; wi < w; ++wi) {
+      for (int32_t g = 0; g < g_n; ++g) {
+        for (int32_t ci = 0; ci < cg; ++ci) {
+          float acc = 0.0f;
+          for (int32_t rr = 0; rr < r; ++rr) {
+            const int32_t hn = hi + ph - rr * dh;
+            if (hn < 0 || hn % sh != 0) continue;
+            const int32_t ho = hn / sh;
+            if (ho >= ho_n) continue;
+            const int32_t byi = ho / bho;
+            for (int32_t ss = 0; ss < s; ++ss) {
+              const int32_t wn = wi + pw - ss * dw;
+              if (wn < 0 || wn % sw != 0) continue;
+              const int32_t wo = wn / sw;
+              if (wo >= wo_n) continue;
+              const int32_t bxi = wo / bwo;
+              for (int32_t ko = 0; ko < kg; ++ko) {
+                const int32_t kk = g * kg + ko;
+                const float dyv = dy[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + kk];
+                const float wv = wt[(((((size_t)kk * by + byi) * bx + bxi) * r + rr) * s + ss) * cg + ci];
+                acc += dyv * wv;
+              }
+            }
+          }
+          dx[(((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg + ci] = acc;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* cpu_block_grad_nhwc (cpu_ref.cpp:316-369): dw[k][by][bx][r][s][ci] = sum over n and the
+ * block's output positions (in that order, in-bounds taps) of x * dy.  With dbias, every
+ * element is first zeroed and dbias[block_bias_index(k, by, bx)] accumulates dy over n and
+ * the block's positions, in the reference's loop order (blocks by, bx outermost), counting
+ * only positions whose (r, s) = (0, 0) tap lies inside the image (the reference adds dy inside
+ * that tap's bounds checks). */
+int orc_block_grad_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* dy, int32_t r,
+                       int32_t s, int32_t k, const int32_t conv[7], int32_t by, int32_t bx, float* dwt, float* dbias,
+                       int32_t bias_mode, int32_t nthreads) {
+  int32_t ho_n, wo_n, bho, bwo;
+  if (block_shape(n, h, w, c, r, s, k, conv, by, bx, &ho_n, &wo_n, &bho, &bwo) != 0) return -1;
+  const int32_t ph = conv[0], pw = conv[1], sh = conv[2], sw = conv[3], dh = conv[4], dw = conv[5], g_n = conv[6];
+  const int32_t cg = c / g_n, kg = k / g_n;
+  const int64_t nel = (int64_t)k * by * bx * r * s * cg;
+#ifdef _OPENMP
+  const int nt = nthreads > 0 ? nthreads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 16) num_threads(nt)
+#else
+  (void)nthreads;
+#endif
+  for (int64_t e = 0; e < nel; ++e) {
+    const int32_t ci = (int32_t)(e % cg);
+    const int32_t ss = (int32_t)((e / cg) % s);
+    const int32_t rr = (int32_t)((e / ((int64_t)cg * s)) % r);
+    const int32_t bxi = (int32_t)((e / ((int64_t)cg * s * r)) % bx);
+    const int32_t byi = (int32_t)((e / ((int64_t)cg * s * r * bx)) % by);
+    const int32_t kk = (int32_t)(e / ((int64_t)cg * s * r * bx * by));
+    const int32_t g = kk / kg;
+    float acc = 0.0f;
+    for (int32_t ni = 0; ni < n; ++ni) {
+      for (int32_t lho = 0; lho < bho; ++lho) {
+        const int32_t ho = byi * bho + lho;
+        const int32_t hi = ho * sh - ph + rr * dh;
+        if (hi < 0 || hi >= h) continue;
+        for (int32_t lwo = 0; lwo < bwo; ++lwo) {
+          const int32_t wo = bxi * bwo + lwo;
+          const int32_t wi = wo * sw - pw + ss * dw;
+          if (wi < 0 || wi >= w) continue;
+          acc += x[(((size_t)ni * h + hi) * w + wi) * c + (size_t)g * cg + ci] *
+                 dy[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + kk];
+        }
+      }
+    }
+    dwt[e] = acc;
+  }
+  if (dbias) {
+    const int64_t nb = (int64_t)k * by * bx;
+    for (int64_t i = 0; i < nb; ++i) dbias[i] = 0.0f;
+    for (int32_t kk = 0; kk < k; ++kk) {
+      for (int32_t byi = 0; byi < by; ++byi) {
+        for (int32_t bxi = 0; bxi < bx; ++bxi) {
+          float* slot = dbias + block_bias_index(kk, byi, bxi, by, bx, bias_mode);
+          for (int32_t ni = 0; ni < n; ++ni) {
+            for (int32_t lho = 0; lho < bho; ++lho) {
+              const int32_t ho = byi * bho + lho;
+              const int32_t hi = ho * sh - ph;
+              if (hi < 0 || hi >= h) continue;
+              for (int32_t lwo = 0; lwo < bwo; ++lwo) {
+                const int32_t wo = bxi * bwo + lwo;
+                const int32_t wi = wo * sw - pw;
+                if (wi < 0 || wi >= w) continue;
+                *slot += dy[(((size_t)ni * ho_n + ho) * wo_n + wo) * k + kk];
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* The bias gradient as launch_block_grad_nhwc computes it (cuda_kernels.cu:461-485 and
+ * :1112-1119): dy summed over every output position of a block, which the reference adds with
+ * float atomics in no fixed order.  Restated here in the fixed order of this library's kernels:
+ * a block's positions, in (n, lho, lwo) order, are cut into runs of `chunk` (chunk <= 0: one
+ * run), each run is summed from 0, and a slot then adds its runs in order from 0 - mode 0: slot
+ * [k][by][bx], its own block's runs; mode 1: slot [k][0][0], every block's runs in (by, bx)
+ * order, the other slots 0.  Returns 0, or -1 on a block grid that does not divide ho x wo. */
+int orc_block_dbias_f32(const float* dy, int32_t n, int32_t ho_n, int32_t wo_n, int32_t k, int32_t by, int32_t bx,
+                        int32_t mode, int32_t chunk, float* dbias) {
+  if (by <= 0 || bx <= 0 || ho_n % by != 0 || wo_n % bx != 0) return -1;
+  const int32_t bho = ho_n / by, bwo = wo_n / bx;
+  const int64_t P = (int64_t)n * bho * bwo;
+  const int64_t run = chunk > 0 ? chunk : (P > 0 ? P : 1);
+  for (int64_t i = 0; i < (int64_t)k * by * bx; ++i) dbias[i] = 0.0f;
+  for (int32_t kk = 0; kk < k; ++kk) {
+    for (int32_t byi = 0; byi < by; ++byi) {
+      for (int32_t bxi = 0; bxi < bx; ++bxi) {
+        float* slot = dbias + block_bias_index(kk, byi, bxi, by, bx, mode);
+        for (int64_t p0 = 0; p0 < P; p0 += run) {
+          const int64_t p1 = p0 + run < P ? p0 + run : P;
+          float part = 0.0f;
+          for (int64_t p = p0; p < p1; ++p) {
+            const int64_t ni = p / ((int64_t)bho * bwo);
+            const int32_t lho = (int32_t)((p / bwo) % bho), lwo = (int32_t)(p % bwo);
+            part += dy[(((size_t)ni * ho_n + byi * bho + lho) * wo_n + bxi * bwo + lwo) * k + kk];
+          }
+          *slot += part;
+        }
+      }
+    }
+  }
+  return 0;
+}

@@ -58,6 +58,28 @@ int orc_bprop_f32(const float* dy, int32_t n, int32_t h, int32_t w, int32_t c, c
 int orc_grad_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* dy, int32_t r, int32_t s,
                  int32_t k, const int32_t conv[7], float* dw, int32_t nthreads);
 
+/* Blocked (locally connected) fp32 convolution in the loop orders and rounding of the
+ * reference's cpu_block_fprop_nhwc / cpu_block_bprop_nhwc / cpu_block_grad_nhwc: the output
+ * grid splits into by x bx blocks of (ho/by) x (wo/bx) positions, each with its own filter
+ * w[k][by][bx][r][s][c/groups].  bias / dbias are k*by*bx floats indexed [k][by][bx]
+ * (bias_mode 0) or at [k][0][0] (bias_mode 1); either may be NULL.  0, or -1 on a rejected
+ * shape. */
+int orc_block_conv_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r,
+                       int32_t s, int32_t k, const int32_t conv[7], int32_t by, int32_t bx, const float* bias,
+                       int32_t bias_mode, float* y, int32_t nthreads);
+int orc_block_bprop_f32(const float* dy, int32_t n, int32_t h, int32_t w, int32_t c, const float* wt, int32_t r,
+                        int32_t s, int32_t k, const int32_t conv[7], int32_t by, int32_t bx, float* dx,
+                        int32_t nthreads);
+int orc_block_grad_f32(const float* x, int32_t n, int32_t h, int32_t w, int32_t c, const float* dy, int32_t r,
+                       int32_t s, int32_t k, const int32_t conv[7], int32_t by, int32_t bx, float* dw, float* dbias,
+                       int32_t bias_mode, int32_t nthreads);
+
+/* The blocked bias gradient in the fixed order of this library's kernels: dy (n x ho x wo x k)
+ * summed over every position of a block, in runs of `chunk` positions (<= 0: one run) added in
+ * order; mode 0 per block, mode 1 into [k][0][0].  0, or -1 on a grid that does not divide. */
+int orc_block_dbias_f32(const float* dy, int32_t n, int32_t ho_n, int32_t wo_n, int32_t k, int32_t by, int32_t bx,
+                        int32_t mode, int32_t chunk, float* dbias);
+
 /* int32 batched matrix product with wrap-around arithmetic, the semantics of the
  * reference's bmm_matmul_i32: A[b] M x K (stored K x M when trans_a), B[b] K x N (stored
  * N x K when trans_b), C[b] M x N, batch strides M*K, K*N, M*N. */

@@ -153,6 +153,53 @@ int ref_backward_f32(int op, const float* a, const float* b, int n, int h, int w
   }
 }
 
+// cpu_block_fprop_nhwc (cpu_ref.cpp:232-270, op 0: a = x, b = w, out = y, bias nullable),
+// cpu_block_bprop_nhwc (:272-314, op 1: a = dy, b = w, out = dx) and cpu_block_grad_nhwc
+// (:316-369, op 2: a = x, b = dy, out = dw, `bias` receives dbias when given) on flat arrays;
+// the filter is [k][by][bx][r][s][c/groups], bias / dbias k*by*bx floats, bias_mode 0
+// (PerBlock) or 1 (Shared).
+int ref_block_f32(int op, const float* a, const float* b, int n, int h, int w, int c, int r, int s, int k,
+                  const int32_t conv[7], int by, int bx, float* bias, int bias_mode, float* out, double* seconds) {
+  try {
+    BlockConv2DParams p;
+    p.conv = to_params(conv);
+    p.block_by = by;
+    p.block_bx = bx;
+    const int cg = (p.conv.groups > 0) ? c / p.conv.groups : 0;
+    const BlockBiasMode mode = bias_mode == 0 ? BlockBiasMode::PerBlock : BlockBiasMode::Shared;
+    TensorNHWC xs(n, h, w, c);
+    if (by <= 0 || bx <= 0) throw std::runtime_error("block_by and block_bx must be > 0");
+    BlockFilterKByBxRSC fs(k, by, bx, r, s, cg);
+    const BlockConvShape sh = infer_block_conv_shape(xs, fs, p);
+    const size_t dy_elems = static_cast<size_t>(n) * sh.base.ho * sh.base.wo * k;
+    const auto t1 = std::chrono::steady_clock::now();
+    if (op == 0) {
+      std::memcpy(xs.ptr(), a, xs.elements() * sizeof(float));
+      std::memcpy(fs.ptr(), b, fs.elements() * sizeof(float));
+      TensorNHWC y;
+      cpu_block_fprop_nhwc(xs, fs, p, y, bias, mode);
+      std::memcpy(out, y.ptr(), y.elements() * sizeof(float));
+    } else if (op == 1) {
+      TensorNHWC dy(n, sh.base.ho, sh.base.wo, k);
+      std::memcpy(dy.ptr(), a, dy_elems * sizeof(float));
+      std::memcpy(fs.ptr(), b, fs.elements() * sizeof(float));
+      cpu_block_bprop_nhwc(dy, fs, p, xs);
+      std::memcpy(out, xs.ptr(), xs.elements() * sizeof(float));
+    } else {
+      TensorNHWC dy(n, sh.base.ho, sh.base.wo, k);
+      std::memcpy(xs.ptr(), a, xs.elements() * sizeof(float));
+      std::memcpy(dy.ptr(), b, dy_elems * sizeof(float));
+      cpu_block_grad_nhwc(xs, dy, p, fs, bias, mode);
+      std::memcpy(out, fs.ptr(), fs.elements() * sizeof(float));
+    }
+    if (seconds) *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
 int ref_verify_tensors(const float* ref, const float* got, size_t count, float abs_eps, float rel_eps,
                        float* max_abs, float* max_rel, size_t* abs_idx, size_t* rel_idx, int* passed) {
   try {
