@@ -3,6 +3,7 @@
     python bench.py [--steps K] [--warmup W] [--config r50_3x3] [--cache cold|warm] [--all]
     python bench.py --bmm [--config r50_3x3_im2col]      # the int32 matrix product instead
     python bench.py --fp32 [--config resnet_like_56x56]  # the fp32 convolution (conv_bench suite)
+    python bench.py --fp32 --blocked [--op bprop]        # the blocked fp32 convolution (blocked suite)
     python bench.py --qi32 [--config r50_3x3]            # the reference's float-code API
 
 One step = one fused conv + bias + requantize (+ ReLU) pass of libmiq_qconv over one batch
@@ -63,6 +64,8 @@ def parse():
                     help="measure the fp32 convolution (launch_fprop_nhwc) on the reference's conv_bench suite")
     ap.add_argument("--qi32", action="store_true",
                     help="measure the reference's float-code API (launch_fprop_nhwc_qi32, LinQuantU8) on the workloads")
+    ap.add_argument("--blocked", action="store_true",
+                    help="with --fp32: the blocked convolution (launch_block_*_nhwc) on the reference's blocked suite")
     ap.add_argument("--op", choices=["fprop", "bprop", "grad"], default="fprop",
                     help="with --fp32: the pass to time (launch_fprop_nhwc / launch_bprop_nhwc / launch_grad_nhwc)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -242,13 +245,25 @@ FP32_SUITE = [
     ("dilated_3x3", 16, 64, 64, 64, 64, 3, 3, (2, 2, 1, 1, 2, 2, 1)),
     ("small_batch", 1, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1)),
 ]
+# The reference's blocked bench suite (src/main.cpp:176-186): the same fields, then the block grid.
+BLOCKED_SUITE = [
+    ("blocked_resnet_56x56_b2x2", 32, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), 2, 2),
+    ("blocked_resnet_56x56_b4x4", 32, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), 4, 4),
+    ("blocked_resnet_28x28_b2x4", 32, 28, 28, 128, 256, 3, 3, (1, 1, 1, 1, 1, 1, 1), 2, 4),
+    ("blocked_grouped_g4_b2x2", 32, 56, 56, 128, 128, 3, 3, (1, 1, 1, 1, 1, 1, 4), 2, 2),
+    ("blocked_pointwise_1x1_b4x4", 32, 56, 56, 128, 256, 1, 1, (0, 0, 1, 1, 1, 1, 1), 4, 4),
+    ("blocked_dilated_3x3_b2x2", 16, 64, 64, 64, 64, 3, 3, (2, 2, 1, 1, 2, 2, 1), 2, 2),
+    ("blocked_small_batch_b4x4", 1, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), 4, 4),
+]
 PEAK_FP32_TFLOPS = 157.3  # dense fp32 MFMA, MI355X
 
 
 def bench_fp32(args) -> None:
-    """Times launch_fprop_nhwc on the conv_bench suite (HIP events over back-to-back launches),
-    checks image 0 of every shape against the oracle with the reference's verify rule, prints
-    a table on stderr and one JSON line for the first shape."""
+    """Times launch_fprop_nhwc / launch_bprop_nhwc / launch_grad_nhwc on the conv_bench suite, or
+    with --blocked launch_block_{fprop,bprop,grad}_nhwc on the blocked suite (HIP events over
+    back-to-back launches); checks image 0 of every shape against the oracle (fprop, bprop) or
+    all images against the bit-exact direct kernel (grad) with the reference's verify rule,
+    prints a table on stderr and one JSON line for the first shape."""
     import numpy as np
     import torch
 
@@ -256,49 +271,83 @@ def bench_fp32(args) -> None:
     import oracle  # checker of the sampled image and the cpu_baseline leg only
 
     dev = torch.device("cuda:0")
+    suite = BLOCKED_SUITE if args.blocked else FP32_SUITE
     rows = []
-    for name, n, h, w, c, k, r, s_, conv in FP32_SUITE:
+    for case in suite:
+        name, n, h, w, c, k, r, s_, conv = case[:9]
+        by, bx = case[9:] if args.blocked else (1, 1)
         if args.config not in (None, name):
             continue
         ph, pw, sh, sw, dh, dw, g = conv
+        bp = M.BlockConv2DParams(M.Conv2DParams(*conv), by, bx)
+        ho, wo = M.infer_conv_shape(n, h, w, c, r, s_, k, M.Conv2DParams(*conv))
         gen = torch.Generator(device=dev)
         gen.manual_seed(42)
         x = torch.rand((n, h, w, c), device=dev, generator=gen) * 2 - 1
-        wt = torch.rand((k, r, s_, c // g), device=dev, generator=gen) * 2 - 1
-        kw = dict(stride=(sh, sw), padding=(ph, pw), dilation=(dh, dw), groups=g)
-        y = M.conv2d_nhwc_f32(x, wt, **kw)
-        torch.cuda.synchronize()
-        ho, wo = y.shape[1], y.shape[2]
+        wshape = (k, by, bx, r, s_, c // g) if args.blocked else (k, r, s_, c // g)
+        wt = torch.rand(wshape, device=dev, generator=gen) * 2 - 1
+        y = torch.empty((n, ho, wo, k), device=dev)
         stream = torch.cuda.current_stream()
+
+        def fprop(out, algo="auto"):
+            if args.blocked:
+                M.launch_block_fprop_nhwc(x, wt, out, n, h, w, c, r, s_, k, bp, algo=algo, stream=stream)
+            else:
+                M.launch_fprop_nhwc(x, wt, out, n, h, w, c, r, s_, k, conv, algo=algo, stream=stream)
+
+        def bprop(dy, out, algo="auto"):
+            if args.blocked:
+                M.launch_block_bprop_nhwc(dy, wt, out, n, h, w, c, r, s_, k, bp, algo=algo, stream=stream)
+            else:
+                M.launch_bprop_nhwc(dy, wt, out, n, h, w, c, r, s_, k, conv, algo=algo, stream=stream)
+
+        def grad(dy, out, algo="auto"):
+            if args.blocked:
+                M.launch_block_grad_nhwc(x, dy, out, n, h, w, c, r, s_, k, bp, algo=algo, stream=stream)
+            else:
+                M.launch_grad_nhwc(x, dy, out, n, h, w, c, r, s_, k, conv, algo=algo, stream=stream)
+
         if args.op == "fprop":
-            want = oracle.conv_f32(x[:1].cpu().numpy(), wt.cpu().numpy(), conv)
+            fprop(y)
+            torch.cuda.synchronize()
+            x1, w1 = x[:1].cpu().numpy(), wt.cpu().numpy()
+            want = oracle.block_conv_f32(x1, w1, conv) if args.blocked else oracle.conv_f32(x1, w1, conv)
             ok = oracle.verify_tensors(want, y[:1].cpu().numpy(), 1e-4, 1e-3)
 
             def step():
-                M.conv2d_nhwc_f32(x, wt, out=y, stream=stream, **kw)
+                fprop(y)
         elif args.op == "bprop":
             dy = torch.rand(y.shape, device=dev, generator=gen) * 2 - 1
             dx = torch.empty_like(x)
-            M.launch_bprop_nhwc(dy, wt, dx, n, h, w, c, r, s_, k, conv, stream=stream)
+            bprop(dy, dx)
             torch.cuda.synchronize()
-            want = oracle.bprop_f32(dy[:1].cpu().numpy(), wt.cpu().numpy(), (1, h, w, c), conv)
+            dy1, w1 = dy[:1].cpu().numpy(), wt.cpu().numpy()
+            want = (oracle.block_bprop_f32(dy1, w1, (1, h, w, c), conv) if args.blocked
+                    else oracle.bprop_f32(dy1, w1, (1, h, w, c), conv))
             ok = oracle.verify_tensors(want, dx[:1].cpu().numpy(), 1e-4, 1e-3)
 
             def step():
-                M.launch_bprop_nhwc(dy, wt, dx, n, h, w, c, r, s_, k, conv, stream=stream)
+                bprop(dy, dx)
         else:
             dy = torch.rand(y.shape, device=dev, generator=gen) * 2 - 1
             dw = torch.empty_like(wt)
-            # the timed problem itself (all n images) checked against the direct kernel, which
-            # is bit-exact with cpu_grad_nhwc, under the reference's verify rule
-            M.launch_grad_nhwc(x, dy, dw, n, h, w, c, r, s_, k, conv, stream=stream)
-            dw_ref = torch.empty_like(wt)
-            M.launch_grad_nhwc(x, dy, dw_ref, n, h, w, c, r, s_, k, conv, algo="direct", stream=stream)
+            # checked on the image-0 problem against the oracle (the reference loop's order) under
+            # the reference's verify rule; at the full batch the reference's own sequential fp32
+            # sum over N*Ho*Wo terms drifts past that rule, so it cannot be the yardstick there
+            x0, dy0, dw0 = x[:1].contiguous(), dy[:1].contiguous(), torch.empty_like(wt)
+            if args.blocked:
+                M.launch_block_grad_nhwc(x0, dy0, dw0, 1, h, w, c, r, s_, k, bp, stream=stream)
+            else:
+                M.launch_grad_nhwc(x0, dy0, dw0, 1, h, w, c, r, s_, k, conv, stream=stream)
+            grad(dy, dw)
             torch.cuda.synchronize()
-            ok = oracle.verify_tensors(dw_ref.cpu().numpy(), dw.cpu().numpy(), 1e-4, 1e-3)
+            x1, dy1 = x0.cpu().numpy(), dy0.cpu().numpy()
+            want = (oracle.block_grad_f32(x1, dy1, wshape, conv) if args.blocked
+                    else oracle.grad_f32(x1, dy1, wshape, conv))
+            ok = oracle.verify_tensors(want, dw0.cpu().numpy(), 1e-4, 1e-3)
 
             def step():
-                M.launch_grad_nhwc(x, dy, dw, n, h, w, c, r, s_, k, conv, stream=stream)
+                grad(dy, dw)
         for _ in range(args.warmup):
             step()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -318,51 +367,63 @@ def bench_fp32(args) -> None:
         tf = flops / (ms * 1e-3) / 1e12
         gbs = nbytes / (ms * 1e-3) / 1e9
         frac = tf / PEAK_FP32_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
-        algo = M.plan_f32(args.op, n, h, w, c, r, s_, k, M.Conv2DParams(*conv))  # what the library dispatches
-        rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, kernel=algo,
+        # what the library dispatches
+        algo = (M.plan_block_f32(args.op, n, h, w, c, r, s_, k, bp) if args.blocked
+                else M.plan_f32(args.op, n, h, w, c, r, s_, k, M.Conv2DParams(*conv)))
+        rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, by=by, bx=bx, kernel=algo,
                          us=round(ms * 1e3, 2), tflops=round(tf, 3), gbs=round(gbs, 1), bound=bound,
-                         frac=round(frac, 4), verified=ok,
-                         verified_on="all images vs the direct kernel" if args.op == "grad" else "image 0 vs the oracle"))
+                         frac=round(frac, 4), verified=ok, verified_on="the image-0 problem vs the oracle"))
         del x, wt, y
         torch.cuda.empty_cache()
     if not rows:
-        print(f"bench.py: unknown --fp32 shape {args.config}; known: {[c[0] for c in FP32_SUITE]}", file=sys.stderr)
+        print(f"bench.py: unknown --fp32 shape {args.config}; known: {[c[0] for c in suite]}", file=sys.stderr)
         sys.exit(2)
-    print(f"{'shape':20s} {'kernel':7s} {'us':>10s} {'TFLOP/s':>8s} {'GB/s':>8s} {'bound':5s} {'frac':>6s} verified",
+    print(f"{'shape':28s} {'kernel':11s} {'us':>10s} {'TFLOP/s':>8s} {'GB/s':>8s} {'bound':5s} {'frac':>6s} verified",
           file=sys.stderr)
     for r in rows:
-        print(f"{r['name']:20s} {r['kernel']:7s} {r['us']:10.2f} {r['tflops']:8.2f} {r['gbs']:8.1f} {r['bound']:5s} "
+        print(f"{r['name']:28s} {r['kernel']:11s} {r['us']:10.2f} {r['tflops']:8.2f} {r['gbs']:8.1f} {r['bound']:5s} "
               f"{r['frac']:6.3f} {r['verified']}", file=sys.stderr)
     head = rows[0]
+    suite_name = ("blocked bench suite (src/main.cpp:176-186)" if args.blocked
+                  else "conv_bench default suite (src/main.cpp:163-174)")
     line = {
-        "metric": f"fp32 conv {args.op} TFLOP/s, conv_bench default suite (src/main.cpp:163-174)",
+        "metric": f"fp32 {'blocked ' if args.blocked else ''}conv {args.op} TFLOP/s, {suite_name}",
         "value": head["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(head["us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": head["name"], "N": head["n"], "H": head["h"], "W": head["w"], "C": head["c"],
-                   "K": head["k"], "R": head["r"], "S": head["s"], "groups": head["groups"], "kernel": head["kernel"],
-                   "timing": "eager back-to-back", "cache": "warm"},
+                   "K": head["k"], "R": head["r"], "S": head["s"], "groups": head["groups"], "by": head["by"],
+                   "bx": head["bx"], "kernel": head["kernel"], "timing": "eager back-to-back", "cache": "warm"},
         "roofline": {"bound": head["bound"], "achieved": head["tflops"] if head["bound"] == "mfma" else head["gbs"],
                      "peak": PEAK_FP32_TFLOPS if head["bound"] == "mfma" else PEAK_HBM_GBS,
                      "unit": "TFLOP/s" if head["bound"] == "mfma" else "GB/s", "frac": head["frac"], "traffic": None},
         "shapes": rows,
     }
-    if not args.no_cpu_baseline and head["name"] == FP32_SUITE[0][0] and args.op == "fprop":
-        _, n, h, w, c, k, r, s_, conv = FP32_SUITE[0]
+    if not args.no_cpu_baseline and head["name"] == suite[0][0] and args.op == "fprop":
+        _, n, h, w, c, k, r, s_, conv = suite[0][:9]
+        by, bx = suite[0][9:] if args.blocked else (1, 1)
         rng = np.random.default_rng(3)
         x1 = rng.uniform(-1, 1, size=(1, h, w, c)).astype(np.float32)
-        w1 = rng.uniform(-1, 1, size=(k, r, s_, c // conv[6])).astype(np.float32)
+        if args.blocked:
+            w1 = rng.uniform(-1, 1, size=(k, by, bx, r, s_, c // conv[6])).astype(np.float32)
+        else:
+            w1 = rng.uniform(-1, 1, size=(k, r, s_, c // conv[6])).astype(np.float32)
+        fn = "cpu_block_fprop_nhwc" if args.blocked else "cpu_fprop_nhwc"
         if oracle.ref() is not None:
-            y1, secs = oracle.ref_conv_f32(x1, w1, conv)
-            kind, what = "reference", "cpu_fprop_nhwc of /root/reference/src/cpu_ref.cpp (g++ -O3)"
+            if args.blocked:
+                y1, secs, _ = oracle.ref_block_f32("fprop", x1, w1, x1.shape, w1.shape, conv)
+            else:
+                y1, secs = oracle.ref_conv_f32(x1, w1, conv)
+            kind, what = "reference", f"{fn} of /root/reference/src/cpu_ref.cpp (g++ -O3)"
         else:
             t0 = time.perf_counter()
-            y1 = oracle.conv_f32(x1, w1, conv, nthreads=1)
+            y1 = (oracle.block_conv_f32(x1, w1, conv, nthreads=1) if args.blocked
+                  else oracle.conv_f32(x1, w1, conv, nthreads=1))
             secs = time.perf_counter() - t0
-            kind, what = "port", "oracle/qconv_oracle.c orc_conv_f32 (gcc -O3)"
+            kind, what = "port", "oracle/qconv_oracle.c " + ("orc_block_conv_f32" if args.blocked else "orc_conv_f32")
         flops1 = 2.0 * y1.shape[1] * y1.shape[2] * k * r * s_ * (c // conv[6])
         line["cpu_baseline"] = {"value": round(flops1 / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
-                                "sample": f"1 of the {n} images of {FP32_SUITE[0][0]} ({flops1 / 1e9:.2f} GFLOP) in "
+                                "sample": f"1 of the {n} images of {suite[0][0]} ({flops1 / 1e9:.2f} GFLOP) in "
                                           f"{secs:.2f} s; {what}, 1 thread on {cpu_model()}"}
     print(json.dumps(line), flush=True)
 

@@ -67,8 +67,11 @@ struct F32Args {
   // the filter of its block.
   int By, Bx, bho, bwo;
   int bias_mode;  // 0: bias[k][by][bx]; 1: bias[k][0][0] for every block
+  int nfast;      // region pixels in (row, column, image) order instead of (image, row, column)
   FastDivM fd_tn, fd_tiles, fd_regions, fd_rx;
 };
+
+enum F32Mode : int { kFwd = 0, kTrans = 1, kTransBlocked = 2 };
 
 __device__ __forceinline__ int f32_slot(int row, int g) { return 4 * row + (g ^ (((row >> 3) & 1) << 1)); }
 
@@ -86,19 +89,38 @@ struct TapCursor {
       }
     }
   }
+  // the same over taps whose s lies in s0..s1
+  __device__ __forceinline__ void advance_in(int Cg, int s0, int s1) {
+    ci += kF32KC;
+    while (ci >= Cg) {
+      ci -= Cg;
+      if (++s > s1) {
+        s = s0;
+        ++r;
+      }
+    }
+  }
 };
 
-// TRANSPOSED: the filter operand is read as the bprop filter of a stride-1 convolution:
+// floor(a / d) and ceil(a / d) for d > 0 and any sign of a
+__device__ __forceinline__ int floor_div(int a, int d) { return a >= 0 ? a / d : -((-a + d - 1) / d); }
+__device__ __forceinline__ int ceil_div(int a, int d) { return -floor_div(-a, d); }
+
+// MODE kFwd: the forward convolution (a blocked filter: one block per region).
+// MODE kTrans / kTransBlocked (TRANSPOSED): the filter operand is read as the bprop filter of a
+// stride-1 convolution:
 // row j (an input channel of the original) and reduction index (r', s', ko) address
 // w[g Kg + ko][by][bx][R-1-r'][S-1-s'][j] of the original filter (`ow_*` extents in F32Args),
-// (by, bx) the block of the input position the tap reads.  A workgroup runs its reduction
-// once per filter block that its pixels' taps can reach (one for a plain filter, and one for a
-// pixel tile inside a block's reach), reading only the input positions of that block each time.
+// (by, bx) the block of the input position the tap reads.  kTrans: a plain filter (one block).
+// kTransBlocked: a workgroup runs its reduction once per filter block that its pixels' taps can
+// reach, over the taps that reach it, reading only the input positions of that block each time.
 // BN: channels per workgroup, 64 (128 pixels, waves 4 x 2) or 32 for groups of at most 32
 // output channels (256 pixels, waves 8 x 1; each thread stages two pixel rows, and the waves
 // of threads 256.. load filter rows again without staging them).
-template <bool TRANSPOSED, int BN>
+template <int MODE, int BN>
 __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a) {
+  constexpr bool TRANSPOSED = MODE != kFwd;
+  constexpr bool MULTI = MODE == kTransBlocked;  // several filter blocks per tile
   constexpr int BM = BN == 64 ? 128 : 256;
   constexpr int NA = BM / 128;  // pixel rows per thread
   __shared__ v4f sA[2][BM * 4];
@@ -127,6 +149,22 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const int n0 = tni * BN;
   if (m0 >= Mr) return;  // whole workgroup, before any barrier: a tile past a clipped region
 
+  // Region pixel m -> (image, row, column): batch-slowest, or with a.nfast batch-fastest, so that
+  // a tile spans few positions and (transposed, blocked filter) reaches few filter blocks.
+  auto decode = [&](int m, int& pn, int& lr, int& lc) {
+    if (MULTI && a.nfast) {
+      const int pos = m / g.N;
+      pn = m - pos * g.N;
+      lr = pos / cols;
+      lc = pos - lr * cols;
+    } else {
+      pn = m / rc;
+      const int prem = m - pn * rc;
+      lr = prem / cols;
+      lc = prem - lr * cols;
+    }
+  };
+
   // A: pixel rows ar + 128 i, reduction values 4 aq .. 4 aq + 3 of each chunk
   const int ar = t >> 2;
   const int aq = t & 3;
@@ -134,11 +172,8 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const float* xn[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int pix = min(m0 + ar + 128 * i, Mr - 1);
-    const int pn = pix / rc;
-    const int prem = pix - pn * rc;
-    const int lr = prem / cols;
-    const int lc = prem - lr * cols;
+    int pn, lr, lc;
+    decode(min(m0 + ar + 128 * i, Mr - 1), pn, lr, lc);
     hbase[i] = (row0 + lr) * g.sh - g.ph;
     wbase[i] = (col0 + lc) * g.sw - g.pw;
     xn[i] = a.x + static_cast<size_t>(pn) * g.H * g.W * g.C + static_cast<size_t>(grp) * g.Cg;
@@ -151,7 +186,6 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     cur.r = tap / g.S;
     cur.s = tap - cur.r * g.S;
   }
-  const TapCursor cur0 = cur;
   int cur_chunk = 0;
   // B: filter row br (channel of the group), reduction values 2 bp, 2 bp + 1 of each chunk
   const int br = (t >> 3) & (BN - 1);
@@ -166,38 +200,52 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   const size_t blk_stride = static_cast<size_t>(a.ow_taps) * a.ow_cg;  // between filter blocks
   const size_t ko_stride = blk_stride * nblk;                          // between original channels
   const float* wt0 = a.w + static_cast<size_t>(grp) * g.Cg * ko_stride + bj;  // (ko = 0, block 0, r = s = 0)
-  TapCursor bcur;
-  if constexpr (TRANSPOSED) {
+  TapCursor bcur{0, 0, 0};
+  if constexpr (MODE == kTrans) {
     const int k = 2 * bp;
     const int tap = k / g.Cg;
     bcur.ci = k - tap * g.Cg;
     bcur.r = tap / g.S;
     bcur.s = tap - bcur.r * g.S;
   }
-  const TapCursor bcur0 = bcur;
 
-  // The filter blocks this tile's taps can reach (inclusive rectangle qy0..qy1 x qx0..qx1),
-  // from the tile's range of output rows and columns; a plain filter has the one block 0.
-  // Input rows read by output row y: y sh - ph + r dh, r < R (likewise columns).
+  // Transposed: the filter blocks this tile's taps can reach (inclusive rectangle qy0..qy1 x
+  // qx0..qx1), from the tile's range of output rows t_hlo..t_hhi and columns t_wlo..t_whi; a
+  // plain filter has the one block 0.  Input rows read by output row y: y sh - ph + r dh.
   int qy0 = 0, qy1 = 0, qx0 = 0, qx1 = 0;
   int nrect = 1;
-  if constexpr (TRANSPOSED) {
+  int t_hlo = 0, t_hhi = 0, t_wlo = 0, t_whi = 0;
+  if constexpr (MULTI) {
     const int p1 = min(m0 + BM, Mr) - 1;
-    const int pn0 = m0 / rc, pn1 = p1 / rc;
-    const int lr0 = (m0 - pn0 * rc) / cols, lr1 = (p1 - pn1 * rc) / cols;
     int rlo = 0, rhi = rows - 1, clo = 0, chi = cols - 1;
-    if (pn0 == pn1) {
-      rlo = lr0;
-      rhi = lr1;
-      if (lr0 == lr1) {
-        clo = m0 - pn0 * rc - lr0 * cols;
-        chi = p1 - pn1 * rc - lr1 * cols;
+    if (a.nfast) {
+      const int pos0 = m0 / g.N, pos1 = p1 / g.N;
+      rlo = pos0 / cols;
+      rhi = pos1 / cols;
+      if (rlo == rhi) {
+        clo = pos0 - rlo * cols;
+        chi = pos1 - rhi * cols;
+      }
+    } else {
+      const int pn0 = m0 / rc, pn1 = p1 / rc;
+      const int lr0 = (m0 - pn0 * rc) / cols, lr1 = (p1 - pn1 * rc) / cols;
+      if (pn0 == pn1) {
+        rlo = lr0;
+        rhi = lr1;
+        if (lr0 == lr1) {
+          clo = m0 - pn0 * rc - lr0 * cols;
+          chi = p1 - pn1 * rc - lr1 * cols;
+        }
       }
     }
-    const int ylo = max((row0 + rlo) * g.sh - g.ph, 0);
-    const int yhi = min((row0 + rhi) * g.sh - g.ph + (g.R - 1) * g.dh, g.H - 1);
-    const int xlo = max((col0 + clo) * g.sw - g.pw, 0);
-    const int xhi = min((col0 + chi) * g.sw - g.pw + (g.S - 1) * g.dw, g.W - 1);
+    t_hlo = row0 + rlo;
+    t_hhi = row0 + rhi;
+    t_wlo = col0 + clo;
+    t_whi = col0 + chi;
+    const int ylo = max(t_hlo * g.sh - g.ph + min(0, (g.R - 1) * g.dh), 0);
+    const int yhi = min(t_hhi * g.sh - g.ph + max(0, (g.R - 1) * g.dh), g.H - 1);
+    const int xlo = max(t_wlo * g.sw - g.pw + min(0, (g.S - 1) * g.dw), 0);
+    const int xhi = min(t_whi * g.sw - g.pw + max(0, (g.S - 1) * g.dw), g.W - 1);
     if (ylo <= yhi && xlo <= xhi) {
       qy0 = ylo / a.bho;
       qy1 = yhi / a.bho;
@@ -208,9 +256,37 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
       nrect = 0;  // no tap reads the input: the tile is zero
     }
   }
-  // current block of the reduction and the input positions it covers
+  // The taps r0..r1 x s0..s1 that read block (by_, bx_) for some pixel of the tile, and the
+  // chunks of that block's reduction (r, s, ko): taps outside read nothing of the block.
+  // Non-positive dilation keeps every tap.
+  auto block_red = [&](int by_, int bx_, int& r0, int& r1, int& s0, int& s1) -> int {
+    const int y0 = by_ * a.bho, y1 = min(y0 + a.bho, g.H) - 1;
+    const int x0 = bx_ * a.bwo, x1 = min(x0 + a.bwo, g.W) - 1;
+    r0 = 0; r1 = g.R - 1; s0 = 0; s1 = g.S - 1;
+    if (g.dh > 0) {
+      r0 = max(r0, ceil_div(y0 - t_hhi * g.sh + g.ph, g.dh));
+      r1 = min(r1, floor_div(y1 - t_hlo * g.sh + g.ph, g.dh));
+    }
+    if (g.dw > 0) {
+      s0 = max(s0, ceil_div(x0 - t_whi * g.sw + g.pw, g.dw));
+      s1 = min(s1, floor_div(x1 - t_wlo * g.sw + g.pw, g.dw));
+    }
+    if (r0 > r1 || s0 > s1) return 0;
+    return ((r1 - r0 + 1) * (s1 - s0 + 1) * g.Cg + kF32KC - 1) / kF32KC;
+  };
+  int nch = a.nchunks;  // chunks of the whole reduction (one block, every tap)
+  if constexpr (MULTI) {
+    nch = 0;
+    for (int y = qy0; y < qy0 + (nrect > 0 ? qy1 - qy0 + 1 : 0); ++y)
+      for (int x = qx0; x <= qx1; ++x) {
+        int r0, r1, s0, s1;
+        nch += block_red(y, x, r0, r1, s0, s1);
+      }
+  }
+  // current block of the reduction, the input positions it covers and its taps
   int qy = qy0, qx = qx0, cib = 0;
   int ylo_b = 0, yhi_b = g.H, xlo_b = 0, xhi_b = g.W;
+  int nch_b = a.nchunks, kd_b = a.kdim, r0b = 0, r1b = g.R - 1, s0b = 0, s1b = g.S - 1;
   const float* wtb = wt0;
   auto set_block = [&]() {
     ylo_b = qy * a.bho;
@@ -218,28 +294,54 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     xlo_b = qx * a.bwo;
     xhi_b = min(xlo_b + a.bwo, g.W);
     wtb = wt0 + static_cast<size_t>(qy * a.Bx + qx) * blk_stride;
+    nch_b = block_red(qy, qx, r0b, r1b, s0b, s1b);
+    kd_b = nch_b > 0 ? (r1b - r0b + 1) * (s1b - s0b + 1) * g.Cg : 0;
   };
-  if constexpr (TRANSPOSED) set_block();
+  auto start_block = [&]() {  // both cursors at the block's first chunk
+    const int ns = s1b - s0b + 1;
+    int tap = (4 * aq) / g.Cg;
+    cur.ci = 4 * aq - tap * g.Cg;
+    cur.r = r0b + tap / ns;
+    cur.s = s0b + tap % ns;
+    tap = (2 * bp) / g.Cg;
+    bcur.ci = 2 * bp - tap * g.Cg;
+    bcur.r = r0b + tap / ns;
+    bcur.s = s0b + tap % ns;
+  };
+  auto next_block = [&]() {  // the next block of the rectangle with taps to run
+    while (qy <= qy1) {
+      if (++qx > qx1) {
+        qx = qx0;
+        ++qy;
+      }
+      if (qy > qy1) break;  // not reached: the chunk count covers the live blocks only
+      set_block();
+      if (nch_b > 0) break;
+    }
+    start_block();
+  };
+  if constexpr (MULTI) {
+    if (nch > 0) {
+      set_block();
+      if (nch_b == 0) next_block();
+      else start_block();
+    }
+  }
 
   auto load = [&](int c, v4f (&va)[NA], v2f& vb, unsigned& oka, bool& okb) {
     if (cur_chunk < c) {  // chunks are loaded in order; a repeat of the last one does not advance
       ++cur_chunk;
-      if constexpr (TRANSPOSED) {
-        if (++cib == a.nchunks) {  // next block of the tile's rectangle
+      if constexpr (MULTI) {
+        if (++cib == nch_b) {  // next block of the tile's rectangle
           cib = 0;
-          cur = cur0;
-          bcur = bcur0;
-          if (++qx > qx1) {
-            qx = qx0;
-            ++qy;
-          }
-          set_block();
+          next_block();
         } else {
-          cur.advance(g.Cg, g.S);
-          bcur.advance(g.Cg, g.S);
+          cur.advance_in(g.Cg, s0b, s1b);
+          bcur.advance_in(g.Cg, s0b, s1b);
         }
       } else {
         cur.advance(g.Cg, g.S);
+        if constexpr (TRANSPOSED) bcur.advance(g.Cg, g.S);
         cib = cur_chunk;
       }
     }
@@ -248,13 +350,13 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     for (int i = 0; i < NA; ++i) {
       const int hi = hbase[i] + cur.r * g.dh;
       const int wi = wbase[i] + cur.s * g.dw;
-      const bool ok = cur.r < g.R && hi >= ylo_b && hi < yhi_b && wi >= xlo_b && wi < xhi_b;
+      const bool ok = cur.r <= r1b && hi >= ylo_b && hi < yhi_b && wi >= xlo_b && wi < xhi_b;
       oka |= static_cast<unsigned>(ok) << i;
       const size_t xo = ok ? (static_cast<size_t>(hi) * g.W + wi) * g.C + cur.ci : 0;
       va[i] = *reinterpret_cast<const v4f*>(xn[i] + xo);
     }
     const int kb = cib * kF32KC + 2 * bp;
-    okb = kb < a.kdim;
+    okb = kb < kd_b;
     if constexpr (TRANSPOSED) {
       // original filter w[ko][by][bx][R-1-r'][S-1-s'][bj], ko = bcur.ci (+1)
       const size_t tap = static_cast<size_t>(g.R - 1 - bcur.r) * g.S + (g.S - 1 - bcur.s);
@@ -284,7 +386,6 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
     for (int im = 0; im < 2; ++im) acc[jn][im] = v4f{0.f, 0.f, 0.f, 0.f};
 
   constexpr int P = kF32Depth;
-  const int nch = nrect * a.nchunks;
   if (nch > 0) {
     const int last = nch - 1;
     v4f va[P][NA];
@@ -329,10 +430,8 @@ __global__ void __launch_bounds__(64 * kF32Waves, 1) f32_igemm_kernel(F32Args a)
   for (int im = 0; im < 2; ++im) {
     const int m = m0 + 32 * wm + 16 * im + (lane & 15);
     if (m >= Mr) continue;
-    const int pn = m / rc;
-    const int prem = m - pn * rc;
-    const int lr = prem / cols;
-    const int lc = prem - lr * cols;
+    int pn, lr, lc;
+    decode(m, pn, lr, lc);
     const size_t pix = (static_cast<size_t>(pn) * g.Ho + row0 + lr) * g.Wo + col0 + lc;
 #pragma unroll
     for (int jn = 0; jn < 2; ++jn) {
@@ -1100,6 +1199,7 @@ hipError_t f32_igemm_launch(const Geom& g, const BlockGeom& bg, const Regions& r
   a.ry = rg.ry; a.rx = rg.rx; a.rh = rg.rh; a.rw = rg.rw;
   a.By = bg.By; a.Bx = bg.Bx; a.bho = bg.bho; a.bwo = bg.bwo;
   a.bias_mode = bias_mode;
+  a.nfast = transposed && bg.By * bg.Bx > 1 ? 1 : 0;
   a.M = g.N * rg.rh * rg.rw;
   a.kdim = g.R * g.S * g.Cg;
   a.nchunks = (a.kdim + kF32KC - 1) / kF32KC;
@@ -1114,12 +1214,15 @@ hipError_t f32_igemm_launch(const Geom& g, const BlockGeom& bg, const Regions& r
   const unsigned blocks = static_cast<unsigned>(a.tiles) * static_cast<unsigned>(g.G) *
                           static_cast<unsigned>(rg.ry * rg.rx);
   const dim3 grid(blocks), block(64 * kF32Waves);
-  if (transposed) {
-    if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<true, 32>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((f32_igemm_kernel<true, 64>), grid, block, 0, stream, a);
+  if (transposed && a.By * a.Bx > 1) {
+    if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<kTransBlocked, 32>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((f32_igemm_kernel<kTransBlocked, 64>), grid, block, 0, stream, a);
+  } else if (transposed) {
+    if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<kTrans, 32>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((f32_igemm_kernel<kTrans, 64>), grid, block, 0, stream, a);
   } else {
-    if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<false, 32>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((f32_igemm_kernel<false, 64>), grid, block, 0, stream, a);
+    if (narrow) hipLaunchKernelGGL((f32_igemm_kernel<kFwd, 32>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((f32_igemm_kernel<kFwd, 64>), grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }
