@@ -301,11 +301,12 @@ def bench_fp32(args) -> None:
             else:
                 M.launch_bprop_nhwc(dy, wt, out, n, h, w, c, r, s_, k, conv, algo=algo, stream=stream)
 
-        def grad(dy, out, algo="auto"):
+        def grad(dy, out, algo="auto", xin=None):
+            xin = x if xin is None else xin
             if args.blocked:
-                M.launch_block_grad_nhwc(x, dy, out, n, h, w, c, r, s_, k, bp, algo=algo, stream=stream)
+                M.launch_block_grad_nhwc(xin, dy, out, n, h, w, c, r, s_, k, bp, algo=algo, stream=stream)
             else:
-                M.launch_grad_nhwc(x, dy, out, n, h, w, c, r, s_, k, conv, algo=algo, stream=stream)
+                M.launch_grad_nhwc(xin, dy, out, n, h, w, c, r, s_, k, conv, algo=algo, stream=stream)
 
         if args.op == "fprop":
             fprop(y)
@@ -345,6 +346,16 @@ def bench_fp32(args) -> None:
             want = (oracle.block_grad_f32(x1, dy1, wshape, conv) if args.blocked
                     else oracle.grad_f32(x1, dy1, wshape, conv))
             ok = oracle.verify_tensors(want, dw0.cpu().numpy(), 1e-4, 1e-3)
+            # and at the full timed size on small-integer inputs, where every partial sum is an
+            # exact fp32 integer in any order: AUTO must equal the direct kernel bit for bit
+            xi = torch.randint(-3, 4, x.shape, device=dev, generator=gen).float()
+            dyi = torch.randint(-3, 4, dy.shape, device=dev, generator=gen).float()
+            grad(dyi, dw, xin=xi)
+            dw_ref = torch.empty_like(wt)
+            grad(dyi, dw_ref, "direct", xin=xi)
+            torch.cuda.synchronize()
+            ok = ok and torch.equal(dw, dw_ref)
+            del xi, dyi, dw_ref
 
             def step():
                 grad(dy, dw)
@@ -372,7 +383,9 @@ def bench_fp32(args) -> None:
                 else M.plan_f32(args.op, n, h, w, c, r, s_, k, M.Conv2DParams(*conv)))
         rows.append(dict(name=name, n=n, h=h, w=w, c=c, k=k, r=r, s=s_, groups=g, stride=sh, by=by, bx=bx, kernel=algo,
                          us=round(ms * 1e3, 2), tflops=round(tf, 3), gbs=round(gbs, 1), bound=bound,
-                         frac=round(frac, 4), verified=ok, verified_on="the image-0 problem vs the oracle"))
+                         frac=round(frac, 4), verified=ok,
+                         verified_on=("the image-0 problem vs the oracle; the full problem on small integers, AUTO "
+                                      "== direct bit for bit" if args.op == "grad" else "image 0 vs the oracle")))
         del x, wt, y
         torch.cuda.empty_cache()
     if not rows:

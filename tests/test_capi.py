@@ -345,3 +345,57 @@ def test_plan_f32_names_the_kernel_each_pass_runs():
         M.plan_f32("wgrad", *r50)
     with pytest.raises(M.MiqError):
         M.plan_f32("fprop", 1, 2, 2, 16, 3, 3, 16, _capi.Conv2DParams(0, 0, 1, 1, 1, 1, 1))  # no output pixels
+
+
+def test_blocked_fp32_dropins_and_validation():
+    # the reference's launch_block_{fprop,bprop,grad}_nhwc (conv_types.h:296-304), same mangled names
+    syms = exported()
+    for need in ("_Z23launch_block_fprop_nhwcPKfS0_PfiiiiiiiRK17BlockConv2DParamsS0_13BlockBiasMode",
+                 "_Z23launch_block_bprop_nhwcPKfS0_PfiiiiiiiRK17BlockConv2DParams",
+                 "_Z22launch_block_grad_nhwcPKfS0_PfiiiiiiiRK17BlockConv2DParamsS1_13BlockBiasMode"):
+        assert need in syms, need
+    lib = M.lib()
+    p = C.c_void_p(256)  # never dereferenced: each call fails validation or has no work
+    conv = _capi.Conv2DParams(1, 1, 1, 1, 1, 1, 1)
+    ok = _capi.BlockConv2DParams(conv, 2, 2)
+    for fn, extra in ((lib.miq_block_fprop_nhwc_f32, (p, 0, 0)), (lib.miq_block_bprop_nhwc_f32, (0,)),
+                      (lib.miq_block_grad_nhwc_f32, (p, 0, 0))):
+        # an 8 x 8 output (3x3, pad 1) does not split into a 3 x 2 grid; a 0 grid is rejected outright
+        for by, bx, msg in ((3, 2, b"divisible by block grid"), (0, 2, b"must be > 0")):
+            bad = _capi.BlockConv2DParams(conv, by, bx)
+            assert fn(p, p, p, 1, 8, 8, 4, 3, 3, 4, C.byref(bad), *extra, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+            assert msg in lib.miq_last_error_message()
+        assert fn(p, p, None, 1, 8, 8, 4, 3, 3, 4, C.byref(ok), *extra, None) == _capi.MIQ_ERR_NULL_POINTER
+        assert fn(p, p, p, 1, 8, 8, 4, 3, 3, 4, None, *extra, None) == _capi.MIQ_ERR_NULL_POINTER
+    # bias_mode and algo are checked before any launch
+    assert lib.miq_block_fprop_nhwc_f32(p, p, p, 1, 8, 8, 4, 3, 3, 4, C.byref(ok), p, 2, 0, None) == \
+        _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert b"bias_mode" in lib.miq_last_error_message()
+    assert lib.miq_block_grad_nhwc_f32(p, p, p, 1, 8, 8, 4, 3, 3, 4, C.byref(ok), p, -1, 0, None) == \
+        _capi.MIQ_ERR_INVALID_ARGUMENT
+    assert lib.miq_block_bprop_nhwc_f32(p, p, p, 1, 8, 8, 4, 3, 3, 4, C.byref(ok), 9, None) == \
+        _capi.MIQ_ERR_INVALID_ARGUMENT
+    # c/groups == 2: no MFMA form
+    assert lib.miq_block_fprop_nhwc_f32(p, p, p, 1, 8, 8, 2, 3, 3, 4, C.byref(ok), None, 0, 2, None) == \
+        _capi.MIQ_ERR_UNSUPPORTED
+    # empty batch: nothing to do for fprop / bprop
+    assert lib.miq_block_fprop_nhwc_f32(None, p, None, 0, 8, 8, 4, 3, 3, 4, C.byref(ok), None, 0, 0, None) == _capi.MIQ_OK
+    assert lib.miq_block_bprop_nhwc_f32(None, p, None, 0, 8, 8, 4, 3, 3, 4, C.byref(ok), 0, None) == _capi.MIQ_OK
+    with pytest.raises(ValueError, match="bias_mode"):
+        M.launch_block_fprop_nhwc(256, 256, 256, 1, 8, 8, 4, 3, 3, 4, ok, 256, "both", stream=0)
+
+
+def test_plan_block_f32():
+    conv = _capi.Conv2DParams(1, 1, 1, 1, 1, 1, 1)
+    b22 = M.BlockConv2DParams(conv, 2, 2)
+    assert M.plan_block_f32("fprop", 32, 56, 56, 64, 3, 3, 64, b22) == "igemm"
+    assert M.plan_block_f32("bprop", 32, 56, 56, 64, 3, 3, 64, b22) == "bprop_igemm"
+    assert M.plan_block_f32("grad", 32, 56, 56, 64, 3, 3, 64, b22) == "grad_igemm"
+    # depthwise blocked: no depthwise kernel for blocked filters, the direct ones run
+    dwp = M.BlockConv2DParams(_capi.Conv2DParams(1, 1, 1, 1, 1, 1, 64), 2, 2)
+    assert M.plan_block_f32("fprop", 32, 56, 56, 64, 3, 3, 64, dwp) == "direct"
+    assert M.plan_block_f32("grad", 32, 56, 56, 64, 3, 3, 64, dwp) == "grad_igemm"
+    s2 = M.BlockConv2DParams(_capi.Conv2DParams(1, 1, 2, 2, 1, 1, 1), 2, 2)
+    assert M.plan_block_f32("bprop", 32, 56, 56, 64, 3, 3, 64, s2) == "direct"
+    with pytest.raises(M.MiqError, match="divisible"):
+        M.plan_block_f32("fprop", 32, 56, 56, 64, 3, 3, 64, M.BlockConv2DParams(conv, 3, 2))
