@@ -41,8 +41,9 @@ typedef enum miq_status {
 
 /* Kernel families of the int8 entry points (miq_qconv_desc.algo). */
 typedef enum miq_algo {
-  MIQ_ALGO_AUTO = 0,   /* pick by shape: band kernel, else flat kernel, else stream kernel, else implicit
-                          GEMM, else stem kernel for thin C, else direct */
+  MIQ_ALGO_AUTO = 0,   /* pick by shape: band kernel, else flat kernel, else stream kernel, else the dot4
+                          kernel for <= 8 output channels per group on 1x1 or small filters, else
+                          implicit GEMM, else stem kernel for thin C, else direct */
   MIQ_ALGO_DIRECT = 1, /* VALU direct convolution: any shape, bandwidth-bound fallback */
   MIQ_ALGO_IGEMM = 2,  /* int8 MFMA implicit GEMM: needs (c/groups) % 16 == 0, 16-byte aligned tensors */
   MIQ_ALGO_STEM = 3,   /* int8 MFMA thin-channel kernel: c/groups < 16, groups == 1 */
@@ -57,7 +58,10 @@ typedef enum miq_algo {
   MIQ_ALGO_FLAT = 7    /* int8 MFMA row-band kernel over virtual pixels (rows padded to the input
                           halo's width), filter held in registers: needs stride 1, (c/groups) % 64
                           == 0, (k/groups) % 64 == 0, r*s*c/groups <= 576, a band's input rows that
-                          fit in LDS, 16-byte aligned tensors, bias and scales */
+                          fit in LDS, 16-byte aligned tensors, bias and scales */,
+  MIQ_ALGO_DOT4 = 8    /* int8 vector-ALU kernel (v_dot4_i32_i8, no matrix instructions): any shape
+                          whose filter tile, r*s*ceil(c/groups/4) x up to 32 channels dwords, fits in
+                          64 KB; the bandwidth-bound fallback for thin C and few output channels */
 } miq_algo;
 
 /* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */

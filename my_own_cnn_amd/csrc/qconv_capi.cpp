@@ -181,6 +181,8 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
         *algo = MIQ_ALGO_FLAT;
       } else if (miq::stream_eligible(*g, x, w, y, rq, epi, nullptr)) {
         *algo = MIQ_ALGO_STREAM;
+      } else if (miq::dot4_preferred(*g)) {
+        *algo = MIQ_ALGO_DOT4;
       } else if (miq::igemm_eligible(*g, x, w, y, epi, nullptr)) {
         *algo = MIQ_ALGO_IGEMM;
       } else if (miq::stem_eligible(*g, x, w, y, epi, nullptr)) {
@@ -211,6 +213,10 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
     case MIQ_ALGO_FLAT:
       if (!miq::flat_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       *algo = MIQ_ALGO_FLAT;
+      break;
+    case MIQ_ALGO_DOT4:
+      if (!miq::dot4_eligible(*g, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_DOT4;
       break;
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
@@ -243,6 +249,7 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
     case MIQ_ALGO_BAND: e = miq::launch_i8_band(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_STREAM: e = miq::launch_i8_stream(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_FLAT: e = miq::launch_i8_flat(g, epi, x, w, y, rq, s); break;
+    case MIQ_ALGO_DOT4: e = miq::launch_i8_dot4(g, epi, x, w, y, rq, s); break;
     default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");

@@ -106,6 +106,15 @@ bool stream_eligible(const Geom& g, const void* x, const void* w, const void* y,
 hipError_t launch_i8_stream(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                             hipStream_t stream);
 
+// int8 convolution on the vector ALU (v_dot4_i32_i8), any group shape: the filter tile
+// (r * s * ceil(Cg/4) * up to 32 channels dwords) must fit in 64 KB of LDS.
+bool dot4_eligible(const Geom& g, std::string* why);
+// AUTO's choice of it: few output channels per group (<= 8) on a 1x1 or small filter, where it
+// measured faster than the implicit GEMM
+bool dot4_preferred(const Geom& g);
+hipError_t launch_i8_dot4(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                          hipStream_t stream);
+
 // int8 MFMA thin-channel kernel for stems: groups == 1, C < 16.
 bool stem_eligible(const Geom& g, const void* x, const void* w, const void* y, Epi epi, std::string* why);
 hipError_t launch_i8_stem(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,

@@ -399,3 +399,18 @@ def test_plan_block_f32():
     assert M.plan_block_f32("bprop", 32, 56, 56, 64, 3, 3, 64, s2) == "direct"
     with pytest.raises(M.MiqError, match="divisible"):
         M.plan_block_f32("fprop", 32, 56, 56, 64, 3, 3, 64, M.BlockConv2DParams(conv, 3, 2))
+
+
+@pytest.mark.parametrize("shape,want", [
+    (((32, 56, 56, 64), (8, 1, 1, 64), {}), "dot4"),           # 1x1, 8 output channels
+    (((32, 28, 28, 512), (4, 1, 1, 512), {}), "dot4"),
+    (((1, 56, 56, 64), (1, 1, 1, 64), {}), "dot4"),
+    (((32, 112, 112, 16), (8, 3, 3, 16), {"padding": 1}), "dot4"),  # 3x3 with r*s*c/g = 144
+    (((32, 56, 56, 64), (8, 3, 3, 64), {"padding": 1}), "igemm"),   # 576: the implicit GEMM measured faster
+    (((32, 56, 56, 64), (12, 1, 1, 64), {}), "igemm"),         # 12 channels: equal, not taken
+    (((32, 56, 56, 64), (16, 1, 1, 64), {}), "band"),          # band kernels win from 16 channels
+    (((32, 224, 224, 3), (64, 7, 7, 3), {"padding": 3, "stride": 2}), "stem"),  # C = 3 stem stays on MFMA
+])
+def test_auto_takes_the_dot4_kernel_where_it_measured_faster(shape, want):
+    xs, ws, kw = shape
+    assert M.plan(M.make_desc(xs, ws, **kw)) == want

@@ -69,7 +69,7 @@ def algos_for(x, w, conv):
     n, h, wd, c = x.shape
     k, r, s, _ = w.shape
     out = ["auto", "direct"]
-    for a in ("igemm", "stem", "band"):
+    for a in ("igemm", "stem", "band", "dot4"):
         d = M.make_desc(x.shape, w.shape, stride=conv[2:4], padding=conv[0:2], dilation=conv[4:6], groups=conv[6],
                         algo=a)
         try:
@@ -93,7 +93,7 @@ def test_int8_accumulators_every_algo(device):
             torch.cuda.synchronize()
             np.testing.assert_array_equal(y.cpu().numpy(), c["y"], err_msg=f"{name} {algo}")
             ran.add(algo)
-    assert ran == {"auto", "direct", "igemm", "stem", "band"}
+    assert ran == {"auto", "direct", "igemm", "stem", "band", "dot4"}
 
 
 def requant_inputs(k, seed):
@@ -153,10 +153,16 @@ def test_config_full_size(device, name):
     np.testing.assert_array_equal(q.cpu().numpy(), want_q)
     want_f = oracle.dequant_f32(acc_h, inp["bias"], inp["w_scale"], wl.in_scale, wl.out_scale, wl.relu)
     np.testing.assert_array_equal(f.cpu().numpy().view(np.uint32), want_f.view(np.uint32))
-    # the VALU fallback agrees on the full problem too
+    # the VALU kernels agree on the full problem too: the direct one and the v_dot4 one
     acc2 = M.qconv2d_nhwc_i8_acc32(xd, wd, algo="direct", **kw)
     torch.cuda.synchronize()
     assert hashlib.sha256(acc2.cpu().numpy().tobytes()).hexdigest() == g["acc_sha256"]
+    acc3 = M.qconv2d_nhwc_i8_acc32(xd, wd, algo="dot4", **kw)
+    q3 = M.qconv2d_nhwc_i8(xd, wd, bd, sd, relu=wl.relu, in_scale=wl.in_scale, out_scale=wl.out_scale, algo="dot4",
+                           **kw)
+    torch.cuda.synchronize()
+    assert hashlib.sha256(acc3.cpu().numpy().tobytes()).hexdigest() == g["acc_sha256"], f"{name}: dot4 accumulators"
+    np.testing.assert_array_equal(q3.cpu().numpy(), want_q)
 
 
 def test_stride_two_is_subsampled_stride_one_full_size(device):

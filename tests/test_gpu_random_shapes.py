@@ -1,6 +1,6 @@
 """A seeded sweep of random convolution shapes: for each, the AUTO choice and every kernel
 family that accepts the shape (row band, virtual-pixel band, filter stream, implicit GEMM, stem, direct) against
-the CPU oracle.  The shapes draw channel counts, filter sizes, strides, padding, dilation and
+the CPU oracle (the vector-ALU dot4 kernel included).  The shapes draw channel counts, filter sizes, strides, padding, dilation and
 groups at random within small sizes, so the planners' choices (tiles per workgroup, ring
 depths, odd and even K-block counts, band heights, partly filled bands and segments) vary
 from shape to shape.  Integer outputs bit-exact; the fp32 view bit for bit."""
@@ -16,7 +16,7 @@ from my_own_cnn_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 
-ALGOS = ["band", "flat", "stream", "igemm", "stem", "direct"]
+ALGOS = ["band", "flat", "stream", "igemm", "stem", "dot4", "direct"]
 
 
 def _shapes(count, seed):
