@@ -4,6 +4,7 @@
     python bench.py --bmm [--config r50_3x3_im2col]      # the int32 matrix product instead
     python bench.py --fp32 [--config resnet_like_56x56]  # the fp32 convolution (conv_bench suite)
     python bench.py --fp32 --blocked [--op bprop]        # the blocked fp32 convolution (blocked suite)
+    python bench.py --fallback                           # v_dot4 kernel against the MFMA kernels on thin layers
     python bench.py --qi32 [--config r50_3x3]            # the reference's float-code API
 
 One step = one fused conv + bias + requantize (+ ReLU) pass of libmiq_qconv over one batch
@@ -64,6 +65,9 @@ def parse():
                     help="measure the fp32 convolution (launch_fprop_nhwc) on the reference's conv_bench suite")
     ap.add_argument("--qi32", action="store_true",
                     help="measure the reference's float-code API (launch_fprop_nhwc_qi32, LinQuantU8) on the workloads")
+    ap.add_argument("--fallback", action="store_true",
+                    help="time the vector-ALU dot4 kernel against the MFMA kernels on thin-channel and few-output-"
+                         "channel layers (every kernel family that accepts each shape)")
     ap.add_argument("--blocked", action="store_true",
                     help="with --fp32: the blocked convolution (launch_block_*_nhwc) on the reference's blocked suite")
     ap.add_argument("--op", choices=["fprop", "bprop", "grad"], default="fprop",
@@ -441,6 +445,112 @@ def bench_fp32(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+# Thin layers for the non-MFMA fallback: the C = 3 stem (C5) and layers with few output channels
+# (name, n, h, w, c, k, r, s, (pad_h, pad_w, stride_h, stride_w, dil_h, dil_w, groups), relu)
+FALLBACK_SHAPES = [
+    ("stem_c3_k64", 32, 224, 224, 3, 64, 7, 7, (3, 3, 2, 2, 1, 1, 1), True),
+    ("stem_c3_k16", 32, 224, 224, 3, 16, 7, 7, (3, 3, 2, 2, 1, 1, 1), True),
+    ("1x1_64to1", 32, 56, 56, 64, 1, 1, 1, (0, 0, 1, 1, 1, 1, 1), False),
+    ("1x1_64to8", 32, 56, 56, 64, 8, 1, 1, (0, 0, 1, 1, 1, 1, 1), False),
+    ("1x1_512to4", 32, 14, 14, 512, 4, 1, 1, (0, 0, 1, 1, 1, 1, 1), False),
+    ("1x1_16to8", 32, 112, 112, 16, 8, 1, 1, (0, 0, 1, 1, 1, 1, 1), False),
+    ("1x1_64to8_n1", 1, 56, 56, 64, 8, 1, 1, (0, 0, 1, 1, 1, 1, 1), False),
+    ("3x3_16to8", 32, 112, 112, 16, 8, 3, 3, (1, 1, 1, 1, 1, 1, 1), True),
+    ("3x3_64to8", 32, 56, 56, 64, 8, 3, 3, (1, 1, 1, 1, 1, 1, 1), True),
+    ("1x1_64to12", 32, 56, 56, 64, 12, 1, 1, (0, 0, 1, 1, 1, 1, 1), False),
+    ("1x1_64to16", 32, 56, 56, 64, 16, 1, 1, (0, 0, 1, 1, 1, 1, 1), False),
+]
+
+
+def bench_fallback(args) -> None:
+    """Times every int8 kernel family that accepts each FALLBACK_SHAPES layer (graph replay of
+    `steps` launches over rotating input/output sets), checks each family's output on image 0
+    against the oracle bit for bit, prints a table on stderr and one JSON line; the rows show
+    which family AUTO takes and what the others measured."""
+    import numpy as np
+    import torch
+
+    import my_own_cnn_amd as M
+    import oracle  # checker of image 0 only
+    from my_own_cnn_amd import workloads as W
+
+    dev = torch.device("cuda:0")
+    families = ["dot4", "igemm", "stem", "band", "flat", "stream"]
+    rows = []
+    for name, n, h, w, c, k, r, s_, conv, relu in FALLBACK_SHAPES:
+        if args.config not in (None, name):
+            continue
+        g = conv[6]
+        kw = dict(padding=conv[:2], stride=conv[2:4], dilation=conv[4:6], groups=g)
+        ho, wo = M.infer_conv_shape(n, h, w, c, r, s_, k, M.Conv2DParams(*conv))
+        x0 = W.fill_i8_uniform(n * h * w * c, 31, -128, 127).reshape(n, h, w, c)
+        wt = W.fill_i8_uniform(k * r * s_ * (c // g), 32, -127, 127).reshape(k, r, s_, c // g)
+        bias = W.fill_i32_uniform(k, 33, -1024, 1024)
+        wsc = W.fill_f32_uniform(k, 34, 1e-3, 1e-2)
+        want = oracle.requant_i8(oracle.conv_i8_acc(x0[:1], wt, conv), bias, wsc, 0.02, 1.0, relu)
+        set_bytes = x0.nbytes + n * ho * wo * k
+        nsets = max(1, min(args.steps, POOL_BYTES // set_bytes))
+        xpool = torch.empty((nsets,) + x0.shape, dtype=torch.int8, device=dev)
+        xpool.copy_(torch.from_numpy(x0).to(dev).unsqueeze(0).expand_as(xpool))
+        ypool = torch.empty((nsets, n, ho, wo, k), dtype=torch.int8, device=dev)
+        wd, bd, sd = (torch.from_numpy(a).to(dev) for a in (wt, bias, wsc))
+        auto = M.plan(M.make_desc(x0.shape, wt.shape, **kw))
+        row = {"name": name, "n": n, "h": h, "w": w, "c": c, "k": k, "r": r, "s": s_, "stride": conv[2], "groups": g,
+               "auto": auto, "us": {}, "verified": {}}
+        for fam in families:
+            try:
+                M.plan(M.make_desc(x0.shape, wt.shape, algo=fam, **kw))
+            except M.MiqError:
+                continue  # this family does not take the shape
+
+            def step(i, fam=fam):
+                M.qconv2d_nhwc_i8(xpool[i % nsets], wd, bd, sd, relu=relu, in_scale=0.02, algo=fam,
+                                  out=ypool[i % nsets], **kw)
+
+            step(0)
+            torch.cuda.synchronize()
+            row["verified"][fam] = bool(np.array_equal(ypool[0, :1].cpu().numpy(), want))
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(args.steps):
+                    step(i)
+            graph.replay()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            gpu_hold(hold_us(args.steps, 3.0))
+            t0.record()
+            graph.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            row["us"][fam] = round(t0.elapsed_time(t1) * 1e3 / args.steps, 2)
+            del graph
+        rows.append(row)
+        del xpool, ypool
+        torch.cuda.empty_cache()
+    if not rows:
+        print(f"bench.py: unknown --fallback shape {args.config}; known: {[f[0] for f in FALLBACK_SHAPES]}",
+              file=sys.stderr)
+        sys.exit(2)
+    print(f"{'shape':14s} {'auto':6s} " + " ".join(f"{f:>8s}" for f in families) + "  verified", file=sys.stderr)
+    for r_ in rows:
+        cells = " ".join(f"{r_['us'][f]:8.2f}" if f in r_["us"] else f"{'-':>8s}" for f in families)
+        print(f"{r_['name']:14s} {r_['auto']:6s} {cells}  {all(r_['verified'].values())}", file=sys.stderr)
+    head = rows[0]
+    line = {
+        "metric": "int8 us per launch by kernel family on thin layers (the vector-ALU fallback against the MFMA "
+                  "kernels)",
+        "value": head["us"][head["auto"]], "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["us"][head["auto"]] / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": head["name"], "kernel": head["auto"], "timing": "hipgraph back-to-back",
+                   "cache": "rotating sets"},
+        "shapes": rows,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def bench_qi32(args) -> None:
     """Times the reference's own entry point, launch_fprop_nhwc_qi32<LinQuantU8>, on the workloads'
     shapes with uint8 float codes and per-sample zero points (int32 accumulators out); checks
@@ -590,6 +700,9 @@ def main():
         return
     if args.qi32:
         bench_qi32(args)
+        return
+    if args.fallback:
+        bench_fallback(args)
         return
     dev = torch.device("cuda:0")
     # every BASELINE config by default (the headline first: its line is `value`); --config
