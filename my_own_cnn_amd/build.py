@@ -36,6 +36,7 @@ SOURCES = [
     "conv_f32.hip",
     "grad_noalloc.hip",
     "qconv_qi32.hip",
+    "qconv_qi32_band.hip",
     "conv_quant_host.cpp",
     "verify.cpp",
     "bench.cpp",

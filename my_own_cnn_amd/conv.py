@@ -138,6 +138,34 @@ def launch_fprop_nhwc_qi32(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Point
              _stream(stream)), "launch_fprop_nhwc_qi32")
 
 
+QI32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2, "band": 4}
+
+
+def fprop_nhwc_qi32_algo(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int,
+                         r: int, s: int, k: int, p=None, in_qp: Pointer = None, f_qp: Pointer = None,
+                         algo: str = "auto", stream=None) -> None:
+    """launch_fprop_nhwc_qi32 with an explicit kernel ("auto", "band", "igemm" or "direct");
+    every choice gives the same int32 results."""
+    tin = DataType(tin)
+    if tin not in SUPPORTED_QI32_INPUTS:
+        raise TypeError("launch_fprop_nhwc_qi32 supports only LinQuantU8 and LinQuantS5")
+    if in_qp is None or f_qp is None:
+        raise RuntimeError("quantized CUDA fprop requires non-null quantization parameters")
+    params = _as_params(p)
+    kind = 0 if tin == DataType.LinQuantU8 else 1
+    check(lib().miq_fprop_nhwc_qi32_algo(kind, _addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k,
+                                         C.byref(params), _addr(in_qp), _addr(f_qp), QI32_ALGOS[algo],
+                                         _stream(stream)), "fprop_nhwc_qi32_algo")
+
+
+def plan_qi32(n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=None) -> str:
+    """The kernel launch_fprop_nhwc_qi32 runs for this problem (aligned tensors)."""
+    out = C.c_int32()
+    params = _as_params(p)
+    check(lib().miq_plan_qi32(n, h, w, c, r, s, k, C.byref(params), C.byref(out)), "plan_qi32")
+    return {v: key for key, v in QI32_ALGOS.items()}[out.value]
+
+
 def launch_block_fprop_nhwc_qi32(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int,
                                  c: int, r: int, s: int, k: int, p: BlockConv2DParams, in_qp: Pointer = None,
                                  f_qp: Pointer = None, stream=None) -> None:

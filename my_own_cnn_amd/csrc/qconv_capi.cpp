@@ -145,25 +145,52 @@ int bprop_f32(const miq::Geom& g, const miq::BlockGeom& bg, const float* dy, con
   return MIQ_OK;
 }
 
+// The kernel AUTO runs for a float-code problem: the row-band kernel, else the implicit GEMM,
+// else the direct kernel.
+int32_t qi32_auto(const miq::Geom& g, const miq::BlockGeom& bg, const void* x, const void* w, const void* y) {
+  if (miq::qi32_band_eligible(g, bg, x, w, y, nullptr)) return MIQ_ALGO_BAND;
+  if (miq::qi32_igemm_eligible(g, bg, x, w, nullptr)) return MIQ_ALGO_IGEMM;
+  return MIQ_ALGO_DIRECT;
+}
+
 int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const miq::Geom& g,
-               const miq::BlockGeom& bg, const void* in_qp, const void* f_qp, void* stream) {
+               const miq::BlockGeom& bg, const void* in_qp, const void* f_qp, void* stream,
+               int32_t algo = MIQ_ALGO_AUTO) {
   const long long filt = filt_elems(g) * bg.By * bg.Bx;
   int st = check_tensors(g, filt, x, w, y);
   if (st != MIQ_OK) return st;
   if (in_qp == nullptr || f_qp == nullptr) {
     return fail(MIQ_ERR_NULL_POINTER, "quantized fprop requires non-null quantization parameters");
   }
+  std::string why;
+  switch (algo) {
+    case MIQ_ALGO_AUTO: algo = qi32_auto(g, bg, x, w, y); break;
+    case MIQ_ALGO_DIRECT: break;
+    case MIQ_ALGO_IGEMM:
+      if (!miq::qi32_igemm_eligible(g, bg, x, w, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      break;
+    case MIQ_ALGO_BAND:
+      if (!miq::qi32_band_eligible(g, bg, x, w, y, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      break;
+    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM or BAND");
+  }
   if (out_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  // plain or blocked filters: the MFMA implicit GEMM where it applies
-  if (miq::qi32_igemm_eligible(g, bg, x, w, nullptr)) {
-    const hipError_t e = miq::launch_qi32_igemm(g, bg, qk, x, w, y, in_qp, f_qp, hs);
-    if (e != hipSuccess) return hip_fail(e, "qi32 implicit GEMM launch");
-    return MIQ_OK;
+  hipError_t e;
+  switch (algo) {
+    case MIQ_ALGO_BAND:
+      e = miq::launch_qi32_band(g, bg, qk, x, w, y, in_qp, f_qp, hs);
+      if (e != hipSuccess) return hip_fail(e, "qi32 row-band launch");
+      return MIQ_OK;
+    case MIQ_ALGO_IGEMM:
+      e = miq::launch_qi32_igemm(g, bg, qk, x, w, y, in_qp, f_qp, hs);
+      if (e != hipSuccess) return hip_fail(e, "qi32 implicit GEMM launch");
+      return MIQ_OK;
+    default:
+      e = miq::launch_qi32_direct(g, bg, qk, x, w, y, in_qp, f_qp, hs);
+      if (e != hipSuccess) return hip_fail(e, "qi32 direct convolution launch");
+      return MIQ_OK;
   }
-  const hipError_t e = miq::launch_qi32_direct(g, bg, qk, x, w, y, in_qp, f_qp, hs);
-  if (e != hipSuccess) return hip_fail(e, "qi32 direct convolution launch");
-  return MIQ_OK;
 }
 
 // Validates an int8 problem and resolves the kernel family.
@@ -329,6 +356,28 @@ int miq_fprop_nhwc_qi32_s5(const float* x, const float* w, int32_t* y, int32_t n
   const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
   if (st != MIQ_OK) return st;
   return qi32_entry(miq::kQpS5, x, w, y, g, miq::BlockGeom{1, 1, g.Ho, g.Wo}, in_qp, f_qp, stream);
+}
+
+int miq_fprop_nhwc_qi32_algo(int32_t qp_kind, const float* x, const float* w, int32_t* y, int32_t n, int32_t h,
+                             int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
+                             const void* in_qp, const void* f_qp, int32_t algo, void* stream) {
+  if (qp_kind != 0 && qp_kind != 1) return fail(MIQ_ERR_INVALID_ARGUMENT, "qp_kind must be 0 (LinQuantU8) or 1 (LinQuantS5)");
+  miq::Geom g;
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  return qi32_entry(qp_kind == 0 ? miq::kQpU8 : miq::kQpS5, x, w, y, g, miq::BlockGeom{1, 1, g.Ho, g.Wo}, in_qp, f_qp,
+                    stream, algo);
+}
+
+int miq_plan_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                  const miq_conv2d_params* p, int32_t* algo) {
+  if (algo == nullptr) return fail(MIQ_ERR_NULL_POINTER, "algo output pointer is NULL");
+  miq::Geom g;
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  *algo = qi32_auto(g, miq::BlockGeom{1, 1, g.Ho, g.Wo}, kAligned, kAligned, kAligned);
+  return MIQ_OK;
 }
 
 int miq_block_fprop_nhwc_qi32_u8(const float* x, const float* w, int32_t* y, int32_t n, int32_t h, int32_t wdt,

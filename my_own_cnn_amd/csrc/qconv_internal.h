@@ -76,6 +76,16 @@ bool qi32_igemm_eligible(const Geom& g, const BlockGeom& bg, const void* x, cons
 hipError_t launch_qi32_igemm(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
                              const void* in_qp, const void* f_qp, hipStream_t stream);
 
+// int32 accumulators on float codes on the int8 row-band structure (codes staged once per band
+// as offset int8 values, filter in registers): plain filters, (C/groups) % 64 == 0,
+// (K/groups) % 16 == 0, stride_w == 1, Wo <= 64, R*S*C/groups <= 576, 16-byte aligned x, w, y.
+// Exact for any codes: a workgroup whose codes leave the parameter type's int8 window computes
+// directly.
+bool qi32_band_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, const void* y,
+                        std::string* why);
+hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
+                            const void* in_qp, const void* f_qp, hipStream_t stream);
+
 // int8 VALU direct convolution: any geometry.
 hipError_t launch_i8_direct(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                             hipStream_t stream);
