@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "miq_qconv.h"
 #include "qconv_internal.h"
@@ -145,6 +146,52 @@ int bprop_f32(const miq::Geom& g, const miq::BlockGeom& bg, const float* dy, con
   return MIQ_OK;
 }
 
+// Grow-only workspace per (device, stream) for the float-code row-band path (its filter
+// prepass output).  Calls on one stream are ordered and share it; each stream has its own, so
+// calls on different streams do not race.  Growing waits for the stream before freeing the old
+// buffer, which earlier launches on it may still read.
+struct StreamWorkspace {
+  int dev;
+  hipStream_t stream;
+  void* p;
+  size_t bytes;
+};
+std::mutex g_qi32_ws_m;
+std::vector<StreamWorkspace> g_qi32_ws;
+
+int stream_workspace(hipStream_t s, size_t bytes, void** out) {
+  *out = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_qi32_ws_m);
+  StreamWorkspace* w = nullptr;
+  for (auto& c : g_qi32_ws) {
+    if (c.dev == dev && c.stream == s) w = &c;
+  }
+  if (w == nullptr) {
+    g_qi32_ws.push_back(StreamWorkspace{dev, s, nullptr, 0});
+    w = &g_qi32_ws.back();
+  }
+  if (w->bytes < bytes) {
+    if (w->p != nullptr) {
+      e = hipStreamSynchronize(s);
+      if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize before growing the qi32 workspace");
+      (void)hipFree(w->p);
+      w->p = nullptr;
+      w->bytes = 0;
+    }
+    e = hipMalloc(&w->p, bytes);
+    if (e != hipSuccess) {
+      w->p = nullptr;
+      return hip_fail(e, "hipMalloc of the qi32 workspace");
+    }
+    w->bytes = bytes;
+  }
+  *out = w->p;
+  return MIQ_OK;
+}
+
 // The kernel AUTO runs for a float-code problem: the row-band kernel, else the implicit GEMM,
 // else the direct kernel.
 int32_t qi32_auto(const miq::Geom& g, const miq::BlockGeom& bg, const void* x, const void* w, const void* y) {
@@ -178,10 +225,14 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   hipError_t e;
   switch (algo) {
-    case MIQ_ALGO_BAND:
-      e = miq::launch_qi32_band(g, bg, qk, x, w, y, in_qp, f_qp, hs);
+    case MIQ_ALGO_BAND: {
+      void* ws = nullptr;
+      st = stream_workspace(hs, miq::qi32_band_workspace_bytes(g), &ws);
+      if (st != MIQ_OK) return st;
+      e = miq::launch_qi32_band(g, bg, qk, x, w, y, in_qp, f_qp, ws, hs);
       if (e != hipSuccess) return hip_fail(e, "qi32 row-band launch");
       return MIQ_OK;
+    }
     case MIQ_ALGO_IGEMM:
       e = miq::launch_qi32_igemm(g, bg, qk, x, w, y, in_qp, f_qp, hs);
       if (e != hipSuccess) return hip_fail(e, "qi32 implicit GEMM launch");

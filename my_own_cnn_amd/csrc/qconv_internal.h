@@ -83,8 +83,12 @@ hipError_t launch_qi32_igemm(const Geom& g, const BlockGeom& bg, QpKind qp, cons
 // directly.
 bool qi32_band_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, const void* y,
                         std::string* why);
+// Device bytes of the workspace launch_qi32_band takes (the filter converted once per call to
+// int8 MFMA fragments, and range flags); the caller keeps it unused by other work until the
+// launches on `stream` have completed.
+size_t qi32_band_workspace_bytes(const Geom& g);
 hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
-                            const void* in_qp, const void* f_qp, hipStream_t stream);
+                            const void* in_qp, const void* f_qp, void* ws, hipStream_t stream);
 
 // int8 VALU direct convolution: any geometry.
 hipError_t launch_i8_direct(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,

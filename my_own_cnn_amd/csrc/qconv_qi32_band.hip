@@ -27,12 +27,18 @@
 // 16-pixel segments run one per phase.  Output channels are not permuted: MFMA row block j
 // holds channels 16j .. 16j + 15, so the 4 lanes of a pixel store 64 contiguous bytes of int32.
 //
-// Staging.  Every load is a 16-byte buffer load of 4 codes into registers (the values must be
-// converted), 1 KB contiguous per wave instruction, 16 in flight per lane; each lane writes its
-// 4 converted values as one LDS word.  The compiler's own waits order them (buffer loads are
-// counted by vmcnt alone).  The filter goes first, then the band's input rows.  After a barrier
-// the filter row sums and the per-column channel sums are read back from LDS (v_dot4 against
-// ones) and the filter is copied into registers.
+// Filter prepass.  A small kernel converts the filter once per call to offset int8 in MFMA
+// fragment order (and a range flag per 64-channel tile and K-block) into a caller workspace;
+// each band workgroup then loads its tiles by DMA (1 KB per buffer_load ... lds), as the int8
+// band kernel loads its filter.  Converting the float filter in every workgroup instead read
+// 147 KB per CU from L2 on C2 and took ~9 us of its 24.
+//
+// Staging.  Input codes come in 16-byte buffer loads of 4 codes into registers (the values
+// must be converted), 1 KB contiguous per wave instruction when C/groups == 64, 16 in flight
+// per lane; each lane writes its 4 converted values as one LDS word.  The compiler's own waits
+// order them (buffer loads are counted by vmcnt alone).  After a barrier the filter row sums and
+// the per-column channel sums are read back from LDS (v_dot4 against ones) and the filter is
+// copied into registers.
 
 #include "qconv_device.h"
 
@@ -54,14 +60,16 @@ struct Qi32BandArgs {
   int32_t* y;
   const unsigned char* in_qp;
   const unsigned char* f_qp;
+  const int8_t* wfrag;  // the filter prepass's int8 fragments; its range flags follow at byte flags_off
+  int flags_off;
   int H, W, C, K, Ho, Wo;
   int ph, pw, sh, dh, dw, R, S;
-  int Cg, Kg, Kdim;
-  int BH, bands_per_img, NT, WPT, kt_per_group, nblocks;
+  int Cg, Kg;
+  int BH, bands_per_img, NT, kt_per_group, nblocks;
   int NQ, NPB, SEGR;
   int dS, d_rb, c_rb, d_out, c_out;  // segment walk, as in the int8 band kernel
   int ni;                            // input units per workgroup = HR * NQ * NPB
-  int filt_lds, halo_lds;            // LDS byte offsets; channel sums, filter sums, wave marks follow
+  int halo_lds;                      // LDS byte offset of the rows (the filter is at 0); column sums, filter sums, wave marks follow
   int tap[kQbMaxKB];                 // K-block b: halo slot offset of (filter row, quad) << 8 | column shift
   int ntiles;
   FastDivM fd_ntiles, fd_bpi, fd_ktpg, fd_rowi, fd_npb;
@@ -119,11 +127,11 @@ template <QpKind Q, int KB, bool MT>
 __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArgs a_in) {
   const Qi32BandArgs a = preload_args(a_in);
   const int NT = MT ? a.NT : 1;
-  const int WPT = MT ? a.WPT : kQbWaves;
+  const int WPT = kQbWaves / NT;
   constexpr unsigned kOff = Q == kQpU8 ? 128u : 0u;
   constexpr int kKdim = 64 * KB;
   extern __shared__ v4i smem[];
-  v4i* filt = smem + a.filt_lds / 16;
+  v4i* filt = smem;
   v4i* halo = smem + a.halo_lds / 16;
   int* csum = reinterpret_cast<int*>(halo + (a.ni + 1) * 64);  // per unit column: sum of its 64 values
   int* tsum = csum + a.ni * 16;                                 // per workgroup channel: filter row sum
@@ -148,81 +156,76 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
   const int wl = wave - tw * WPT;
   const int row_instr = a.NQ * a.NPB;
 
-  const int zx = __builtin_amdgcn_readfirstlane(qb_zero_point<Q>(a.in_qp, n));
-  const int zw = __builtin_amdgcn_readfirstlane(qb_zero_point<Q>(a.f_qp, 0));
-  const unsigned xpad = static_cast<unsigned>(zx) - kOff;  // staged value of a padded tap
+  // zero points: loaded first, made uniform after the first input loads are issued
+  const int zx_v = qb_zero_point<Q>(a.in_qp, n);
+  const int zw_v = qb_zero_point<Q>(a.f_qp, 0);
+  unsigned xpad = 0;  // staged value of a padded tap: zx - offset
   bool bad = false;
 
-  // ---- staging jobs: one 16-byte load (4 codes) per lane, 1 KB contiguous per wave
-  // instruction, converted to one LDS word.
-  //   Filter job e < nfj: floats 4 (lane + 64 (wave + 8e)) of the workgroup's NT * 64 KRSC rows
-  //   (one contiguous range), to MFMA fragment order: fragment (t, b, j) = channels 16j + row
-  //   of tile t, K-block b; lane (row, q) of it holds bytes 64b + 16q .. of that row.
-  //   Input job nfj + 4u + d: unit i = wave + 8u, its pixels 4d + lane / 16, channels
-  //   4 (lane % 16) .. + 3 of the unit's quad.
-  const __amdgpu_buffer_rsrc_t rw =
-      make_rsrc(a.w + (static_cast<size_t>(gi) * a.Kg + k0) * kKdim, (a.Kg - k0) * kKdim * 4);
+  // ---- filter: the workgroup's NT tiles of int8 fragments from the prepass, contiguous,
+  // by DMA (1 KB per instruction); then the range flags of its tiles' K-blocks
+  const int kt64 = a.kt_per_group * NT;
+  const int tile0 = gi * kt64 + k0 / 64;
+  {
+    const __amdgpu_buffer_rsrc_t rf = make_rsrc(a.wfrag + static_cast<size_t>(tile0) * KB * 4096, NT * KB * 4096);
+    for (int f = wave; f < NT * 4 * KB; f += kQbWaves) load_lds16(rf, filt + f * 64, 16u * lane, static_cast<unsigned>(f * 1024));
+    const __amdgpu_buffer_rsrc_t rfl =
+        make_rsrc(a.wfrag + a.flags_off + static_cast<size_t>(tile0) * KB * 4, NT * KB * 4);
+    // NT * KB <= 72 flags, two per lane; those past the range read 0
+    bad = (__builtin_amdgcn_raw_buffer_load_b32(rfl, 4u * static_cast<unsigned>(lane), 0, 0) |
+           __builtin_amdgcn_raw_buffer_load_b32(rfl, 4u * static_cast<unsigned>(lane + 64), 0, 0)) != 0;
+  }
+
+  // ---- input rows: one 16-byte load (4 codes) per lane, 1 KB contiguous per wave instruction
+  // when C/groups == 64, converted to one LDS word.  Job e: unit i = wave + 8 (e / 4), its
+  // pixels 4 (e % 4) + lane / 16, channels 4 (lane % 16) .. + 3 of the unit's quad.
   const int hi0 = ho0 * a.sh - a.ph;
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(a.x + static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg,
                 (a.H * a.W * a.C - gi * a.Cg) * 4);
-  const int nfj = 2 * NT * KB;
   const int nie = a.ni > wave ? (a.ni - wave + kQbWaves - 1) / kQbWaves : 0;
-  const int nj = nfj + 4 * nie;
+  const int nj = max(4 * nie, 1);
   constexpr int kD = 16;  // jobs in flight per lane
   v4f jv[kD];
   bool jok[kD];
-  // Both job kinds are computed and one is selected (uniformly): straight-line code, so the
-  // compiler's waits stay exact.
-  auto in_pos = [&](int e, int& i, int& pcol, bool& ok, unsigned& off) {
-    const int ue = max(e - nfj, 0);
-    i = wave + kQbWaves * (ue >> 2);
+  auto job_load = [&](int e, int slot) {
+    const int i = wave + kQbWaves * (e >> 2);
     const int hr = fdiv(i, a.fd_rowi);
     const int rem = i - hr * row_instr;
     const int q = fdiv(rem, a.fd_npb);
     const int pb = rem - q * a.NPB;
     const int hi = hi0 + hr;
-    pcol = 4 * (ue & 3) + (lane >> 4);
-    const int col = 16 * pb + pcol - a.pw;
-    ok = static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) && static_cast<unsigned>(col) < static_cast<unsigned>(a.W);
-    off = ok ? static_cast<unsigned>(((hi * a.W + col) * a.C + 64 * q + 4 * (lane & 15)) * 4) : 0u;
-  };
-  auto job_load = [&](int e, int slot) {
-    const bool isf = e < nfj;
-    int i, pcol;
-    bool ok;
-    unsigned off;
-    in_pos(e, i, pcol, ok, off);
-    const unsigned foff = static_cast<unsigned>(4 * (lane + 64 * (wave + kQbWaves * min(e, nfj - 1)))) * 4u;
+    const int col = 16 * pb + 4 * (e & 3) + (lane >> 4) - a.pw;
+    const bool ok = static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) &&
+                    static_cast<unsigned>(col) < static_cast<unsigned>(a.W);
     jok[slot] = ok;
-    jv[slot] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(isf ? rw : rx, isf ? foff : off, 0, 0));
+    const unsigned off = ok ? static_cast<unsigned>(((hi * a.W + col) * a.C + 64 * q + 4 * (lane & 15)) * 4) : 0u;
+    jv[slot] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
   };
   auto job_store = [&](int e, int slot) {
-    const bool isf = e < nfj;
-    const int f = 4 * (lane + 64 * (wave + kQbWaves * min(e, nfj - 1)));
-    const int ct = f / kKdim;
-    const int col = f - ct * kKdim;
-    const int slot16 = (((ct >> 6) * KB + (col >> 6)) * 4 + ((ct >> 4) & 3)) * 64 + 16 * ((col & 63) >> 4) + (ct & 15);
-    const unsigned faddr = filt_addr + 16u * static_cast<unsigned>(slot16) + 4u * static_cast<unsigned>((col & 15) >> 2);
-    const int i = wave + kQbWaves * (max(e - nfj, 0) >> 2);
-    const int pcol = 4 * (max(e - nfj, 0) & 3) + (lane >> 4);
-    const unsigned xaddr = halo_addr + 16u * static_cast<unsigned>(i * 64 + 16 * ((lane & 15) >> 2) + pcol) +
-                           4u * static_cast<unsigned>(lane & 3);
-    const unsigned v = qb_pack4(jv[slot], isf ? k0 + ct < a.Kg : jok[slot], kOff, isf ? 0u : xpad, bad);
-    qb_lds_store32(isf ? faddr : xaddr, v);
+    const int i = wave + kQbWaves * (e >> 2);
+    const int pcol = 4 * (e & 3) + (lane >> 4);
+    const unsigned v = qb_pack4(jv[slot], jok[slot], kOff, xpad, bad);
+    qb_lds_store32(halo_addr + 16u * static_cast<unsigned>(i * 64 + 16 * ((lane & 15) >> 2) + pcol) +
+                       4u * static_cast<unsigned>(lane & 3),
+                   v);
   };
   // Every pass issues the same loads (indices past the end repeat the last job, whose data is
   // never used), so the compiler's waits count exactly the loads still in flight.
 #pragma unroll
   for (int u = 0; u < kD; ++u) job_load(min(u, nj - 1), u);
-  for (int e0 = 0; e0 < nj; e0 += kD) {
+  const int zx = __builtin_amdgcn_readfirstlane(zx_v);
+  const int zw = __builtin_amdgcn_readfirstlane(zw_v);
+  xpad = static_cast<unsigned>(zx) - kOff;
+  for (int e0 = 0; e0 < 4 * nie; e0 += kD) {
 #pragma unroll
     for (int u = 0; u < kD; ++u) {
       const int e = e0 + u;
-      if (e < nj) job_store(e, u);
+      if (e < 4 * nie) job_store(e, u);
       job_load(min(e + kD, nj - 1), u);
     }
   }
+  wait_vmcnt(0);  // the filter DMA (not tracked by the compiler)
   const bool wbad = __any(bad);
   if (lane == 0) marks[wave] = wbad ? 1 : 0;
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -246,7 +249,7 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
       const int t = pix / a.Wo;
       const int wo = pix - t * a.Wo;
       const int ho = ho0 + t;
-      const float* wk = a.w + (static_cast<size_t>(gi) * a.Kg + kg) * a.Kdim;
+      const float* wk = a.w + (static_cast<size_t>(gi) * a.Kg + kg) * kKdim;
       uint32_t acc = 0;
       for (int r = 0; r < a.R; ++r) {
         const int hi = ho * a.sh - a.ph + r * a.dh;
@@ -412,9 +415,41 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
   }
 }
 
+// Filter prepass: block (tile, b) converts K-block b (64 values of every channel) of one
+// 64-channel tile of a group to offset int8 in MFMA fragment order, fragment (b, j) = channels
+// 16j .. 16j + 15, lane (row, q) of it holding bytes 16q .. 16q + 15 of the K-block of channel
+// 16j + row; channels past K/groups are zeros.  Thread (channel c, quarter p) converts values
+// 4p + 16k, k = 0..3, so the 4 threads of a channel fill one 16-byte slot per k.  The block
+// writes 1 to its range flag when a value lies outside int8.
+template <QpKind Q>
+__global__ void __launch_bounds__(256) qi32_filter_prep_kernel(const float* w, int8_t* frag, int* flags, int Kg,
+                                                               int Kdim, int kt64, int KB) {
+  constexpr unsigned kOff = Q == kQpU8 ? 128u : 0u;
+  const int blk = blockIdx.x;
+  const int tile = blk / KB;
+  const int b = blk - tile * KB;
+  const int gi = tile / kt64;
+  const int c = threadIdx.x >> 2;
+  const int p = threadIdx.x & 3;
+  const int kg = 64 * (tile - gi * kt64) + c;
+  const bool ok = kg < Kg;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + static_cast<size_t>(gi) * Kg * Kdim, Kg * Kdim * 4);
+  const unsigned src = static_cast<unsigned>((min(kg, Kg - 1) * Kdim + 64 * b + 4 * p) * 4);
+  v4f v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rw, src + 64u * k, 0, 0));
+  bool bad = false;
+  unsigned* out = reinterpret_cast<unsigned*>(frag + static_cast<size_t>(tile) * KB * 4096 +
+                                              16 * ((b * 4 + ((c >> 4) & 3)) * 64 + (c & 15)) + 4 * p);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) out[64 * k] = qb_pack4(v[k], ok, kOff, 0u, bad);
+  const int any = __syncthreads_or(bad ? 1 : 0);
+  if (threadIdx.x == 0) flags[blk] = any ? 1 : 0;
+}
+
 struct Qi32BandPlan {
   int KB, NQ, NPB, SEGR, NT, WPT, BH, bands_per_img, kt_per_group, HR, ni;
-  int filt_lds, halo_lds;
+  int halo_lds;
   size_t lds_bytes;
 };
 
@@ -454,6 +489,9 @@ bool qb_plan(const Geom& g, const BlockGeom& bg, Qi32BandPlan* p, std::string* w
   if (static_cast<long long>(g.Ho) * g.Wo * g.K * 4 >= (1LL << 30)) return no("qi32 band kernel needs images below 2^30 output bytes");
   if (static_cast<long long>(g.H) * g.W * g.C * 4 >= (1LL << 31)) return no("qi32 band kernel needs images below 2^31 input bytes");
   if (static_cast<long long>(g.Kg) * g.R * g.S * g.Cg * 4 >= (1LL << 31)) return no("qi32 band kernel needs group filters below 2^31 bytes");
+  if (static_cast<long long>(g.G) * ((g.Kg + 63) / 64) * g.R * g.S * (g.Cg / 64) * 4096 >= (1LL << 31)) {
+    return no("qi32 band kernel needs converted filters below 2^31 bytes");
+  }
   p->KB = static_cast<int>(kb);
   p->NQ = g.Cg / 64;
   p->NPB = static_cast<int>((hcols + 15) / 16);
@@ -491,7 +529,6 @@ bool qb_plan(const Geom& g, const BlockGeom& bg, Qi32BandPlan* p, std::string* w
         p->bands_per_img = static_cast<int>(bands);
         p->HR = static_cast<int>(hr);
         p->ni = static_cast<int>(ni);
-        p->filt_lds = 0;
         p->halo_lds = static_cast<int>(static_cast<size_t>(nt) * qb_tile_slots(p->KB) * 16);
         p->lds_bytes = lds;
       }
@@ -536,8 +573,13 @@ bool qi32_band_eligible(const Geom& g, const BlockGeom& bg, const void* x, const
   return qb_plan(g, bg, &pl, why);
 }
 
+size_t qi32_band_workspace_bytes(const Geom& g) {
+  const size_t nfblk = static_cast<size_t>(g.G) * ((g.Kg + 63) / 64) * g.R * g.S * (g.Cg / 64);
+  return nfblk * 4096 + nfblk * 4;
+}
+
 hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
-                            const void* in_qp, const void* f_qp, hipStream_t stream) {
+                            const void* in_qp, const void* f_qp, void* ws, hipStream_t stream) {
   if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
   Qi32BandPlan pl;
   if (!qb_plan(g, bg, &pl, nullptr)) return hipErrorInvalidConfiguration;
@@ -547,11 +589,11 @@ hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const
   a.f_qp = static_cast<const unsigned char*>(f_qp);
   a.H = g.H; a.W = g.W; a.C = g.C; a.K = g.K; a.Ho = g.Ho; a.Wo = g.Wo;
   a.ph = g.ph; a.pw = g.pw; a.sh = g.sh; a.dh = g.dh; a.dw = g.dw; a.R = g.R; a.S = g.S;
-  a.Cg = g.Cg; a.Kg = g.Kg; a.Kdim = g.R * g.S * g.Cg;
-  a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.NT = pl.NT; a.WPT = pl.WPT;
+  a.Cg = g.Cg; a.Kg = g.Kg;
+  a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.NT = pl.NT;
   a.kt_per_group = pl.kt_per_group; a.NQ = pl.NQ; a.NPB = pl.NPB; a.SEGR = pl.SEGR;
   a.ni = pl.ni;
-  a.filt_lds = pl.filt_lds; a.halo_lds = pl.halo_lds;
+  a.halo_lds = pl.halo_lds;
   // K-block b = (tap, chunk quad): halo slot offset of its filter row and quad, column shift
   for (int b = 0; b < kQbMaxKB; ++b) {
     if (b < pl.KB) {
@@ -581,9 +623,21 @@ hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const
   }
   const long long nblocks = static_cast<long long>(g.N) * pl.bands_per_img * g.G * pl.kt_per_group;
   a.nblocks = static_cast<int>(nblocks);
+  // the workspace (qi32_band_workspace_bytes) holds the prepass's fragments, then its flags
+  const int kt64 = (g.Kg + 63) / 64;
+  const int nfblk = g.G * kt64 * pl.KB;
+  const size_t frag_bytes = static_cast<size_t>(nfblk) * 4096;
+  a.wfrag = static_cast<const int8_t*>(ws);
+  a.flags_off = static_cast<int>(frag_bytes);
+  int8_t* frag = static_cast<int8_t*>(ws);
+  int* flags = reinterpret_cast<int*>(frag + frag_bytes);
   if (qp == kQpU8) {
+    hipLaunchKernelGGL(qi32_filter_prep_kernel<kQpU8>, dim3(nfblk), dim3(256), 0, stream, w, frag, flags, g.Kg,
+                       g.R * g.S * g.Cg, kt64, pl.KB);
     qb_dispatch<kQpU8, kQbMaxKB>(pl.KB, a, pl, static_cast<unsigned>(nblocks), stream);
   } else {
+    hipLaunchKernelGGL(qi32_filter_prep_kernel<kQpS5>, dim3(nfblk), dim3(256), 0, stream, w, frag, flags, g.Kg,
+                       g.R * g.S * g.Cg, kt64, pl.KB);
     qb_dispatch<kQpS5, kQbMaxKB>(pl.KB, a, pl, static_cast<unsigned>(nblocks), stream);
   }
   return hipGetLastError();
