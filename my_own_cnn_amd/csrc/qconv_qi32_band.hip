@@ -34,7 +34,7 @@
 // 147 KB per CU from L2 on C2 and took ~9 us of its 24.
 //
 // Staging.  Input codes come in 16-byte buffer loads of 4 codes into registers (the values
-// must be converted), 1 KB contiguous per wave instruction when C/groups == 64, 16 in flight
+// must be converted), 1 KB contiguous per wave instruction when C/groups == 64, 4 in flight
 // per lane; each lane writes its 4 converted values as one LDS word.  The compiler's own waits
 // order them (buffer loads are counted by vmcnt alone).  After a barrier the filter row sums and
 // the per-column channel sums are read back from LDS (v_dot4 against ones) and the filter is
@@ -185,7 +185,9 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
                 (a.H * a.W * a.C - gi * a.Cg) * 4);
   const int nie = a.ni > wave ? (a.ni - wave + kQbWaves - 1) / kQbWaves : 0;
   const int nj = max(4 * nie, 1);
-  constexpr int kD = 16;  // jobs in flight per lane
+  // jobs in flight per lane: the last pass repeats the last job's load up to kD - 1 times, which
+  // costs more than a deeper queue gains (C2: 4 in flight 14.5 us, 8: 15.1 us, 16: 16.5 us)
+  constexpr int kD = 4;
   v4f jv[kD];
   bool jok[kD];
   auto job_load = [&](int e, int slot) {
