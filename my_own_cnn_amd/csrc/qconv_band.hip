@@ -109,6 +109,12 @@ static_assert(sizeof(BandArgs) <= 256, "kernel arguments fit one s_load batch");
 template <int KB, int EPI, bool MT>
 __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_in) {
   const BandArgs a = preload_args(a_in);
+  // Channel order of the MFMA rows.  int8 outputs: row block j, row rho <-> channel
+  // 16 * (rho / 4) + 4j + rho % 4, so a lane holds 16 consecutive channels (one 16-byte
+  // store).  4-byte outputs: natural order (channel 16j + rho), so the 4 lanes of a pixel
+  // store 64 contiguous bytes per instruction; 16-byte pieces 64 bytes apart, as the int8
+  // order would give, ran the int32 output of C2 at 45.6 us against 7 us for int8.
+  constexpr bool NAT = EPI != kEpiI8;
   const int NT = MT ? a.NT : 1;
   const int WPT = MT ? a.WPT : kBandWaves;
   extern __shared__ v4i smem[];
@@ -196,12 +202,13 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
                    static_cast<unsigned>((k0 + 64 * t) * a.Kdim + 1024 * u));
       }
     } else {
-      const unsigned lane_row = static_cast<unsigned>((16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
+      const int rl = NAT ? row_l : 16 * (row_l >> 2) + (row_l & 3);
+      const unsigned lane_row = static_cast<unsigned>(rl * a.Kdim + 16 * grp_l);
       for (int f = wave; f < NT * 4 * KB; f += kBandWaves) {
         const int t = MT ? f / (4 * KB) : 0;
         const int ff = f - t * (4 * KB);
         load_lds16(rw, filt + f * 64, lane_row,
-                   static_cast<unsigned>((k0 + 64 * t + 4 * (ff & 3)) * a.Kdim + 64 * (ff >> 2)));
+                   static_cast<unsigned>((k0 + 64 * t + (NAT ? 16 : 4) * (ff & 3)) * a.Kdim + 64 * (ff >> 2)));
       }
     }
   }
@@ -228,12 +235,16 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   v4i A[KB][4];
   // lane (row_l, grp_l) of fragment (b, j), odd KB: channel n = 16 * (row_l / 4) + 4j +
   // row_l % 4 of the tile, 16-byte unit 4 * KB * n + 4b + grp_l, plus its block's shift
-  const v4i* ft = filt + tw * band_tile_slots(KB) + 4 * KB * (16 * (row_l >> 2) + (row_l & 3)) + grp_l +
-                  2 * (row_l >> 3);
+  // (natural order: channel n = 16j + row_l, unit 4 * KB * n + 4b + grp_l + 2 * (j / 2))
+  const v4i* ft = NAT ? filt + tw * band_tile_slots(KB) + 4 * KB * row_l + grp_l
+                      : filt + tw * band_tile_slots(KB) + 4 * KB * (16 * (row_l >> 2) + (row_l & 3)) + grp_l +
+                            2 * (row_l >> 3);
   auto read_A = [&](int b) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if constexpr (KB & 1)
+      if constexpr ((KB & 1) && NAT)
+        A[b][j] = ft[64 * KB * j + 2 * (j >> 1) + 4 * b];
+      else if constexpr (KB & 1)
         A[b][j] = ft[16 * KB * j + 4 * b];
       else
         A[b][j] = filt[(tw * 4 * KB + b * 4 + j) * 64 + lane];
@@ -243,9 +254,12 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   for (int b = 0; b < KB; ++b) read_A(b);
   wait_vmcnt(rest_loads);  // phase 0's rows and the epilogue parameters
   barrier_only();
-  // epilogue parameters of this lane's 16 channels kc0 + 4j + r (zero past Kg)
-  const int kc0 = k0 + 64 * tw + 16 * grp_l;
+  // epilogue parameters of this lane's 16 channels (zero past Kg): kc0 + 4j + r, or in
+  // natural order kt0 + 16j + 4 grp_l + r
+  const int kt0 = k0 + 64 * tw;
+  const int kc0 = kt0 + 16 * grp_l;
   const bool ch_ok = kc0 < a.Kg;  // Kg % 16 == 0: a lane's 16 channels all exist or none does
+  const int nj_ok = min(4, (a.Kg - kt0) >> 4);  // natural order: row blocks inside the group
   v4i bias_v[4];
   v4f mult_v[4];
 #pragma unroll
@@ -253,8 +267,9 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
     bias_v[j] = v4i{0, 0, 0, 0};
     mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (EPI != kEpiAcc32) {
-      bias_v[j] = ep[128 * tw + 4 * grp_l + j];
-      const v4i ws = ep[128 * tw + 64 + 4 * grp_l + j];
+      const int ev = NAT ? 4 * j + grp_l : 4 * grp_l + j;
+      bias_v[j] = ep[128 * tw + ev];
+      const v4i ws = ep[128 * tw + 64 + ev];
 #pragma unroll
       for (int r = 0; r < 4; ++r) mult_v[j][r] = requant_multiplier(a.act_scale, __int_as_float(ws[r]));
     }
@@ -284,7 +299,8 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
   const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + static_cast<size_t>(gi) * a.Kg;
   const __amdgpu_buffer_rsrc_t ry =
       make_rsrc(static_cast<char*>(a.y) + out0 * kOutBytes, band_rows * a.Wo * a.K * kOutBytes);
-  const unsigned lane_out = static_cast<unsigned>((row_l * a.K + kc0) * kOutBytes) + (ch_ok ? 0u : 0x40000000u);
+  const unsigned lane_out = NAT ? static_cast<unsigned>((row_l * a.K + kt0 + 4 * grp_l) * kOutBytes)
+                               : static_cast<unsigned>((row_l * a.K + kc0) * kOutBytes) + (ch_ok ? 0u : 0x40000000u);
   const int nseg = band_rows * a.SEGR;
   // The segment (row t, column seg_c) of the current phase, walked forward by WPT segments
   // per phase: its input offset seg_in (t * row_bytes + 1024 * seg_c), output soffset
@@ -319,6 +335,7 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        if (j >= nj_ok) break;  // natural order: channels 16j .. past the group
         v4i v = acc[j];
         if constexpr (EPI == kEpiF32) {
 #pragma unroll
@@ -328,7 +345,7 @@ __global__ void __launch_bounds__(64 * kBandWaves, 1) i8_band_kernel(BandArgs a_
             v[r] = __float_as_int(f);
           }
         }
-        __builtin_amdgcn_raw_buffer_store_b128(v, ry, lane_out_q + 16 * j, soff, kStoreAux);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, lane_out_q + 64 * j, soff, kStoreAux);
         store_gap(v);
       }
     }

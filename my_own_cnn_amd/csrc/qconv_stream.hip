@@ -30,8 +30,9 @@
 // barrier shows that every wave has read K-block b into its registers, so b's buffer then
 // receives K-block b + D.
 //
-// Output channels are permuted as in the other MFMA kernels (MFMA j row rho <-> channel
-// 16 * (rho / 4) + 4j + rho % 4), so each lane holds 16 consecutive channels of one pixel.
+// int8 outputs permute channels as in the other MFMA kernels (MFMA j row rho <-> channel
+// 16 * (rho / 4) + 4j + rho % 4), so each lane holds 16 consecutive channels of one pixel;
+// 4-byte outputs keep the natural order (channel 16j + rho).
 // Accumulators start at the bias; the epilogue is the shared int8 arithmetic and one
 // 16-byte non-temporal store per lane (four for int32 / fp32 outputs), each followed by
 // store_gap() on its data registers.
@@ -102,6 +103,10 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 template <int WK, int EPI, int D>
 __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamArgs a_in) {
   const StreamArgs a = preload_args(a_in);
+  // 4-byte outputs use natural channel order (MFMA row block j, row rho <-> channel 16j + rho),
+  // so the 4 lanes of a pixel store 64 contiguous bytes per instruction; int8 outputs keep 16
+  // consecutive channels per lane (one 16-byte store).
+  constexpr bool NAT = EPI != kEpiI8;
   constexpr int WP = kStreamWaves / WK;  // waves per 64-channel tile
   constexpr int LPW = WK / 2;            // filter loads per wave per K-block (4 * WK over 8 waves)
   extern __shared__ v4i st_lds[];
@@ -165,7 +170,8 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   // bytes [64b + 16 * grp_l, +16) of that channel's KRSC row (K-block b = tap * NQ + q covers
   // row bytes tap * Cg + 64q = 64b).
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + static_cast<size_t>(gi) * a.Kg * a.Kdim, a.Kg * a.Kdim);
-  const unsigned lane_row = static_cast<unsigned>((16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
+  const unsigned lane_row =
+      static_cast<unsigned>((NAT ? row_l : 16 * (row_l >> 2) + (row_l & 3)) * a.Kdim + 16 * grp_l);
   auto issue_filter = [&](int b, int slot) {  // K-block b into ring buffer `slot`
     v4i* buf = ring + slot * (4 * WK * 64);
 #pragma unroll
@@ -173,7 +179,7 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
       const int f = wave + kStreamWaves * u;
       const int t = f >> 2;
       const int j = f & 3;
-      load_lds16(rw, buf + f * 64, lane_row, static_cast<unsigned>((kwg0 + 64 * t + 4 * j) * a.Kdim + 64 * b));
+      load_lds16(rw, buf + f * 64, lane_row, static_cast<unsigned>((kwg0 + 64 * t + (NAT ? 16 : 4) * j) * a.Kdim + 64 * b));
     }
   };
   const int pre = min(D, a.KB);
@@ -187,7 +193,9 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   const int nseg_band = (rows * a.Wo + 15) >> 4;
   const int nsv = min(kStreamNseg, max(0, (nseg_band - wp + WP - 1) / WP));
   constexpr int kOutBytes = EPI == kEpiI8 ? 1 : 4;
-  const int kc0 = kwg0 + 64 * wk + 16 * grp_l;  // this lane's first output channel (in group gi)
+  // this lane's first output channel (in group gi): 16 consecutive ones, or in natural order
+  // channels kc0 + 16j + r
+  const int kc0 = kwg0 + 64 * wk + (NAT ? 4 : 16) * grp_l;
 #pragma unroll
   for (int i = 0; i < kStreamNseg; ++i) {
     const int p = 16 * (wp + i * WP) + row_l;
@@ -211,7 +219,7 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   }
   barrier_only();
 
-  // epilogue parameters of this lane's 16 channels kc0 + 4j + r
+  // epilogue parameters of this lane's 16 channels (kc0 + 4j + r, or kc0 + 16j + r)
   v4i bias_v[4];
   v4f mult_v[4];
 #pragma unroll
@@ -219,8 +227,9 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
     bias_v[j] = v4i{0, 0, 0, 0};
     mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (EPI != kEpiAcc32) {
-      bias_v[j] = ep[16 * wk + 4 * grp_l + j];
-      const v4i ws = ep[64 + 16 * wk + 4 * grp_l + j];
+      const int ev = NAT ? 4 * j + grp_l : 4 * grp_l + j;
+      bias_v[j] = ep[16 * wk + ev];
+      const v4i ws = ep[64 + 16 * wk + ev];
 #pragma unroll
       for (int r = 0; r < 4; ++r) mult_v[j][r] = requant_multiplier(a.act_scale, __int_as_float(ws[r]));
     }
@@ -341,7 +350,7 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
             v[r] = __float_as_int(f);
           }
         }
-        __builtin_amdgcn_raw_buffer_store_b128(v, ry, ovoff[i] + 16u * j, 0, kStoreAux);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, ovoff[i] + (NAT ? 64u : 16u) * j, 0, kStoreAux);
         store_gap(v);
       }
     }
