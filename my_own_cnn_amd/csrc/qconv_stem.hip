@@ -257,6 +257,10 @@ static_assert(sizeof(StemBandArgs) <= 256, "kernel arguments fit one s_load batc
 template <int KB, int EPI>
 __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBandArgs a_in) {
   const StemBandArgs a = preload_args(a_in);
+  // 4-byte outputs use natural channel order (MFMA row block j, row rho <-> channel 16j + rho),
+  // so the 4 lanes of a pixel store 64 contiguous bytes per instruction; int8 outputs keep 16
+  // consecutive channels per lane (one 16-byte store).
+  constexpr bool NAT = EPI != kEpiI8;
   extern __shared__ v4i sb_lds[];
   const unsigned char* bytes = reinterpret_cast<const unsigned char*>(sb_lds);
   v4i* filt = sb_lds + a.filt_lds / 16;
@@ -320,7 +324,7 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
     const int nvalid = q < a.NQ ? min(16, a.SC - 16 * h) : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int kl = 16 * (row_l >> 2) + 4 * j + (row_l & 3);
+      const int kl = NAT ? 16 * j + row_l : 16 * (row_l >> 2) + 4 * j + (row_l & 3);
       v4i v = lds_load16_unaligned(fbytes, kl * a.RSC + (nvalid > 0 ? r * a.SC + 16 * h : 0));
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
@@ -331,7 +335,8 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
       A[b][j] = v;
     }
   }
-  // epilogue parameters of this lane's 16 channels k0 + 16 * grp_l + 4j + r
+  // epilogue parameters of this lane's 16 channels k0 + 16 * grp_l + 4j + r (natural order:
+  // k0 + 16j + 4 * grp_l + r)
   v4i bias_v[4];
   v4f mult_v[4];
 #pragma unroll
@@ -339,8 +344,9 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
     bias_v[j] = v4i{0, 0, 0, 0};
     mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (EPI != kEpiAcc32) {
-      bias_v[j] = ep[4 * grp_l + j];
-      const v4i ws = ep[64 + 4 * grp_l + j];
+      const int ev = NAT ? 4 * j + grp_l : 4 * grp_l + j;
+      bias_v[j] = ep[ev];
+      const v4i ws = ep[64 + ev];
 #pragma unroll
       for (int r = 0; r < 4; ++r) mult_v[j][r] = requant_multiplier(a.act_scale, __int_as_float(ws[r]));
     }
@@ -397,7 +403,7 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
     base = window(sg + kSbWaves < nseg ? sg + kSbWaves : sg, t, wo);
     fetch(base);
     // a pixel past the row's end gets an offset 2^30 higher: past num_records, dropped
-    const unsigned voff = static_cast<unsigned>(((t_cur * a.Wo + wo_cur) * a.K + 16 * grp_l) * kOutBytes) +
+    const unsigned voff = static_cast<unsigned>(((t_cur * a.Wo + wo_cur) * a.K + (NAT ? 4 : 16) * grp_l) * kOutBytes) +
                           (static_cast<unsigned>(wo_cur >= a.Wo) << 30);
     v4i acc[4];
 #pragma unroll
@@ -422,7 +428,7 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
             v[r] = __float_as_int(f);
           }
         }
-        __builtin_amdgcn_raw_buffer_store_b128(v, ry, voff + 16 * j, 0, kStoreAux);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, voff + (NAT ? 64 : 16) * j, 0, kStoreAux);
         store_gap(v);
       }
     }
