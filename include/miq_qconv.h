@@ -179,15 +179,17 @@ int miq_block_fprop_nhwc_qi32_s5(const float* x, const float* w, int32_t* y,
  * miq_qparams_u8 structs (launch_fprop_nhwc_qi32_u8's), 1 miq_qparams_s5 structs; algo is
  * MIQ_ALGO_AUTO (what the entry points above run), MIQ_ALGO_BAND (row bands, 16-byte aligned
  * x, w and y, (c/groups) % 64 == 0, (k/groups) % 16 == 0, stride_w 1, output width <= 64,
- * r*s*c/groups <= 576), MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT.  Results are identical for every
- * choice.  No reference counterpart: it exists for tests and benchmarks. */
+ * r*s*c/groups <= 576), MIQ_ALGO_STREAM (the int8 stream kernel on a padded offset-int8 copy
+ * of the input: c/groups % 64 == 0, k/groups % 128 == 0, stride_w <= 4, 16-byte aligned
+ * tensors), MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT.  Results are identical for every choice.  No
+ * reference counterpart: it exists for tests and benchmarks. */
 int miq_fprop_nhwc_qi32_algo(int32_t qp_kind, const float* x, const float* w, int32_t* y,
                              int32_t n, int32_t h, int32_t wdt, int32_t c,
                              int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
                              const void* in_qp, const void* f_qp, int32_t algo, void* stream);
 
 /* The kernel the float-code entry points run for a plain-filter problem with 256-byte aligned
- * tensors: writes MIQ_ALGO_BAND, MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT to *algo.  No reference
+ * tensors: writes MIQ_ALGO_BAND, MIQ_ALGO_STREAM, MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT to *algo.  No reference
  * counterpart. */
 int miq_plan_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
                   const miq_conv2d_params* p, int32_t* algo);

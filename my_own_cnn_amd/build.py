@@ -37,6 +37,7 @@ SOURCES = [
     "grad_noalloc.hip",
     "qconv_qi32.hip",
     "qconv_qi32_band.hip",
+    "qconv_qi32_route.hip",
     "conv_quant_host.cpp",
     "verify.cpp",
     "bench.cpp",

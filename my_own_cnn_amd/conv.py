@@ -138,7 +138,7 @@ def launch_fprop_nhwc_qi32(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Point
              _stream(stream)), "launch_fprop_nhwc_qi32")
 
 
-QI32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2, "band": 4}
+QI32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2, "band": 4, "stream": 5}
 
 
 def fprop_nhwc_qi32_algo(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int,

@@ -192,10 +192,11 @@ int stream_workspace(hipStream_t s, size_t bytes, void** out) {
   return MIQ_OK;
 }
 
-// The kernel AUTO runs for a float-code problem: the row-band kernel, else the implicit GEMM,
-// else the direct kernel.
+// The kernel AUTO runs for a float-code problem: the row-band kernel, else the stream route,
+// else the implicit GEMM, else the direct kernel.
 int32_t qi32_auto(const miq::Geom& g, const miq::BlockGeom& bg, const void* x, const void* w, const void* y) {
   if (miq::qi32_band_eligible(g, bg, x, w, y, nullptr)) return MIQ_ALGO_BAND;
+  if (miq::qi32_route_eligible(g, bg, x, w, y, nullptr)) return MIQ_ALGO_STREAM;
   if (miq::qi32_igemm_eligible(g, bg, x, w, nullptr)) return MIQ_ALGO_IGEMM;
   return MIQ_ALGO_DIRECT;
 }
@@ -219,7 +220,11 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
     case MIQ_ALGO_BAND:
       if (!miq::qi32_band_eligible(g, bg, x, w, y, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       break;
-    default: return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM or BAND");
+    case MIQ_ALGO_STREAM:
+      if (!miq::qi32_route_eligible(g, bg, x, w, y, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      break;
+    default:
+      return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND or STREAM");
   }
   if (out_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
@@ -231,6 +236,14 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
       if (st != MIQ_OK) return st;
       e = miq::launch_qi32_band(g, bg, qk, x, w, y, in_qp, f_qp, ws, hs);
       if (e != hipSuccess) return hip_fail(e, "qi32 row-band launch");
+      return MIQ_OK;
+    }
+    case MIQ_ALGO_STREAM: {
+      void* ws = nullptr;
+      st = stream_workspace(hs, miq::qi32_route_workspace_bytes(g), &ws);
+      if (st != MIQ_OK) return st;
+      e = miq::launch_qi32_route(g, qk, x, w, y, in_qp, f_qp, ws, hs);
+      if (e != hipSuccess) return hip_fail(e, "qi32 stream route launch");
       return MIQ_OK;
     }
     case MIQ_ALGO_IGEMM:

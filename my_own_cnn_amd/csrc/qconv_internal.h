@@ -28,6 +28,7 @@ enum Epi : int {
   kEpiI8 = 0,     // requantized int8
   kEpiAcc32 = 1,  // raw int32 accumulators
   kEpiF32 = 2,    // dequantized fp32 view
+  kEpiQi32 = 3,   // int32 of the float-code route: offset codes' corrections added (stream kernel only)
 };
 
 // Requantization inputs; act_scale = in_scale / out_scale, computed on the host.
@@ -90,6 +91,16 @@ size_t qi32_band_workspace_bytes(const Geom& g);
 hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
                             const void* in_qp, const void* f_qp, void* ws, hipStream_t stream);
 
+// int32 accumulators on float codes through the int8 stream kernel (prepass to a padded
+// offset-int8 image and int8 filter in the workspace, the stream kernel with the offset
+// corrections, an exact direct pass only when a code leaves int8): plain filters on the shapes
+// the stream kernel takes after padding is folded into the image.
+bool qi32_route_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, const void* y,
+                         std::string* why);
+size_t qi32_route_workspace_bytes(const Geom& g);
+hipError_t launch_qi32_route(const Geom& g, QpKind qp, const float* x, const float* w, int32_t* y, const void* in_qp,
+                             const void* f_qp, void* ws, hipStream_t stream);
+
 // int8 VALU direct convolution: any geometry.
 hipError_t launch_i8_direct(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                             hipStream_t stream);
@@ -105,6 +116,13 @@ bool band_eligible(const Geom& g, const void* x, const void* w, const void* y, c
                    std::string* why);
 hipError_t launch_i8_band(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
+
+// The stream kernel on offset int8 codes (x' = code - o, w' = code - o) of a padded input (g has
+// no padding), int32 out:  y = sum x'w' + dx[n] * T[k] + Kdim * dx[n] * dw + dw * W(p), with
+// T[k] the sum of filter row k, W(p) the sum of the pixel's window, and qrec[4n .. 4n + 3] =
+// {dx[n], dw, Kdim * dx[n] * dw, 0} (mod 2^32).
+hipError_t launch_i8_stream_qi32(const Geom& g, const int8_t* x, const int8_t* w, const int32_t* T,
+                                 const int32_t* qrec, int32_t* y, hipStream_t stream);
 
 // int8 MFMA row-band kernel over virtual pixels (stride 1), filter in registers:
 // (C/groups) % 64 == 0, (K/groups) % 64 == 0, R*S*C/groups <= 576.

@@ -131,6 +131,7 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   const int ho0 = bi * a.RB;
   const int rows = min(a.RB, a.Ho - ho0);
 
+
   // ---- input rows: instruction i = ((hr * NQ + q) * sw + par) * NPB + pb to wave i % 8;
   // lane l reads parity-plane position 16 * pb + l % 16 (halo column * sw + par), chunk
   // 4q + l / 16.  Rows and columns outside the image get 2^30: past num_records.
@@ -155,12 +156,16 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
       load_lds16(rx, halo + hr * a.RowS + rem * 64, voff, soff);
     }
   }
-  // ---- bias (wave 0) and per-channel scales (wave 1) of the KT channels: 1 KB each ----
+  // ---- bias (wave 0) and per-channel scales (wave 1) of the KT channels: 1 KB each.
+  // kEpiQi32: the filter row sums T (in bias) and image n's 16-byte record {dx, dw,
+  // Kdim * dx * dw, 0} (in wscale) ----
   if (EPI != kEpiAcc32 && wave < 2) {
     const int valid = max(0, a.Kg - kwg0) * 4;
     const size_t off = static_cast<size_t>(gi) * a.Kg + kwg0;
     if (wave == 0) {
       load_lds16(make_rsrc(a.bias ? a.bias + off : nullptr, a.bias ? valid : 0), ep, 16u * lane, 0);
+    } else if constexpr (EPI == kEpiQi32) {
+      load_lds16(make_rsrc(a.wscale + 4 * static_cast<size_t>(n), 16), ep + 64, 16u * lane, 0);
     } else {
       load_lds16(make_rsrc(a.wscale + off, valid), ep + 64, 16u * lane, 0);
     }
@@ -226,7 +231,7 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   for (int j = 0; j < 4; ++j) {
     bias_v[j] = v4i{0, 0, 0, 0};
     mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (EPI != kEpiAcc32) {
+    if constexpr (EPI == kEpiI8 || EPI == kEpiF32) {
       const int ev = NAT ? 4 * j + grp_l : 4 * grp_l + j;
       bias_v[j] = ep[16 * wk + ev];
       const v4i ws = ep[64 + 16 * wk + ev];
@@ -234,17 +239,34 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
       for (int r = 0; r < 4; ++r) mult_v[j][r] = requant_multiplier(a.act_scale, __int_as_float(ws[r]));
     }
   }
+  // kEpiQi32: accumulators start at dx * T + Kdim * dx * dw; the epilogue adds dw * W(p)
+  unsigned qdw = 0;
+  if constexpr (EPI == kEpiQi32) {
+    const v4i rec = ep[64];
+    const unsigned dx = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(rec[0]));
+    qdw = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(rec[1]));
+    const unsigned c0 = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(rec[2]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4i tv = ep[16 * wk + 4 * j + grp_l];  // natural order: channels 16j + 4 grp_l + r
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bias_v[j][r] = static_cast<int>(dx * static_cast<unsigned>(tv[r]) + c0);
+    }
+  }
 
   // K-loop over K-blocks b = (r * S + s) * NQ + q (taps (r, s), chunk quads q), two per
   // pass so the fragment registers alternate without copies.  NS = the wave's segment
   // count (0 .. 4): a wave without segments still loads and synchronises.
   v4i acc[4][kStreamNseg];
+  int wsum[kStreamNseg];  // kEpiQi32: this lane's share of each segment pixel's window sum
   auto kloop = [&](auto ns_tag) {
     constexpr int NS = decltype(ns_tag)::value;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < kStreamNseg; ++i) acc[j][i] = bias_v[j];
+#pragma unroll
+    for (int i = 0; i < kStreamNseg; ++i) wsum[i] = 0;
     // tap and quad of the K-block whose fragments are read next, and each segment's slot
     // (quad 0) for that tap
     int q = 0, s = 0, tap_row = 0;  // tap_row = r * dh * RowS
@@ -286,6 +308,12 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
         for (int i = 0; i < NS; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j], B[i], acc[j][i], 0, 0, 0);
+        if constexpr (EPI == kEpiQi32) {
+#pragma unroll
+          for (int i = 0; i < NS; ++i)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) wsum[i] = __builtin_amdgcn_sdot4(B[i][d], 0x01010101, wsum[i], false);
+        }
       }
     };
     // step b: K-block b's fragments are in registers; publish b + 1, refill b's buffer
@@ -334,7 +362,21 @@ __global__ void __launch_bounds__(64 * kStreamWaves, 1) i8_stream_kernel(StreamA
   for (int i = 0; i < kStreamNseg; ++i) {
     if (i >= nsv) break;
     v4i v4[4] = {acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
-    if constexpr (EPI == kEpiI8) {
+    if constexpr (EPI == kEpiQi32) {
+      // the pixel's window sum: the 4 lanes of its row each summed their 16 channels of every K-block
+      int ws = wsum[i];
+      ws += __shfl_xor(ws, 16);
+      ws += __shfl_xor(ws, 32);
+      const unsigned corr = qdw * static_cast<unsigned>(ws);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v4i v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = static_cast<int>(static_cast<unsigned>(v4[j][r]) + corr);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, ovoff[i] + 64u * j, 0, kStoreAux);
+        store_gap(v);
+      }
+    } else if constexpr (EPI == kEpiI8) {
       const v4i pk = a.relu ? pack_u8_relu(v4, mult_v) : pack_i8(v4, mult_v, lo);
       __builtin_amdgcn_raw_buffer_store_b128(pk, ry, ovoff[i], 0, kStoreAux);
       store_gap(pk);
@@ -466,6 +508,7 @@ void stream_launch(const StreamArgs& a, const StreamPlan& pl, Epi epi, unsigned 
   switch (epi) {
     case kEpiI8: go(i8_stream_kernel<WK, kEpiI8, D>); break;
     case kEpiAcc32: go(i8_stream_kernel<WK, kEpiAcc32, D>); break;
+    case kEpiQi32: go(i8_stream_kernel<WK, kEpiQi32, D>); break;
     default: go(i8_stream_kernel<WK, kEpiF32, D>); break;
   }
 }
@@ -495,8 +538,10 @@ bool stream_eligible(const Geom& g, const void* x, const void* w, const void* y,
   return stream_plan(g, epi, &pl, why);
 }
 
-hipError_t launch_i8_stream(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
-                            hipStream_t stream) {
+namespace {
+
+hipError_t launch_stream_any(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                             hipStream_t stream) {
   if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
   StreamPlan pl;
   if (!stream_plan(g, epi, &pl, nullptr)) return hipErrorInvalidConfiguration;
@@ -525,6 +570,19 @@ hipError_t launch_i8_stream(const Geom& g, Epi epi, const int8_t* x, const int8_
     stream_launch_d<2>(a, pl, epi, static_cast<unsigned>(nblocks), stream);
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_i8_stream(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                            hipStream_t stream) {
+  return launch_stream_any(g, epi, x, w, y, rq, stream);
+}
+
+hipError_t launch_i8_stream_qi32(const Geom& g, const int8_t* x, const int8_t* w, const int32_t* T,
+                                 const int32_t* qrec, int32_t* y, hipStream_t stream) {
+  const Requant rq{T, reinterpret_cast<const float*>(qrec), 1.0f, 0};
+  return launch_stream_any(g, kEpiQi32, x, w, y, rq, stream);
 }
 
 }  // namespace miq
