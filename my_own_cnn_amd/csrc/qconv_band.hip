@@ -46,7 +46,10 @@
 //
 // Skew.  The two waves of a SIMD (w and w + 4) are offset by one epilogue: the leading
 // wave runs MFMA(p) then epilogue(p), the trailing one epilogue(p - 1) then MFMA(p), so one
-// wave's VALU work runs beside the other's matrix instructions.
+// wave's VALU work runs beside the other's matrix instructions.  The wait for the remaining
+// rows after phase 0 realigns them (both then run epilogue 0, MFMA 1, ...); the trailing
+// wave taking MFMA(p) first keeps them apart, but measured slower in graph replay
+// (C2 7.27 -> 7.41 us).
 //
 // Epilogue.  Accumulators start at the bias; the output is convert, scale, clamp, round
 // (the 1.5*2^23 addition; with ReLU, v_cvt_pk_u8_f32 rounds to nearest even and packs) and
