@@ -98,18 +98,29 @@ __device__ __forceinline__ v4i lds_read16(unsigned addr) {
 }
 
 // int8 output of one lane: channels kc0 .. kc0 + 15 of one pixel, accumulators biased.
+// Each value is clamped, then rounded to nearest even by adding 1.5 * 2^23, which leaves
+// rint(v) in two's complement in the low mantissa bits; an SDWA v_add_f32 writes the low
+// byte of that sum straight into byte r of the packed word (dst_sel BYTE_r, the other bytes
+// preserved), so no v_perm_b32 / v_or_b32 packing is needed (12 fewer VALU operations per
+// 16 values).
 __device__ __forceinline__ v4i pack_i8(const v4i (&acc)[4], const v4f (&mult)[4], float lo) {
+  const float magic = 12582912.0f;
   v4i pk;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    unsigned u[4];
+    float c[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = static_cast<float>(acc[j][r]) * mult[j][r];
-      u[r] = __float_as_uint(__builtin_amdgcn_fmed3f(v, lo, 127.0f) + 12582912.0f);
-    }
-    pk[j] = static_cast<int>(__builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u) |
-                             __builtin_amdgcn_perm(u[3], u[2], 0x04000c0cu));
+    for (int r = 0; r < 4; ++r) c[r] = __builtin_amdgcn_fmed3f(static_cast<float>(acc[j][r]) * mult[j][r], lo, 127.0f);
+    unsigned u;
+    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
+        : "=v"(u) : "v"(c[0]), "v"(magic));
+    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+        : "+v"(u) : "v"(c[1]), "v"(magic));
+    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+        : "+v"(u) : "v"(c[2]), "v"(magic));
+    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
+        : "+v"(u) : "v"(c[3]), "v"(magic));
+    pk[j] = static_cast<int>(u);
   }
   return pk;
 }
