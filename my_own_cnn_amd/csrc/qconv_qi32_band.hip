@@ -501,8 +501,9 @@ bool qb_plan(const Geom& g, const BlockGeom& bg, Qi32BandPlan* p, std::string* w
   const int kt64 = (g.Kg + 63) / 64;
   const int cus = qb_cu_count();
   // Cost in cycles of one round of workgroups (one per CU): the two waves of the busiest
-  // SIMD run KB * 4 MFMAs plus an epilogue per phase; staging reads every float code once
-  // (about 25 bytes a cycle per CU) and converts it.
+  // SIMD run KB * 4 MFMAs plus an epilogue per phase; the loads are the filter's int8
+  // fragments from the prepass and every float code of the band's rows (about 25 bytes a
+  // cycle per CU).
   bool found = false;
   double best = 0.0;
   for (int nt = 1; nt <= kQbWaves; nt *= 2) {
@@ -519,7 +520,7 @@ bool qb_plan(const Geom& g, const BlockGeom& bg, Qi32BandPlan* p, std::string* w
       const long long rounds = (wgs + cus - 1) / cus;
       const long long nph = (static_cast<long long>(bh) * p->SEGR + wpt - 1) / wpt;
       const double phase = p->KB * 64.0 + 600.0;
-      const double load = 3000.0 + static_cast<double>(nt * 64LL * p->KB * 64 * 4 + ni * 4096) / 25.0;
+      const double load = 3000.0 + static_cast<double>(nt * 4096LL * p->KB + ni * 4096) / 25.0;
       const double cost = static_cast<double>(rounds) * (2.0 * static_cast<double>(nph) * phase + load);
       if (!found || cost < best - 1e-9) {
         found = true;
