@@ -326,10 +326,11 @@ int miq_block_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t 
 
 /* Kernel families of the fp32 passes (miq_plan_f32). */
 typedef enum miq_f32_kernel {
-  MIQ_F32_DIRECT = 0,          /* one thread per output element, the reference CPU loop's order */
+  MIQ_F32_DIRECT = 0,          /* the reference CPU loop's order, one thread per output element (dx: per 4
+                                  channels when (c/groups) % 4 == 0 and dx, w are 16-byte aligned) */
   MIQ_F32_IGEMM = 1,           /* fp32 MFMA implicit GEMM, 128 pixels x 64 channels per workgroup */
   MIQ_F32_IGEMM32 = 2,         /* the same with 256 pixels x 32 channels (groups of <= 32 channels) */
-  MIQ_F32_DEPTHWISE = 3,       /* depthwise fprop, 4 channels per thread */
+  MIQ_F32_DEPTHWISE = 3,       /* depthwise fprop or dx, 4 channels per thread */
   MIQ_F32_BPROP_IGEMM = 4,     /* stride-1 dx as the forward implicit GEMM over dy */
   MIQ_F32_GRAD_IGEMM = 5,      /* dw as a GEMM over pixels split across workgroups */
   MIQ_F32_GRAD_DEPTHWISE = 6   /* depthwise dw, pixel runs per thread */

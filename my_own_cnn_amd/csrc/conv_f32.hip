@@ -690,6 +690,96 @@ __global__ void __launch_bounds__(kDirectThreads) f32_bprop_direct_kernel(const 
   dx[e] = acc;
 }
 
+// The same dx with 4 consecutive input channels per thread ((C/groups) % 4 == 0, dx and the
+// filter 16-byte aligned): per output channel one float4 of the filter (KRSC rows are
+// ci-contiguous) and one dy value shared by the 4 sums.  Each channel's sum keeps the (r, s, ko)
+// order of cpu_bprop_nhwc with one multiply and one add per term, so dx is the direct kernel's
+// bit for bit; the loads per multiply-add drop from 2 to 1/2.
+__global__ void __launch_bounds__(kDirectThreads) f32_bprop_direct4_kernel(const float* __restrict__ dy,
+                                                                           const float* __restrict__ w,
+                                                                           float* __restrict__ dx, Geom g,
+                                                                           BlockGeom bg, long long total, Split3 sp) {
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;
+  int c4, wi, hi, n;
+  sp.apply(e, total < (1LL << 31), c4, wi, hi, n);
+  const int c = 4 * c4;
+  const int grp = c / g.Cg;
+  const int ci = c - grp * g.Cg;
+  const size_t tstride = static_cast<size_t>(g.R) * g.S * g.Cg;    // between filter blocks
+  const size_t wstride = tstride * bg.By * bg.Bx;                 // between output channels
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < g.R; ++r) {
+    const int hn = hi + g.ph - r * g.dh;
+    if (hn < 0 || hn % g.sh != 0) continue;
+    const int ho = hn / g.sh;
+    if (ho >= g.Ho) continue;
+    for (int s = 0; s < g.S; ++s) {
+      const int wn = wi + g.pw - s * g.dw;
+      if (wn < 0 || wn % g.sw != 0) continue;
+      const int wo = wn / g.sw;
+      if (wo >= g.Wo) continue;
+      const float* dyp = dy + ((static_cast<size_t>(n) * g.Ho + ho) * g.Wo + wo) * g.K + static_cast<size_t>(grp) * g.Kg;
+      const int blk = (ho / bg.bho) * bg.Bx + wo / bg.bwo;
+      const float* wp = w + static_cast<size_t>(grp) * g.Kg * wstride + blk * tstride +
+                        (static_cast<size_t>(r) * g.S + s) * g.Cg + ci;
+      for (int ko = 0; ko < g.Kg; ++ko) {
+        const float d = dyp[ko];
+        const v4f wv = *reinterpret_cast<const v4f*>(wp + ko * wstride);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(d, wv[j]));
+      }
+    }
+  }
+  *reinterpret_cast<v4f*>(dx + 4 * e) = acc;
+  store_gap(acc);
+}
+
+// Depthwise dx (C/groups == K/groups == 1, C % 4 == 0, plain filter): one thread per input
+// pixel and 4 consecutive channels, the filter staged in LDS as [tap][channel] as in
+// f32_depthwise_kernel, one float4 of dy per tap.  Channel c's sum runs over the taps (r, s)
+// whose output position is whole and in range, in cpu_bprop_nhwc's order with its single
+// output channel: dx is the direct kernel's bit for bit, at any stride.
+__global__ void __launch_bounds__(kDirectThreads) f32_depthwise_bprop_kernel(const float* __restrict__ dy,
+                                                                             const float* __restrict__ w,
+                                                                             float* __restrict__ dx, Geom g,
+                                                                             long long total, Split3 sp) {
+  __shared__ v4f wl[kDwLdsFloats / 4];
+  const int taps = g.R * g.S;
+  float* wf = reinterpret_cast<float*>(wl);
+  for (int i = threadIdx.x; i < taps * g.C; i += kDirectThreads) {  // w[c][t] -> wl[t][c]
+    const int c = i / taps;
+    const int t = i - c * taps;
+    wf[t * g.C + c] = w[i];
+  }
+  __syncthreads();
+  const long long e = static_cast<long long>(blockIdx.x) * kDirectThreads + threadIdx.x;
+  if (e >= total) return;  // after the only barrier
+  int c4, wi, hi, n;
+  sp.apply(e, total < (1LL << 31), c4, wi, hi, n);
+  const int c = 4 * c4;
+  const float* dyn = dy + static_cast<size_t>(n) * g.Ho * g.Wo * g.K + c;
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < g.R; ++r) {
+    const int hn = hi + g.ph - r * g.dh;
+    if (hn < 0 || hn % g.sh != 0) continue;
+    const int ho = hn / g.sh;
+    if (ho >= g.Ho) continue;
+    for (int s = 0; s < g.S; ++s) {
+      const int wn = wi + g.pw - s * g.dw;
+      if (wn < 0 || wn % g.sw != 0) continue;
+      const int wo = wn / g.sw;
+      if (wo >= g.Wo) continue;
+      const v4f dv = *reinterpret_cast<const v4f*>(dyn + (static_cast<size_t>(ho) * g.Wo + wo) * g.K);
+      const v4f wv = wl[((r * g.S + s) * g.C + c) >> 2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __fadd_rn(acc[j], __fmul_rn(dv[j], wv[j]));
+    }
+  }
+  *reinterpret_cast<v4f*>(dx + 4 * e) = acc;
+  store_gap(acc);
+}
+
 // dw of the convolution, the reference's cpu_grad_nhwc order (cpu_ref.cpp:192-230): one thread
 // per dw[k][r][s][ci] element, acc += x * dy over n, ho, wo in that order (in-bounds taps).
 // With a blocked filter, per dw[k][by][bx][r][s][ci] element over n and the block's positions,
@@ -1111,8 +1201,35 @@ hipError_t launch_f32_depthwise(const Geom& g, const float* x, const float* w, f
   return hipGetLastError();
 }
 
+bool f32_bprop_direct4_eligible(const Geom& g, const void* w, const void* dx) {
+  return g.Cg % 4 == 0 && g.Cg > 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+         (reinterpret_cast<uintptr_t>(dx) & 15u) == 0;
+}
+
+bool f32_depthwise_bprop_eligible(const Geom& g, const void* dy, const void* dx) {
+  return g.Cg == 1 && g.Kg == 1 && g.C % 4 == 0 && g.C > 0 && static_cast<long long>(g.R) * g.S * g.C <= kDwLdsFloats &&
+         (reinterpret_cast<uintptr_t>(dy) & 15u) == 0 && (reinterpret_cast<uintptr_t>(dx) & 15u) == 0;
+}
+
+hipError_t launch_f32_depthwise_bprop(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream) {
+  const long long total = static_cast<long long>(g.N) * g.H * g.W * (g.C / 4);
+  if (total == 0) return hipSuccess;
+  const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;
+  hipLaunchKernelGGL(f32_depthwise_bprop_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kDirectThreads), 0, stream,
+                     dy, w, dx, g, total, make_split3(g.C / 4, g.W, g.H));
+  return hipGetLastError();
+}
+
 hipError_t launch_f32_bprop_direct(const Geom& g, const BlockGeom& bg, const float* dy, const float* w, float* dx,
                                    hipStream_t stream) {
+  if (f32_bprop_direct4_eligible(g, w, dx)) {
+    const long long quads = static_cast<long long>(g.N) * g.H * g.W * (g.C / 4);
+    if (quads == 0) return hipSuccess;
+    const long long qblocks = (quads + kDirectThreads - 1) / kDirectThreads;
+    hipLaunchKernelGGL(f32_bprop_direct4_kernel, dim3(static_cast<unsigned>(qblocks)), dim3(kDirectThreads), 0, stream,
+                       dy, w, dx, g, bg, quads, make_split3(g.C / 4, g.W, g.H));
+    return hipGetLastError();
+  }
   const long long total = static_cast<long long>(g.N) * g.H * g.W * g.C;
   if (total == 0) return hipSuccess;
   const long long blocks = (total + kDirectThreads - 1) / kDirectThreads;

@@ -140,8 +140,11 @@ int bprop_f32(const miq::Geom& g, const miq::BlockGeom& bg, const float* dy, con
   }
   if (in_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const bool dense = bg.By == 1 && bg.Bx == 1;
   const hipError_t e = igemm ? miq::launch_f32_bprop_igemm(g, bg, dy, w, dx, hs)
-                             : miq::launch_f32_bprop_direct(g, bg, dy, w, dx, hs);
+                       : algo == MIQ_ALGO_AUTO && dense && miq::f32_depthwise_bprop_eligible(g, dy, dx)
+                           ? miq::launch_f32_depthwise_bprop(g, dy, w, dx, hs)
+                           : miq::launch_f32_bprop_direct(g, bg, dy, w, dx, hs);
   if (e != hipSuccess) return hip_fail(e, "fp32 bprop launch");
   return MIQ_OK;
 }
@@ -651,7 +654,9 @@ int plan_f32(int32_t op, const miq::Geom& g, const miq::BlockGeom& bg, int32_t a
     case 1:  // bprop: the order of bprop_f32
       switch (algo) {
         case MIQ_ALGO_AUTO:
-          *kernel = miq::f32_bprop_igemm_eligible(g, bg, al, al, nullptr) ? MIQ_F32_BPROP_IGEMM : MIQ_F32_DIRECT;
+          *kernel = miq::f32_bprop_igemm_eligible(g, bg, al, al, nullptr)            ? MIQ_F32_BPROP_IGEMM
+                    : dense && miq::f32_depthwise_bprop_eligible(g, al, al) ? MIQ_F32_DEPTHWISE
+                                                                             : MIQ_F32_DIRECT;
           return MIQ_OK;
         case MIQ_ALGO_DIRECT: *kernel = MIQ_F32_DIRECT; return MIQ_OK;
         case MIQ_ALGO_IGEMM:

@@ -167,6 +167,8 @@ hipError_t launch_f32_direct(const Geom& g, const BlockGeom& bg, const float* x,
 bool f32_depthwise_eligible(const Geom& g, const void* x, const void* y);
 hipError_t launch_f32_depthwise(const Geom& g, const float* x, const float* w, float* y, hipStream_t stream);
 // fp32 dx and dw in the reference CPU loop orders (one thread per output element).
+bool f32_depthwise_bprop_eligible(const Geom& g, const void* dy, const void* dx);
+hipError_t launch_f32_depthwise_bprop(const Geom& g, const float* dy, const float* w, float* dx, hipStream_t stream);
 hipError_t launch_f32_bprop_direct(const Geom& g, const BlockGeom& bg, const float* dy, const float* w, float* dx,
                                    hipStream_t stream);
 // fp32 dx of a stride-1 convolution on the MFMA implicit GEMM (the forward kernel over dy with

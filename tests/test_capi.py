@@ -327,7 +327,9 @@ def test_plan_f32_names_the_kernel_each_pass_runs():
     assert M.plan_f32("fprop", *r50, dw) == "depthwise"
     assert M.plan_f32("fprop", *r50, algo="direct") == "direct"
     assert M.plan_f32("bprop", *r50) == "bprop_igemm"
-    assert M.plan_f32("bprop", *r50, dw) == "direct"
+    assert M.plan_f32("bprop", *r50, dw) == "depthwise"
+    assert M.plan_f32("bprop", *r50, dw, algo="direct") == "direct"
+    assert M.plan_f32("bprop", 8, 28, 28, 32, 3, 3, 32, _capi.Conv2DParams(1, 1, 2, 2, 1, 1, 1)) == "direct"
     assert M.plan_f32("grad", *r50) == "grad_igemm"
     assert M.plan_f32("grad", *r50, dw) == "grad_depthwise"
     assert M.plan_f32("grad", *r50, algo="direct") == "direct"

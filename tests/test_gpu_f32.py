@@ -136,6 +136,50 @@ def test_fp32_bprop_and_grad_bit_exact(device, case):
     assert oracle.verify_tensors(want_dw, got, 1e-4, 1e-3), float(np.abs(got - want_dw).max())
 
 
+DW_BPROP = [
+    ("dw_s1", 2, 13, 11, 24, 24, 3, 3, (1, 1, 1, 1, 1, 1, 24)),
+    ("dw_s2_d2", 2, 15, 13, 36, 36, 3, 5, (2, 3, 2, 1, 2, 1, 36)),
+    ("dw_s3_pad0", 1, 17, 16, 8, 8, 5, 3, (0, 1, 3, 2, 1, 1, 8)),
+]
+
+
+@pytest.mark.parametrize("case", DW_BPROP, ids=[c[0] for c in DW_BPROP])
+def test_fp32_depthwise_bprop_bit_exact(device, case):
+    # AUTO's depthwise dx kernel keeps cpu_bprop_nhwc's tap order: bit-exact at any stride
+    _, n, h, w, c, k, r, s, conv = case
+    x, wt = _data(case, 900 + DW_BPROP.index(case))
+    ho, wo = oracle.conv_output_shape(n, h, w, c, r, s, k, conv)
+    dy = np.random.default_rng(950 + DW_BPROP.index(case)).uniform(-1, 1, size=(n, ho, wo, k)).astype(np.float32)
+    p = M.Conv2DParams(*conv)
+    assert M.plan_f32("bprop", n, h, w, c, r, s, k, p) == "depthwise"
+    wd, dyd = torch.from_numpy(wt).to(device), torch.from_numpy(dy).to(device)
+    dx = torch.full(x.shape, 7.0, dtype=torch.float32, device=device)
+    M.launch_bprop_nhwc(dyd, wd, dx, n, h, w, c, r, s, k, conv)
+    torch.cuda.synchronize()
+    want = oracle.bprop_f32(dy, wt, x.shape, conv)
+    np.testing.assert_array_equal(dx.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_fp32_direct_bprop_four_channels_and_unaligned(device):
+    # (c/groups) % 4 == 0 with aligned dx and filter: 4 channels per thread; an unaligned dx takes
+    # the one-element kernel; both give cpu_bprop_nhwc's bits (stride 2, groups 2, K not a multiple of 4)
+    case = ("s2_g2", 2, 19, 17, 16, 18, 3, 3, (1, 1, 2, 2, 1, 1, 2))
+    _, n, h, w, c, k, r, s, conv = case
+    x, wt = _data(case, 990)
+    ho, wo = oracle.conv_output_shape(n, h, w, c, r, s, k, conv)
+    dy = np.random.default_rng(991).uniform(-1, 1, size=(n, ho, wo, k)).astype(np.float32)
+    want = oracle.bprop_f32(dy, wt, x.shape, conv)
+    wd, dyd = torch.from_numpy(wt).to(device), torch.from_numpy(dy).to(device)
+    dx = torch.full(x.shape, 7.0, dtype=torch.float32, device=device)
+    M.launch_bprop_nhwc(dyd, wd, dx, n, h, w, c, r, s, k, conv, algo="direct")
+    buf = torch.full((x.size + 1,), 7.0, dtype=torch.float32, device=device)
+    M.launch_bprop_nhwc(dyd, wd, buf[1:], n, h, w, c, r, s, k, conv, algo="direct")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dx.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(buf[1:].cpu().numpy().reshape(want.shape).view(np.uint32), want.view(np.uint32))
+    assert float(buf[0]) == 7.0
+
+
 def test_fp32_bprop_igemm_applies_at_stride_1_only(device):
     x, wt = _data(SUITE[0], 9)
     conv = SUITE[0][8]
