@@ -247,6 +247,7 @@ struct StemBandArgs {
   int HR;                // staged input rows per band
   int nfilt;             // filter load instructions
   int filt_lds, ep_lds, halo_lds;  // LDS byte offsets
+  int slot_lds;          // LDS byte offset of the filter's 16-byte operand slots (16 KB)
   float act_scale;
   int relu;
   FastDivM fd_nbands, fd_bpi, fd_segr, fd_rowsld;
@@ -312,27 +313,40 @@ __global__ void __launch_bounds__(64 * kSbWaves, 1) i8_stem_band_kernel(StemBand
   barrier_only();
 
   // ---- filter fragments: lane (row_l, grp_l) of fragment (b, j) holds channel
-  // 16*(row_l/4) + 4j + row_l%4 of the tile, chunk q = 4b + grp_l (filter row q / CPR,
-  // bytes 16 * (q % CPR) .. of its SC-byte slot; bytes past SC and chunks past NQ are 0).
-  v4i A[KB][4];
+  // 16*(row_l/4) + 4j + row_l%4 of the tile (natural order: 16j + row_l), chunk q = 4b + grp_l
+  // (filter row q / CPR, bytes 16 * (q % CPR) .. of its SC-byte slot; bytes past SC and
+  // chunks past NQ are 0).  The workgroup assembles each (channel, chunk) operand once from
+  // the contiguous filter bytes into 16-byte slots, channel kl's chunk q at slot
+  // 16 kl + ((q + kl + 4 (kl / 16)) mod 16): the 16 lanes of a lane group then read 16
+  // distinct slots modulo 16 in either channel order.  Every wave then reads its fragments
+  // with 16-byte LDS reads (assembled per wave instead, from five dwords and a funnel shift
+  // each, the register copy took about 1 us on C5).
   const unsigned char* fbytes = bytes + a.filt_lds;
-#pragma unroll
-  for (int b = 0; b < KB; ++b) {
-    const int q = 4 * b + grp_l;
+  v4i* slots = sb_lds + a.slot_lds / 16;
+  auto slot_of = [](int kl, int q) { return 16 * kl + ((q + kl + 4 * (kl >> 4)) & 15); };
+  for (int idx = threadIdx.x; idx < 64 * 4 * KB; idx += 64 * kSbWaves) {
+    const int kl = idx / (4 * KB);
+    const int q = idx - kl * (4 * KB);
     const int r = a.CPR == 2 ? (q >> 1) : q;
     const int h = q - r * a.CPR;
     const int nvalid = q < a.NQ ? min(16, a.SC - 16 * h) : 0;
+    v4i v = lds_load16_unaligned(fbytes, kl * a.RSC + (nvalid > 0 ? r * a.SC + 16 * h : 0));
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int keep = min(4, max(0, nvalid - 4 * d));
+      const unsigned msk = keep >= 4 ? 0xffffffffu : ((1u << (8 * keep)) - 1u);
+      v[d] = static_cast<int>(static_cast<unsigned>(v[d]) & msk);
+    }
+    slots[slot_of(kl, q)] = v;
+  }
+  __syncthreads();
+  v4i A[KB][4];
+#pragma unroll
+  for (int b = 0; b < KB; ++b) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kl = NAT ? 16 * j + row_l : 16 * (row_l >> 2) + 4 * j + (row_l & 3);
-      v4i v = lds_load16_unaligned(fbytes, kl * a.RSC + (nvalid > 0 ? r * a.SC + 16 * h : 0));
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int keep = min(4, max(0, nvalid - 4 * d));
-        const unsigned msk = keep >= 4 ? 0xffffffffu : ((1u << (8 * keep)) - 1u);
-        v[d] = static_cast<int>(static_cast<unsigned>(v[d]) & msk);
-      }
-      A[b][j] = v;
+      A[b][j] = slots[slot_of(kl, 4 * b + grp_l)];
     }
   }
   // epilogue parameters of this lane's 16 channels k0 + 16 * grp_l + 4j + r (natural order:
@@ -477,8 +491,9 @@ bool make_band_plan(const Geom& g, StemBandPlan* pl) {
   pl->nfilt = static_cast<int>((64 * RSC + 20 + 1023) / 1024);  // + the loader's over-read
   const int segr = (g.Wo + 15) / 16;
   const int cus = sb_cu_count();
-  // filter, then 2 KB for bias and scales (each of their two loads writes all 64 lanes)
-  const size_t fixed = static_cast<size_t>(pl->nfilt) * 1024 + 2048;
+  // filter, then 2 KB for bias and scales (each of their two loads writes all 64 lanes) and
+  // 16 KB of filter operand slots (64 channels x 16 chunks)
+  const size_t fixed = static_cast<size_t>(pl->nfilt) * 1024 + 2048 + 16384;
   bool found = false;
   double best = 0.0;
   for (int bh = 1; bh <= g.Ho; ++bh) {
@@ -498,7 +513,7 @@ bool make_band_plan(const Geom& g, StemBandPlan* pl) {
       pl->HR = static_cast<int>(hr);
       pl->filt_lds = 0;
       pl->ep_lds = pl->nfilt * 1024;
-      pl->halo_lds = pl->ep_lds + 2048;
+      pl->halo_lds = pl->ep_lds + 2048 + 16384;
       pl->lds = lds;
     }
   }
@@ -534,7 +549,7 @@ hipError_t launch_stem_band(const Geom& g, Epi epi, const int8_t* x, const int8_
   a.nblocks = a.nbands * (g.K / 64);
   a.SEGR = (g.Wo + 15) / 16;
   a.P = pl.P; a.PLB = pl.PLB; a.rows_ld = pl.rows_ld; a.HR = pl.HR; a.nfilt = pl.nfilt;
-  a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.halo_lds = pl.halo_lds;
+  a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.halo_lds = pl.halo_lds; a.slot_lds = pl.ep_lds + 2048;
   a.act_scale = rq.act_scale; a.relu = rq.relu;
   a.fd_nbands = fastdiv_m(a.nbands);
   a.fd_bpi = fastdiv_m(pl.bands_per_img);
