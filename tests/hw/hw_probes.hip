@@ -307,8 +307,10 @@ void probe_lds(hipStream_t st) {
 // ---------------------------------------------------------------- mfma
 // NACC independent accumulator chains of one MFMA shape per wave; NV VALU ops (v_mul_f32 on 8
 // registers) and ND ds_read_b128 (feeding the next iteration's B operand) per MFMA group.
+// Thread 0 of each workgroup records the shader clock counter (s_memtime) and the 100 MHz
+// counter (s_memrealtime) around the loop: clk[4 * block + 0..3] = {t0, r0, t1, r1}.
 template <int SHAPE, int NACC, int NV, int ND>
-__global__ void __launch_bounds__(512) mfma_kernel(int iters, int* out) {
+__global__ void __launch_bounds__(512) mfma_kernel(int iters, int* out, long long* clk) {
   extern __shared__ v4i lds[];
   const int lane = threadIdx.x & 63;
   for (int i = threadIdx.x; i < 2048; i += blockDim.x) lds[i] = v4i{i, i + 1, i + 2, i + 3};
@@ -346,9 +348,22 @@ __global__ void __launch_bounds__(512) mfma_kernel(int iters, int* out) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) f[v & 7] *= m;
   };
+  long long t0 = 0, r0 = 0;
+  if (threadIdx.x == 0) {
+    t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
   for (int i = 0; i < iters; i += 2) {
     group(B0, i);
     group(B1, i + 1);
+  }
+  if (threadIdx.x == 0) {
+    const long long t1 = __builtin_amdgcn_s_memtime();
+    const long long r1 = __builtin_amdgcn_s_memrealtime();
+    clk[4 * blockIdx.x + 0] = t0;
+    clk[4 * blockIdx.x + 1] = r0;
+    clk[4 * blockIdx.x + 2] = t1;
+    clk[4 * blockIdx.x + 3] = r1;
   }
   int s = 0;
   for (int j = 0; j < NACC; ++j) s += acc[j][0] + acc[j][1];
@@ -358,43 +373,58 @@ __global__ void __launch_bounds__(512) mfma_kernel(int iters, int* out) {
 }
 
 template <int SHAPE, int NACC, int NV, int ND>
-void run_mfma(int waves_per_simd, int* out, hipStream_t st) {
+void run_mfma(int waves_per_simd, int* out, long long* clk, hipStream_t st) {
   const int iters = 20000;
   const int lds_bytes = 96 * 1024;  // one workgroup per CU
   auto k = mfma_kernel<SHAPE, NACC, NV, ND>;
   CK(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes));
   const float us =
-      time_us([&] { hipLaunchKernelGGL(k, dim3(kCUs), dim3(256 * waves_per_simd), lds_bytes, st, iters, out); }, 3,
+      time_us([&] { hipLaunchKernelGGL(k, dim3(kCUs), dim3(256 * waves_per_simd), lds_bytes, st, iters, out, clk); }, 3,
               st);
   CK(hipGetLastError());
+  // shader clock of the last launch: median over workgroups of cycles / (100 MHz ticks * 10 ns)
+  std::vector<long long> h(4 * kCUs);
+  CK(hipMemcpy(h.data(), clk, h.size() * sizeof(long long), hipMemcpyDeviceToHost));
+  std::vector<double> ghz;
+  for (int b = 0; b < kCUs; ++b) {
+    const long long dr = h[4 * b + 3] - h[4 * b + 1];
+    if (dr > 0) ghz.push_back(double(h[4 * b + 2] - h[4 * b]) / (double(dr) * 10.0));
+  }
+  std::sort(ghz.begin(), ghz.end());
+  const double clock_ghz = ghz.empty() ? 0.0 : ghz[ghz.size() / 2];
   const double mfma_per_simd = double(iters) * NACC * waves_per_simd;
   const double ops = double(SHAPE == 16 ? 32768 : 65536) * NACC * iters * 4 * waves_per_simd * kCUs;
-  std::printf("mfma shape %dx%d chains %d valu %d ds_read %d waves_per_simd %d ns_per_mfma %.3f tops %.1f peak_frac %.3f\n",
+  std::printf("mfma shape %dx%d chains %d valu %d ds_read %d waves_per_simd %d ns_per_mfma %.3f tops %.1f peak_frac %.3f "
+              "clock_ghz %.2f\n",
               SHAPE, SHAPE, NACC, NV, ND, waves_per_simd, us * 1000.0 / mfma_per_simd, ops / us * 1e-6,
-              ops / us * 1e-6 / 5000.0);
+              ops / us * 1e-6 / 5000.0, clock_ghz);
 }
 
 void probe_mfma(hipStream_t st) {
   int* out = nullptr;
+  long long* clk = nullptr;
   CK(hipMalloc(&out, kCUs * 1024 * sizeof(int)));
-  run_mfma<16, 4, 0, 0>(1, out, st);
-  run_mfma<16, 4, 0, 0>(2, out, st);
-  run_mfma<16, 8, 0, 0>(1, out, st);
-  run_mfma<32, 2, 0, 0>(1, out, st);
-  run_mfma<32, 2, 0, 0>(2, out, st);
-  run_mfma<32, 4, 0, 0>(1, out, st);
-  run_mfma<16, 4, 4, 0>(1, out, st);
-  run_mfma<16, 4, 8, 0>(1, out, st);
-  run_mfma<16, 4, 16, 0>(1, out, st);
-  run_mfma<16, 4, 8, 0>(2, out, st);
-  run_mfma<16, 4, 0, 1>(1, out, st);
-  run_mfma<16, 4, 0, 1>(2, out, st);
-  run_mfma<16, 4, 0, 2>(1, out, st);
-  run_mfma<16, 4, 8, 1>(1, out, st);
-  run_mfma<16, 4, 8, 1>(2, out, st);
-  run_mfma<32, 2, 8, 1>(1, out, st);
-  run_mfma<32, 2, 8, 1>(2, out, st);
+  CK(hipMalloc(&clk, 4 * kCUs * sizeof(long long)));
+  CK(hipMemset(clk, 0, 4 * kCUs * sizeof(long long)));
+  run_mfma<16, 4, 0, 0>(1, out, clk, st);
+  run_mfma<16, 4, 0, 0>(2, out, clk, st);
+  run_mfma<16, 8, 0, 0>(1, out, clk, st);
+  run_mfma<32, 2, 0, 0>(1, out, clk, st);
+  run_mfma<32, 2, 0, 0>(2, out, clk, st);
+  run_mfma<32, 4, 0, 0>(1, out, clk, st);
+  run_mfma<16, 4, 4, 0>(1, out, clk, st);
+  run_mfma<16, 4, 8, 0>(1, out, clk, st);
+  run_mfma<16, 4, 16, 0>(1, out, clk, st);
+  run_mfma<16, 4, 8, 0>(2, out, clk, st);
+  run_mfma<16, 4, 0, 1>(1, out, clk, st);
+  run_mfma<16, 4, 0, 1>(2, out, clk, st);
+  run_mfma<16, 4, 0, 2>(1, out, clk, st);
+  run_mfma<16, 4, 8, 1>(1, out, clk, st);
+  run_mfma<16, 4, 8, 1>(2, out, clk, st);
+  run_mfma<32, 2, 8, 1>(1, out, clk, st);
+  run_mfma<32, 2, 8, 1>(2, out, clk, st);
   CK(hipFree(out));
+  CK(hipFree(clk));
 }
 
 }  // namespace
