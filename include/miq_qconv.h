@@ -61,7 +61,11 @@ typedef enum miq_algo {
                           fit in LDS, 16-byte aligned tensors, bias and scales */,
   MIQ_ALGO_DOT4 = 8    /* int8 vector-ALU kernel (v_dot4_i32_i8, no matrix instructions): any shape
                           whose filter tile, r*s*ceil(c/groups/4) x up to 32 channels dwords, fits in
-                          64 KB; the bandwidth-bound fallback for thin C and few output channels */
+                          64 KB; the bandwidth-bound fallback for thin C and few output channels */,
+  MIQ_ALGO_PIPE = 9    /* int8 MFMA row-band kernel whose input rows stream into LDS under the matrix
+                          instructions (a loader wave publishes each row): int8 output only, groups
+                          1, c == k == 64, stride 1, a 3x3 or 1x1 filter, output width % 8 == 0,
+                          16-byte aligned tensors, bias and scales */
 } miq_algo;
 
 /* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */

@@ -31,6 +31,7 @@ SOURCES = [
     "qconv_band.hip",
     "qconv_stream.hip",
     "qconv_flat.hip",
+    "qconv_pipe.hip",
     "qconv_dot4.hip",
     "gemm_i32.hip",
     "conv_f32.hip",

@@ -312,6 +312,10 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
       if (!miq::dot4_eligible(*g, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       *algo = MIQ_ALGO_DOT4;
       break;
+    case MIQ_ALGO_PIPE:
+      if (!miq::pipe_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_PIPE;
+      break;
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
   }
@@ -344,6 +348,7 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
     case MIQ_ALGO_STREAM: e = miq::launch_i8_stream(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_FLAT: e = miq::launch_i8_flat(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_DOT4: e = miq::launch_i8_dot4(g, epi, x, w, y, rq, s); break;
+    case MIQ_ALGO_PIPE: e = miq::launch_i8_pipe(g, epi, x, w, y, rq, s); break;
     default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");

@@ -131,6 +131,14 @@ bool flat_eligible(const Geom& g, const void* x, const void* w, const void* y, c
 hipError_t launch_i8_flat(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
 
+// int8 MFMA row-band kernel whose input rows stream into LDS under the matrix instructions
+// (loader wave, per-row LDS flags): int8 output, groups 1, C == K == 64, stride 1, 3x3 or 1x1,
+// Wo % 8 == 0.
+bool pipe_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                   std::string* why);
+hipError_t launch_i8_pipe(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
+                          hipStream_t stream);
+
 // int8 MFMA kernel with the filter streamed through LDS: (C/groups) % 64 == 0,
 // (K/groups) % 128 == 0, stride_w <= 4.
 bool stream_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,

@@ -146,8 +146,12 @@ def test_entry_points_reject_before_touching_the_gpu():
     assert lib.miq_qconv2d_nhwc_i8(C.byref(d), fake, fake, None, None, fake, None) == _capi.MIQ_ERR_NULL_POINTER
     d = M.make_desc((1, 8, 8, 32), (4, 3, 3, 32), padding=1, out_scale=0.0)
     assert lib.miq_qconv2d_nhwc_i8(C.byref(d), fake, fake, None, fake, fake, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
-    d = M.make_desc((1, 8, 8, 32), (4, 3, 3, 32), padding=1, algo=9)
+    d = M.make_desc((1, 8, 8, 32), (4, 3, 3, 32), padding=1, algo=99)
     assert lib.miq_qconv2d_nhwc_i8_acc32(C.byref(d), fake, fake, fake, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
+    # the pipe kernel writes int8 outputs only
+    d = M.make_desc((1, 8, 8, 64), (64, 3, 3, 64), padding=1, algo="pipe")
+    assert lib.miq_qconv2d_nhwc_i8_acc32(C.byref(d), fake, fake, fake, None) == _capi.MIQ_ERR_UNSUPPORTED
+    assert b"int8 outputs only" in lib.miq_last_error_message()
     d = M.make_desc((-1, 8, 8, 32), (4, 3, 3, 32), padding=1)
     assert lib.miq_qconv2d_nhwc_i8_acc32(C.byref(d), fake, fake, fake, None) == _capi.MIQ_ERR_INVALID_ARGUMENT
 
@@ -188,7 +192,7 @@ def test_plan_never_sends_nonpositive_dilation_to_mfma_kernels(dil):
     except M.MiqError:
         return  # the shape itself is rejected: nothing runs
     assert auto == "direct", (dil, auto)
-    for algo in ("band", "stream", "igemm", "stem"):
+    for algo in ("band", "stream", "igemm", "stem", "pipe"):
         with pytest.raises(M.MiqError):
             M.plan(M.make_desc(x_shape, w_shape, padding=1, dilation=dil, algo=algo))
 

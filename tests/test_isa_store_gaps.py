@@ -19,7 +19,7 @@ from my_own_cnn_amd import build as B
 
 KERNEL_SOURCES = ["qconv_igemm.hip", "qconv_stem.hip", "qconv_band.hip", "qconv_stream.hip", "qconv_direct.hip",
                   "gemm_i32.hip", "conv_f32.hip", "qconv_qi32.hip", "qconv_dot4.hip",
-                  "qconv_qi32_band.hip", "qconv_qi32_route.hip"]
+                  "qconv_qi32_band.hip", "qconv_qi32_route.hip", "qconv_flat.hip", "qconv_pipe.hip"]
 
 
 def _regs(spec):
