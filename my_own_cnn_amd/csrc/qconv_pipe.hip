@@ -365,9 +365,12 @@ __global__ void __launch_bounds__(64 * kPipeWaves, 1) i8_pipe_kernel(PipeArgs a_
     asm volatile("" ::: "memory");
   };
   // The requantized half-segment (32 channels) goes to the LDS staging area and the segment's
-  // count of staged halves is raised; the wave that stages the second half writes the whole
-  // segment (16 pixels x 64 channels, one contiguous kilobyte of NHWC output) with one 16-byte
-  // store per lane and the write-through non-temporal policy.
+  // count of staged halves is raised (LDS operations of a wave complete in order, so a count
+  // seen raised means its bytes are written).  The odd-half waves (h == 1) store whole segments
+  // (16 pixels x 64 channels, one contiguous kilobyte of NHWC output, one 16-byte
+  // write-through non-temporal store per lane): those of a pair once they have computed the
+  // next pair, when the even-half wave of the same segments has staged its half as well.
+  // Nothing in this waits on an atomic's return.
   const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * 64;
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + out0, band_px * 64);
   typedef int v2i __attribute__((ext_vector_type(2)));
@@ -376,18 +379,33 @@ __global__ void __launch_bounds__(64 * kPipeWaves, 1) i8_pipe_kernel(PipeArgs a_
     pack8<RELU>(a0, a1, mult_v, d0, d1);
     *reinterpret_cast<__attribute__((address_space(3))) v2i*>(static_cast<uintptr_t>(stage_lane + kPipeStageSeg * seg)) =
         v2i{static_cast<int>(d0), static_cast<int>(d1)};
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staged bytes are written before the count rises
-    int before = 0;
-    if (lane == 0) before = __hip_atomic_fetch_add(scount + seg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (__builtin_amdgcn_readfirstlane(before) == 1) {
-      asm volatile("" ::: "memory");
-      const v4i d = lds_read16(base + static_cast<unsigned>(a.out_lds) + kPipeStageSeg * seg + kPipeStagePx * rho + 16u * g);
-      // pixels past the band get an offset past num_records (dropped), in voffset itself
-      const unsigned voff = 1024u * seg + 64u * rho + 16u * g + (16 * seg + rho < band_px ? 0u : 0x40000000u);
-      __builtin_amdgcn_raw_buffer_store_b128(d, ry, voff, 0, kStoreAux);
-      store_gap(d);
-    }
+    if (lane == 0) __hip_atomic_fetch_add(scount + seg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   };
+  auto store_seg = [&](int seg) {
+    const v4i d = lds_read16(base + static_cast<unsigned>(a.out_lds) + kPipeStageSeg * seg + kPipeStagePx * rho + 16u * g);
+    // pixels past the band get an offset past num_records (dropped), in voffset itself
+    const unsigned voff = 1024u * seg + 64u * rho + 16u * g + (16 * seg + rho < band_px ? 0u : 0x40000000u);
+    __builtin_amdgcn_raw_buffer_store_b128(d, ry, voff, 0, kStoreAux);
+    store_gap(d);
+  };
+  // segments ps and ps + 1 (when two) once both halves of each are staged (ps even: the two
+  // counts are one aligned 8-byte word)
+  auto store_pair = [&](int ps, bool two) {
+    // bounded: the even-half wave stages every half, so this ends long before the bound
+    for (int it = 0; it < (1 << 20); ++it) {
+      const long long both = __hip_atomic_load(reinterpret_cast<long long*>(scount + ps), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int c0 = __builtin_amdgcn_readfirstlane(static_cast<int>(both));
+      const int c1 = __builtin_amdgcn_readfirstlane(static_cast<int>(both >> 32));
+      if (c0 >= 2 && (!two || c1 >= 2)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+    store_seg(ps);
+    if (two) store_seg(ps + 1);
+  };
+  int pend = -1;        // the odd-half wave's pair waiting to be stored (first segment), or -1
+  bool pend_two = false;
 
   const int rext = (R - 1) * a.dh + 1;
   for (int pp = m; 2 * pp < nseg; pp += 4) {
@@ -422,6 +440,9 @@ __global__ void __launch_bounds__(64 * kPipeWaves, 1) i8_pipe_kernel(PipeArgs a_
       }
       stage(s0, c00, c01);
       stage(s0 + 1, c10, c11);
+      if (h == 1 && pend >= 0) store_pair(pend, pend_two);
+      pend = s0;
+      pend_two = true;
     } else {
       v4i c00, c01;
       constexpr int RS = KB < 3 ? KB : 3;
@@ -439,8 +460,12 @@ __global__ void __launch_bounds__(64 * kPipeWaves, 1) i8_pipe_kernel(PipeArgs a_
         __builtin_amdgcn_sched_barrier(0);
       }
       stage(s0, c00, c01);
+      if (h == 1 && pend >= 0) store_pair(pend, pend_two);
+      pend = s0;
+      pend_two = false;
     }
   }
+  if (h == 1 && pend >= 0) store_pair(pend, pend_two);
 }
 
 struct PipePlan {
