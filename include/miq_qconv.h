@@ -14,8 +14,16 @@
  *     asynchronous with respect to the host; the caller synchronises.
  *   - Arguments are validated on the host before anything is enqueued; a failed
  *     validation returns a non-zero status and leaves the output untouched.
- *   - The library allocates no device memory and keeps no mutable global state, so
- *     calls are re-entrant; calls on different streams may overlap.
+ *   - Device memory the library allocates itself: the entry points with the reference's
+ *     signatures that need a workspace and have no argument for one keep grow-only buffers
+ *     (the float-code row-band and stream paths one per (device, stream), at most 64 such
+ *     pairs; the fp32 filter gradient one per device), allocated with hipMalloc on first use
+ *     and when a larger problem arrives.  A grown-out buffer is kept, not freed, until the
+ *     process ends, and no call synchronises.  Each has a form that takes the caller's
+ *     workspace and allocates nothing (miq_fprop_nhwc_qi32_ws, miq_grad_nhwc_f32_ws).  The
+ *     32 MiB array of miq_grad_nhwc_f32_noalloc is part of the library's device code and is
+ *     allocated when that code is loaded on a device.  Nothing else is allocated, and no
+ *     other global state changes, so calls on different streams may overlap.
  *   - miq_last_error_message() returns the text of the last non-OK status raised on
  *     the calling thread.
  */
@@ -192,6 +200,27 @@ int miq_fprop_nhwc_qi32_algo(int32_t qp_kind, const float* x, const float* w, in
                              int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
                              const void* in_qp, const void* f_qp, int32_t algo, void* stream);
 
+/* Bytes of device workspace miq_fprop_nhwc_qi32_ws needs for this shape and algo (the row-band
+ * and stream kernels' prepass output; 0 for the others and for an empty output), for 256-byte
+ * aligned tensors (misaligned ones can only take kernels that need none).  No GPU access.  No
+ * reference counterpart: it sizes the caller-provided form of the workspace that
+ * launch_fprop_nhwc_qi32_impl (/root/reference/src/cuda_kernels.cu:1351-1354) allocates. */
+int miq_fprop_nhwc_qi32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s,
+                                       int32_t k, const miq_conv2d_params* p, int32_t algo, size_t* bytes);
+
+/* miq_fprop_nhwc_qi32_algo with a caller-provided device workspace of at least
+ * miq_fprop_nhwc_qi32_workspace_size bytes (NULL allowed when that size is 0); allocates
+ * nothing and never synchronises, so it can be recorded into a HIP graph.  Same result bits as
+ * the entry points above.  The workspace must not be used by another call until this one's
+ * work on `stream` has finished.  Replaces launch_fprop_nhwc_qi32_u8 / _s5
+ * (/root/reference/src/cuda_kernels.cu:1467-1481) with the per-call workspace of
+ * launch_fprop_nhwc_qi32_impl (:1351-1354) passed in instead. */
+int miq_fprop_nhwc_qi32_ws(int32_t qp_kind, const float* x, const float* w, int32_t* y,
+                           int32_t n, int32_t h, int32_t wdt, int32_t c,
+                           int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
+                           const void* in_qp, const void* f_qp, int32_t algo, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* The kernel the float-code entry points run for a plain-filter problem with 256-byte aligned
  * tensors: writes MIQ_ALGO_BAND, MIQ_ALGO_STREAM, MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT to *algo.  No reference
  * counterpart. */
@@ -252,8 +281,8 @@ int miq_bprop_nhwc_f32(const float* dy, const float* w, float* dx, int32_t n, in
  *   MIQ_ALGO_DIRECT: the loop order and rounding of cpu_grad_nhwc: its result bit for bit.
  * The split kernels agree with cpu_grad_nhwc within abs 1e-4 / rel 1e-3, not bit for bit.
  * The ordered sums need a device workspace: this entry point keeps one per device, allocated
- * on first use and grown (hipMalloc; a device synchronisation before the old one is freed) as
- * the reference's static workspace is; calls that overlap on one device share it and race.
+ * (hipMalloc) on first use and grown as the reference's static workspace is, without freeing
+ * the outgrown buffer or synchronising; calls that overlap on one device share it and race.
  * Replaces launch_grad_nhwc (/root/reference/src/cuda_kernels.cu:874-937). */
 int miq_grad_nhwc_f32(const float* x, const float* dy, float* dw, int32_t n, int32_t h, int32_t wdt, int32_t c,
                       int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p, int32_t algo, void* stream);
@@ -276,7 +305,8 @@ int miq_grad_nhwc_f32_ws(const float* x, const float* dy, float* dw, int32_t n, 
 
 /* miq_grad_nhwc_f32 (same algo values, same result bits) without any device allocation: the
  * ordered split partial sums live in a file-scope device array of the library, 32 MiB per
- * device, held from the first call on a device until the process ends.  Shapes whose partial
+ * device, allocated when the library's device code is loaded on a device (its first kernel
+ * launch there, whichever entry point makes it) and held until the process ends.  Shapes whose partial
  * sums need more (miq_grad_nhwc_f32_workspace_size > 33554432 bytes) are rejected with
  * MIQ_ERR_UNSUPPORTED before anything is enqueued.  Calls that overlap on one device (other
  * streams or threads) share the array and race.  No reference counterpart: it exists for

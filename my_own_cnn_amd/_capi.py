@@ -123,6 +123,11 @@ SIGNATURES = {
     "miq_fprop_nhwc_qi32_algo": (
         C.c_int, [_I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P, _P, _I, _P]),
     "miq_plan_qi32": (C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _PI]),
+    "miq_fprop_nhwc_qi32_workspace_size": (
+        C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, C.POINTER(C.c_size_t)]),
+    "miq_fprop_nhwc_qi32_ws": (
+        C.c_int, [_I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P, _P, _I, _P, C.c_size_t,
+                  _P]),
     "miq_qconv2d_nhwc_i8": (C.c_int, [C.POINTER(QConvDesc), _P, _P, _P, _P, _P, _P]),
     "miq_qconv2d_nhwc_i8_acc32": (C.c_int, [C.POINTER(QConvDesc), _P, _P, _P, _P]),
     "miq_qconv2d_nhwc_i8_dequant": (C.c_int, [C.POINTER(QConvDesc), _P, _P, _P, _P, _P, _P]),

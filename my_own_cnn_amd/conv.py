@@ -143,9 +143,11 @@ QI32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2, "band": 4, "stream": 5}
 
 def fprop_nhwc_qi32_algo(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int,
                          r: int, s: int, k: int, p=None, in_qp: Pointer = None, f_qp: Pointer = None,
-                         algo: str = "auto", stream=None) -> None:
-    """launch_fprop_nhwc_qi32 with an explicit kernel ("auto", "band", "igemm" or "direct");
-    every choice gives the same int32 results."""
+                         algo: str = "auto", stream=None, workspace: Pointer = None, workspace_bytes: int = 0) -> None:
+    """launch_fprop_nhwc_qi32 with an explicit kernel ("auto", "band", "stream", "igemm" or
+    "direct"); every choice gives the same int32 results.  `workspace`: a device buffer of at
+    least qi32_workspace_size() bytes, which makes the call allocation-free
+    (miq_fprop_nhwc_qi32_ws); None uses the library's per-stream workspace."""
     tin = DataType(tin)
     if tin not in SUPPORTED_QI32_INPUTS:
         raise TypeError("launch_fprop_nhwc_qi32 supports only LinQuantU8 and LinQuantS5")
@@ -153,9 +155,23 @@ def fprop_nhwc_qi32_algo(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer
         raise RuntimeError("quantized CUDA fprop requires non-null quantization parameters")
     params = _as_params(p)
     kind = 0 if tin == DataType.LinQuantU8 else 1
-    check(lib().miq_fprop_nhwc_qi32_algo(kind, _addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k,
-                                         C.byref(params), _addr(in_qp), _addr(f_qp), QI32_ALGOS[algo],
-                                         _stream(stream)), "fprop_nhwc_qi32_algo")
+    if workspace is None:
+        check(lib().miq_fprop_nhwc_qi32_algo(kind, _addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k,
+                                             C.byref(params), _addr(in_qp), _addr(f_qp), QI32_ALGOS[algo],
+                                             _stream(stream)), "fprop_nhwc_qi32_algo")
+    else:
+        check(lib().miq_fprop_nhwc_qi32_ws(kind, _addr(d_x), _addr(d_w), _addr(d_y), n, h, w, c, r, s, k,
+                                           C.byref(params), _addr(in_qp), _addr(f_qp), QI32_ALGOS[algo],
+                                           _addr(workspace), workspace_bytes, _stream(stream)), "fprop_nhwc_qi32_ws")
+
+
+def qi32_workspace_size(n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=None, algo: str = "auto") -> int:
+    """Bytes of device workspace fprop_nhwc_qi32_algo(..., workspace=...) needs (no GPU access)."""
+    out = C.c_size_t()
+    params = _as_params(p)
+    check(lib().miq_fprop_nhwc_qi32_workspace_size(n, h, w, c, r, s, k, C.byref(params), QI32_ALGOS[algo],
+                                                   C.byref(out)), "qi32_workspace_size")
+    return out.value
 
 
 def plan_qi32(n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=None) -> str:

@@ -9,6 +9,7 @@
 #include <string>
 #include <vector>
 
+#include "grow_buffer.h"
 #include "miq_qconv.h"
 #include "qconv_internal.h"
 
@@ -149,50 +150,56 @@ int bprop_f32(const miq::Geom& g, const miq::BlockGeom& bg, const float* dy, con
   return MIQ_OK;
 }
 
-// Grow-only workspace per (device, stream) for the float-code row-band path (its filter
-// prepass output).  Calls on one stream are ordered and share it; each stream has its own, so
-// calls on different streams do not race.  Growing waits for the stream before freeing the old
-// buffer, which earlier launches on it may still read.
-struct StreamWorkspace {
+// hipMalloc as grow_buffer's allocator: 0 or the HIP error (cleared from the thread's last
+// error, so a failed doubled request does not surface in a later call).
+struct HipAlloc {
+  hipError_t err = hipSuccess;
+  int operator()(void** p, size_t bytes) {
+    err = hipMalloc(p, bytes);
+    if (err != hipSuccess) {
+      (void)hipGetLastError();
+      *p = nullptr;
+      return 1;
+    }
+    return 0;
+  }
+};
+
+// The float-code row-band and stream paths' workspace (the prepass's output) behind the
+// reference-signature entry points: one grow-only buffer per (device, stream), at most
+// kMaxQi32Workspaces of them.  Calls on one stream are ordered and share it; calls on
+// different streams never share one.  Neither growth nor any other call here synchronises.
+struct StreamKey {
   int dev;
   hipStream_t stream;
-  void* p;
-  size_t bytes;
+  bool operator==(const StreamKey& o) const { return dev == o.dev && stream == o.stream; }
 };
+constexpr size_t kMaxQi32Workspaces = 64;
 std::mutex g_qi32_ws_m;
-std::vector<StreamWorkspace> g_qi32_ws;
+miq::GrowBufferTable<StreamKey> g_qi32_ws(kMaxQi32Workspaces);
 
 int stream_workspace(hipStream_t s, size_t bytes, void** out) {
   *out = nullptr;
+  if (bytes == 0) return MIQ_OK;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lock(g_qi32_ws_m);
-  StreamWorkspace* w = nullptr;
-  for (auto& c : g_qi32_ws) {
-    if (c.dev == dev && c.stream == s) w = &c;
+  miq::GrowBuffer* b = g_qi32_ws.find_or_add(StreamKey{dev, s});
+  if (b == nullptr) {
+    return fail(MIQ_ERR_UNSUPPORTED,
+                "the float-code workspace table is full (64 (device, stream) pairs); use miq_fprop_nhwc_qi32_ws");
   }
-  if (w == nullptr) {
-    g_qi32_ws.push_back(StreamWorkspace{dev, s, nullptr, 0});
-    w = &g_qi32_ws.back();
-  }
-  if (w->bytes < bytes) {
-    if (w->p != nullptr) {
-      e = hipStreamSynchronize(s);
-      if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize before growing the qi32 workspace");
-      (void)hipFree(w->p);
-      w->p = nullptr;
-      w->bytes = 0;
-    }
-    e = hipMalloc(&w->p, bytes);
-    if (e != hipSuccess) {
-      w->p = nullptr;
-      return hip_fail(e, "hipMalloc of the qi32 workspace");
-    }
-    w->bytes = bytes;
-  }
-  *out = w->p;
+  HipAlloc alloc;
+  if (miq::grow_buffer(*b, bytes, alloc, out) != 0) return hip_fail(alloc.err, "hipMalloc of the qi32 workspace");
   return MIQ_OK;
+}
+
+// Bytes of workspace a float-code problem needs on the kernel `algo` (resolved, not AUTO).
+size_t qi32_workspace_bytes(const miq::Geom& g, int32_t algo) {
+  if (algo == MIQ_ALGO_BAND) return miq::qi32_band_workspace_bytes(g);
+  if (algo == MIQ_ALGO_STREAM) return miq::qi32_route_workspace_bytes(g);
+  return 0;
 }
 
 // The kernel AUTO runs for a float-code problem: the row-band kernel, else the stream route,
@@ -204,9 +211,16 @@ int32_t qi32_auto(const miq::Geom& g, const miq::BlockGeom& bg, const void* x, c
   return MIQ_ALGO_DIRECT;
 }
 
+// A caller workspace for qi32_entry: `given` false means the library's own (stream_workspace).
+struct CallerWorkspace {
+  bool given = false;
+  void* p = nullptr;
+  size_t bytes = 0;
+};
+
 int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const miq::Geom& g,
                const miq::BlockGeom& bg, const void* in_qp, const void* f_qp, void* stream,
-               int32_t algo = MIQ_ALGO_AUTO) {
+               int32_t algo = MIQ_ALGO_AUTO, CallerWorkspace cw = CallerWorkspace{}) {
   const long long filt = filt_elems(g) * bg.By * bg.Bx;
   int st = check_tensors(g, filt, x, w, y);
   if (st != MIQ_OK) return st;
@@ -229,22 +243,26 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND or STREAM");
   }
+  const size_t ws_bytes = qi32_workspace_bytes(g, algo);
+  if (cw.given && cw.bytes < ws_bytes) {
+    return fail(MIQ_ERR_INVALID_ARGUMENT, "workspace is smaller than miq_fprop_nhwc_qi32_workspace_size reports");
+  }
+  if (cw.given && ws_bytes > 0 && cw.p == nullptr) return fail(MIQ_ERR_NULL_POINTER, "workspace pointer is NULL");
   if (out_elems(g) == 0) return MIQ_OK;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
+  void* ws = cw.p;
+  if (!cw.given) {
+    st = stream_workspace(hs, ws_bytes, &ws);
+    if (st != MIQ_OK) return st;
+  }
   hipError_t e;
   switch (algo) {
     case MIQ_ALGO_BAND: {
-      void* ws = nullptr;
-      st = stream_workspace(hs, miq::qi32_band_workspace_bytes(g), &ws);
-      if (st != MIQ_OK) return st;
       e = miq::launch_qi32_band(g, bg, qk, x, w, y, in_qp, f_qp, ws, hs);
       if (e != hipSuccess) return hip_fail(e, "qi32 row-band launch");
       return MIQ_OK;
     }
     case MIQ_ALGO_STREAM: {
-      void* ws = nullptr;
-      st = stream_workspace(hs, miq::qi32_route_workspace_bytes(g), &ws);
-      if (st != MIQ_OK) return st;
       e = miq::launch_qi32_route(g, qk, x, w, y, in_qp, f_qp, ws, hs);
       if (e != hipSuccess) return hip_fail(e, "qi32 stream route launch");
       return MIQ_OK;
@@ -441,6 +459,50 @@ int miq_fprop_nhwc_qi32_algo(int32_t qp_kind, const float* x, const float* w, in
                     stream, algo);
 }
 
+int miq_fprop_nhwc_qi32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s,
+                                       int32_t k, const miq_conv2d_params* p, int32_t algo, size_t* bytes) {
+  if (bytes == nullptr) return fail(MIQ_ERR_NULL_POINTER, "bytes output pointer is NULL");
+  *bytes = 0;
+  miq::Geom g;
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  // sized for 256-byte aligned tensors: misaligned ones can only take kernels that need none
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  const miq::BlockGeom bg{1, 1, g.Ho, g.Wo};
+  std::string why;
+  switch (algo) {
+    case MIQ_ALGO_AUTO: algo = qi32_auto(g, bg, kAligned, kAligned, kAligned); break;
+    case MIQ_ALGO_DIRECT:
+    case MIQ_ALGO_IGEMM: break;
+    case MIQ_ALGO_BAND:
+      if (!miq::qi32_band_eligible(g, bg, kAligned, kAligned, kAligned, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      break;
+    case MIQ_ALGO_STREAM:
+      if (!miq::qi32_route_eligible(g, bg, kAligned, kAligned, kAligned, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      break;
+    default:
+      return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND or STREAM");
+  }
+  *bytes = out_elems(g) == 0 ? 0 : qi32_workspace_bytes(g, algo);
+  return MIQ_OK;
+}
+
+int miq_fprop_nhwc_qi32_ws(int32_t qp_kind, const float* x, const float* w, int32_t* y, int32_t n, int32_t h,
+                           int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
+                           const void* in_qp, const void* f_qp, int32_t algo, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (qp_kind != 0 && qp_kind != 1) return fail(MIQ_ERR_INVALID_ARGUMENT, "qp_kind must be 0 (LinQuantU8) or 1 (LinQuantS5)");
+  miq::Geom g;
+  const int st = infer_geom(n, h, wdt, c, r, s, k, p, &g);
+  if (st != MIQ_OK) return st;
+  CallerWorkspace cw;
+  cw.given = true;
+  cw.p = workspace;
+  cw.bytes = workspace_bytes;
+  return qi32_entry(qp_kind == 0 ? miq::kQpU8 : miq::kQpS5, x, w, y, g, miq::BlockGeom{1, 1, g.Ho, g.Wo}, in_qp, f_qp,
+                    stream, algo, cw);
+}
+
 int miq_plan_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
                   const miq_conv2d_params* p, int32_t* algo) {
   if (algo == nullptr) return fail(MIQ_ERR_NULL_POINTER, "algo output pointer is NULL");
@@ -596,16 +658,12 @@ int grad_launch(const miq::Geom& g, const miq::BlockGeom& bg, const GradChoice& 
 
 // Grow-only device workspace per device for miq_grad_nhwc_f32 and miq_block_grad_nhwc_f32
 // (the reference keeps one static workspace for its fp32 path, cuda_kernels.cu:155-158, grown
-// by ensure_capacity).  Growing waits for the device before freeing the old buffer, which
-// earlier launches may still read.  Calls that overlap on one device share it and race, as the
-// reference's do.
-struct DeviceWorkspace {
-  std::mutex m;
-  void* p = nullptr;
-  size_t bytes = 0;
-};
+// by ensure_capacity).  As the float-code workspace, it grows without freeing or waiting:
+// retired buffers stay allocated until the process ends.  Calls that overlap on one device
+// share it and race, as the reference's do.
 constexpr int kMaxDevices = 64;
-DeviceWorkspace g_grad_ws[kMaxDevices];
+std::mutex g_grad_ws_m;
+miq::GrowBuffer g_grad_ws[kMaxDevices];
 
 int cached_workspace(size_t bytes, void** out) {
   *out = nullptr;
@@ -614,24 +672,9 @@ int cached_workspace(size_t bytes, void** out) {
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev < 0 || dev >= kMaxDevices) return fail(MIQ_ERR_UNSUPPORTED, "device index beyond the workspace table");
-  DeviceWorkspace& w = g_grad_ws[dev];
-  std::lock_guard<std::mutex> lock(w.m);
-  if (w.bytes < bytes) {
-    if (w.p != nullptr) {
-      e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize before growing the grad workspace");
-      (void)hipFree(w.p);
-      w.p = nullptr;
-      w.bytes = 0;
-    }
-    e = hipMalloc(&w.p, bytes);
-    if (e != hipSuccess) {
-      w.p = nullptr;
-      return hip_fail(e, "hipMalloc of the grad workspace");
-    }
-    w.bytes = bytes;
-  }
-  *out = w.p;
+  std::lock_guard<std::mutex> lock(g_grad_ws_m);
+  HipAlloc alloc;
+  if (miq::grow_buffer(g_grad_ws[dev], bytes, alloc, out) != 0) return hip_fail(alloc.err, "hipMalloc of the grad workspace");
   return MIQ_OK;
 }
 

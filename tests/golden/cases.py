@@ -58,3 +58,35 @@ def config_goldens():
 
 def c1_acc():
     return np.load(HERE / "c1_tiny.npz")["acc"]
+
+
+# Full-size float-code problems (the reference's launch_fprop_nhwc_qi32 API at the C2 and C4
+# shapes): inputs regenerated from splitmix64 streams, outputs pinned by sha256 in
+# qi32_full.json (written by make_qi32_full.py from the reference's cpu_fprop_nhwc_qi32).
+QI32_FULL = {
+    # name: (kind, workload, code range, seed)
+    "c2_u8": ("u8", "r50_3x3", (0.0, 255.0), 7100),
+    "c2_s5": ("s5", "r50_3x3", (-16.0, 15.0), 7200),
+    "c4_u8": ("u8", "down_s2", (0.0, 255.0), 7300),
+}
+
+
+def qi32_full_inputs(name: str):
+    """(kind, x, w, conv7, in_zp, f_zp) of a full-size float-code problem: fractional codes
+    uniform over the kind's code range, per-image input zero points, one filter zero point."""
+    from my_own_cnn_amd.workloads import WORKLOADS, fill_f32_uniform, fill_i32_uniform
+
+    kind, wl_name, (lo, hi), seed = QI32_FULL[name]
+    wl = WORKLOADS[wl_name]
+    x = fill_f32_uniform(wl.n * wl.h * wl.w * wl.c, seed, lo, hi).reshape(wl.n, wl.h, wl.w, wl.c)
+    w = fill_f32_uniform(wl.k * wl.r * wl.s * wl.c, seed + 1, lo, hi).reshape(wl.k, wl.r, wl.s, wl.c)
+    zlo, zhi = (0, 255) if kind == "u8" else (-128, 127)
+    zp = fill_i32_uniform(wl.n, seed + 2, zlo, zhi)
+    fzp = int(fill_i32_uniform(1, seed + 3, zlo, zhi)[0])
+    conv = (wl.pad, wl.pad, wl.stride, wl.stride, 1, 1, wl.groups)
+    return kind, x, w, conv, zp, fzp
+
+
+def qi32_full_goldens():
+    with open(HERE / "qi32_full.json") as f:
+        return json.load(f)

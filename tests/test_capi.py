@@ -181,6 +181,50 @@ def test_plan_of_the_workloads(name, algo):
     assert M.plan(d) == algo
 
 
+def test_qi32_workspace_size():
+    """The caller-workspace size of the float-code path (no GPU access): the row-band kernel's
+    filter prepass output on C2 (9 K-blocks of one 64-channel tile: 4 KB of int8 fragments and
+    a 4-byte range flag each), the stream route's on C4 (the zero-padded int8 copy of the input,
+    32 x 58 x 58 x 128 bytes, then the int8 filter 256 x 1152, per-channel sums 256 x 4, per-image
+    parameters 32 x 16 and 3396 flags, each part 256-byte aligned), and none for the kernels
+    that need none."""
+    c2 = M.Conv2DParams(1, 1, 1, 1, 1, 1, 1)
+    c4 = M.Conv2DParams(1, 1, 2, 2, 1, 1, 1)
+    assert M.qi32_workspace_size(32, 56, 56, 64, 3, 3, 64, c2) == 9 * 4096 + 9 * 4
+    assert M.qi32_workspace_size(32, 56, 56, 64, 3, 3, 64, c2, algo="band") == 9 * 4096 + 9 * 4
+    padded = 32 * 58 * 58 * 128
+    assert padded % 256 == 0
+    route = padded + 256 * 1152 + 256 * 4 + 32 * 16 + 3396 * 4
+    assert M.qi32_workspace_size(32, 56, 56, 128, 3, 3, 256, c4) == (route + 255) // 256 * 256
+    for algo in ("igemm", "direct"):
+        assert M.qi32_workspace_size(32, 56, 56, 64, 3, 3, 64, c2, algo=algo) == 0
+    assert M.qi32_workspace_size(1, 32, 32, 16, 3, 3, 32, c2) == 0  # C1 runs the implicit GEMM
+    with pytest.raises(M.MiqError, match="band"):
+        M.qi32_workspace_size(1, 32, 32, 16, 3, 3, 32, c2, algo="band")  # c % 64 != 0
+    lib = M.lib()
+    out = C.c_size_t(5)
+    assert lib.miq_fprop_nhwc_qi32_workspace_size(32, 56, 56, 64, 3, 3, 64, C.byref(c2), 99, C.byref(out)) == 2
+    assert lib.miq_fprop_nhwc_qi32_workspace_size(32, 56, 56, 64, 3, 3, 64, C.byref(c2), 0, None) == 1
+
+
+def test_qi32_ws_validates_before_launch():
+    """The caller-workspace entry point checks its workspace on the host before anything is
+    enqueued: too small or NULL where one is needed is an error (no GPU access needed)."""
+    lib = M.lib()
+    c2 = M.Conv2DParams(1, 1, 1, 1, 1, 1, 1)
+    need = M.qi32_workspace_size(32, 56, 56, 64, 3, 3, 64, c2)
+    fake = C.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    st = lib.miq_fprop_nhwc_qi32_ws(0, fake, fake, fake, 32, 56, 56, 64, 3, 3, 64, C.byref(c2), fake, fake, 4,
+                                    fake, need - 1, None)
+    assert st == 2 and b"smaller than miq_fprop_nhwc_qi32_workspace_size" in lib.miq_last_error_message()
+    st = lib.miq_fprop_nhwc_qi32_ws(0, fake, fake, fake, 32, 56, 56, 64, 3, 3, 64, C.byref(c2), fake, fake, 4,
+                                    None, need, None)
+    assert st == 1 and b"workspace pointer is NULL" in lib.miq_last_error_message()
+    st = lib.miq_fprop_nhwc_qi32_ws(2, fake, fake, fake, 32, 56, 56, 64, 3, 3, 64, C.byref(c2), fake, fake, 0,
+                                    fake, need, None)
+    assert st == 2 and b"qp_kind" in lib.miq_last_error_message()
+
+
 @pytest.mark.parametrize("dil", [(-1, -1), (1, -1), (-1, 1), (0, 1), (1, 0)])
 def test_plan_never_sends_nonpositive_dilation_to_mfma_kernels(dil):
     """infer_conv_shape accepts dilation <= 0 (as the reference's does); only the direct

@@ -114,3 +114,15 @@ def test_oracle_against_reference_random():
         want, _ = oracle.ref_conv_qi32(kind, x, wt, conv, zp, fzp, block)
         got = oracle.conv_qi32(x, wt, conv, zp, fzp, block)
         np.testing.assert_array_equal(got, want, err_msg=f"trial {trial}")
+
+
+@pytest.mark.parametrize("name", list(cases.QI32_FULL))
+def test_qi32_full_size_against_reference_sha(name):
+    """The oracle's float-code convolution at the full C2 / C4 sizes equals the reference's own
+    cpu_fprop_nhwc_qi32 on the same inputs (sha256 of the int32 outputs, written from
+    oracle/_ref by tests/golden/make_qi32_full.py)."""
+    g = cases.qi32_full_goldens()[name]
+    kind, x, w, conv, zp, fzp = cases.qi32_full_inputs(name)
+    y = oracle.conv_qi32(x, w, conv, zp, fzp)
+    assert list(y.shape) == g["shape"]
+    assert hashlib.sha256(y.tobytes()).hexdigest() == g["sha256"]

@@ -76,3 +76,47 @@ def test_noalloc_grad_rejects_what_does_not_fit(device):
                                        C.c_void_p(dw.data_ptr()), n, h, w, c, r, s, k, C.byref(p), 0, None)
     assert st == _capi.MIQ_ERR_UNSUPPORTED
     assert b"allocation-free" in lib.miq_last_error_message()
+
+
+def test_noalloc_grad_in_a_graph(device):
+    """miq_grad_nhwc_f32_noalloc recorded into a HIP graph (torch.cuda.graph on a side stream)
+    and replayed three times, with eager work and synchronisations between replays: every
+    replay gives the ordered entry point's bits, and the captured call allocates nothing (the
+    device's free memory does not drop by anything near the 28.9 MB workspace the allocating
+    entry point would need)."""
+    lib = M.lib()
+    name, n, h, w, c, k, r, s, conv = SHAPES[0]
+    rng = np.random.default_rng(77)
+    ho, wo = oracle.conv_output_shape(n, h, w, c, r, s, k, conv)
+    xd = torch.from_numpy(rng.uniform(-1, 1, size=(n, h, w, c)).astype(np.float32)).to(device)
+    dyd = torch.from_numpy(rng.uniform(-1, 1, size=(n, ho, wo, k)).astype(np.float32)).to(device)
+    wshape = (k, r, s, c // conv[6])
+    need = M.grad_workspace_size(n, h, w, c, r, s, k, conv)
+    assert need > 16 << 20
+    ref = torch.empty(wshape, dtype=torch.float32, device=device)
+    _call(lib.miq_grad_nhwc_f32, xd, dyd, ref, (n, h, w, c, k, r, s), conv)
+    got = torch.empty(wshape, dtype=torch.float32, device=device)
+    _call(lib.miq_grad_nhwc_f32_noalloc, xd, dyd, got, (n, h, w, c, k, r, s), conv)  # first call on the device
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    free0 = torch.cuda.mem_get_info()[0]
+    graph = torch.cuda.CUDAGraph()
+    p = _capi.Conv2DParams(*conv)
+    print("noalloc grad graph: capture", flush=True)
+    with torch.cuda.graph(graph, stream=side):
+        st = lib.miq_grad_nhwc_f32_noalloc(C.c_void_p(xd.data_ptr()), C.c_void_p(dyd.data_ptr()),
+                                           C.c_void_p(got.data_ptr()), n, h, w, c, r, s, k, C.byref(p), 0,
+                                           C.c_void_p(side.cuda_stream))
+    assert st == _capi.MIQ_OK, lib.miq_last_error_message()
+    torch.cuda.synchronize()
+    want = ref.cpu().numpy().view(np.uint32)
+    for rep in range(3):
+        got.fill_(float(rep) - 5.0)
+        torch.cuda.synchronize()
+        print(f"noalloc grad graph: replay {rep}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want, err_msg=f"replay {rep}")
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free0 - free1 < need // 2, (free0, free1, need)
