@@ -49,7 +49,8 @@ typedef enum miq_status {
 
 /* Kernel families of the int8 entry points (miq_qconv_desc.algo). */
 typedef enum miq_algo {
-  MIQ_ALGO_AUTO = 0,   /* pick by shape: band kernel, else flat kernel, else stream kernel, else the dot4
+  MIQ_ALGO_AUTO = 0,   /* pick by shape: pointwise kernel (int8 output), else band kernel, else flat
+                          kernel, else stream kernel, else the dot4
                           kernel for <= 8 output channels per group on 1x1 or small filters, else
                           implicit GEMM, else stem kernel for thin C, else direct */
   MIQ_ALGO_DIRECT = 1, /* VALU direct convolution: any shape, bandwidth-bound fallback */
@@ -73,7 +74,11 @@ typedef enum miq_algo {
   MIQ_ALGO_PIPE = 9    /* int8 MFMA row-band kernel whose input rows stream into LDS under the matrix
                           instructions (a loader wave publishes each row): int8 output only, groups
                           1, c == k == 64, stride 1, a 3x3 or 1x1 filter, output width % 8 == 0,
-                          16-byte aligned tensors, bias and scales */
+                          16-byte aligned tensors, bias and scales */,
+  MIQ_ALGO_POINTWISE = 10 /* int8 MFMA GEMM over the flattened pixels of a 1x1 convolution, input
+                          streamed into LDS by a loader wave: int8 output only, groups 1, stride 1,
+                          no padding, c 64 or 128, k % 64 == 0, 16-byte aligned tensors, bias and
+                          scales */
 } miq_algo;
 
 /* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */

@@ -32,6 +32,7 @@ SOURCES = [
     "qconv_stream.hip",
     "qconv_flat.hip",
     "qconv_pipe.hip",
+    "qconv_pointwise.hip",
     "qconv_dot4.hip",
     "gemm_i32.hip",
     "conv_f32.hip",

@@ -287,7 +287,9 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
   std::string why;
   switch (d->algo) {
     case MIQ_ALGO_AUTO:
-      if (miq::band_eligible(*g, x, w, y, rq, epi, nullptr)) {
+      if (miq::pointwise_eligible(*g, x, w, y, rq, epi, nullptr)) {
+        *algo = MIQ_ALGO_POINTWISE;
+      } else if (miq::band_eligible(*g, x, w, y, rq, epi, nullptr)) {
         *algo = MIQ_ALGO_BAND;
       } else if (miq::flat_eligible(*g, x, w, y, rq, epi, nullptr)) {
         *algo = MIQ_ALGO_FLAT;
@@ -334,6 +336,10 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
       if (!miq::pipe_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       *algo = MIQ_ALGO_PIPE;
       break;
+    case MIQ_ALGO_POINTWISE:
+      if (!miq::pointwise_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_POINTWISE;
+      break;
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
   }
@@ -367,6 +373,7 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
     case MIQ_ALGO_FLAT: e = miq::launch_i8_flat(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_DOT4: e = miq::launch_i8_dot4(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_PIPE: e = miq::launch_i8_pipe(g, epi, x, w, y, rq, s); break;
+    case MIQ_ALGO_POINTWISE: e = miq::launch_i8_pointwise(g, x, w, static_cast<int8_t*>(y), rq, s); break;
     default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");

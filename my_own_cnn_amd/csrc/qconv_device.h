@@ -92,6 +92,18 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, v4i* lds, u
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
 }
 
+// Writes v to the LDS word at p (a pointer into __shared__ memory) without waiting for this
+// wave's outstanding loads.  After a buffer_load ... lds the compiler puts a vmcnt(0) wait in
+// front of any LDS store, plain or atomic, because it cannot tell the loads' LDS destinations
+// from the stored word apart: a loader wave that publishes its progress word by word would
+// wait for all of its loads at the first publish.  The store is issued by inline assembly,
+// which that analysis does not see; this wave's LDS operations still complete in order, and
+// an LDS operation the compiler does not count only makes its lgkmcnt waits stricter.
+__device__ __forceinline__ void lds_publish(int* p, int v) {
+  const unsigned addr = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p) & 0xffffffffu);
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+
 // 16 bytes from LDS byte address `addr`.
 __device__ __forceinline__ v4i lds_read16(unsigned addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(static_cast<uintptr_t>(addr));

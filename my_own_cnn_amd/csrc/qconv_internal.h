@@ -139,6 +139,13 @@ bool pipe_eligible(const Geom& g, const void* x, const void* w, const void* y, c
 hipError_t launch_i8_pipe(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
 
+// int8 MFMA pointwise kernel (1x1, stride 1, no padding, groups 1, C 64 or 128, K % 64 == 0):
+// a GEMM over the flattened pixels with the input streamed into LDS by a loader wave.
+bool pointwise_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                        std::string* why);
+hipError_t launch_i8_pointwise(const Geom& g, const int8_t* x, const int8_t* w, int8_t* y, const Requant& rq,
+                               hipStream_t stream);
+
 // int8 MFMA kernel with the filter streamed through LDS: (C/groups) % 64 == 0,
 // (K/groups) % 128 == 0, stride_w <= 4.
 bool stream_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,

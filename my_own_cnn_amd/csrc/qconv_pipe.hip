@@ -163,7 +163,7 @@ __device__ __forceinline__ void loader_publish(int K, int done, int* myflag, int
     if (M < K) {
       wait_vm<M * NJ>();
       asm volatile("" ::: "memory");
-      if (lane == 0) __hip_atomic_store(myflag, done + K - M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (lane == 0) lds_publish(myflag, done + K - M);
     }
     loader_publish<NJ, M - 1>(K, done, myflag, lane);
   }

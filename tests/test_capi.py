@@ -172,7 +172,7 @@ def test_python_mirror_errors():
         M.launch_fprop_nhwc_qi32(M.DataType.LinQuantI8, 1, 1, 1, 1, 5, 5, 4, 3, 3, 4, None, 1, 1)
 
 
-@pytest.mark.parametrize("name,algo", [("tiny", "igemm"), ("r50_3x3", "band"), ("r50_1x1", "band"),
+@pytest.mark.parametrize("name,algo", [("tiny", "igemm"), ("r50_3x3", "band"), ("r50_1x1", "pointwise"),
                                        ("down_s2", "stream"), ("stem", "stem")])
 def test_plan_of_the_workloads(name, algo):
     wl = M.WORKLOADS[name]
@@ -464,3 +464,22 @@ def test_plan_block_f32():
 def test_auto_takes_the_dot4_kernel_where_it_measured_faster(shape, want):
     xs, ws, kw = shape
     assert M.plan(M.make_desc(xs, ws, **kw)) == want
+
+
+@pytest.mark.parametrize("xs,ws,kw,ok", [
+    ((64, 28, 28, 128), (512, 1, 1, 128), {}, True),
+    ((2, 7, 7, 64), (192, 1, 1, 64), {}, True),
+    ((2, 7, 7, 64), (64, 3, 3, 64), {"padding": 1}, False),        # not 1x1
+    ((2, 8, 8, 64), (64, 1, 1, 64), {"stride": 2}, False),         # strided
+    ((2, 8, 8, 64), (64, 1, 1, 64), {"padding": 1}, False),        # padded
+    ((2, 8, 8, 256), (64, 1, 1, 256), {}, False),                  # c = 256
+    ((2, 8, 8, 64), (48, 1, 1, 64), {}, False),                    # k % 64 != 0
+    ((2, 8, 8, 128), (128, 1, 1, 64), {"groups": 2}, False),       # grouped
+])
+def test_pointwise_planner(xs, ws, kw, ok):
+    d = M.make_desc(xs, ws, algo="pointwise", **kw)
+    if ok:
+        assert M.plan(d) == "pointwise"
+    else:
+        with pytest.raises(M.MiqError):
+            M.plan(d)
