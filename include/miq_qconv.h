@@ -52,7 +52,8 @@ typedef enum miq_algo {
   MIQ_ALGO_AUTO = 0,   /* pick by shape: pointwise kernel (int8 output), else band kernel, else flat
                           kernel, else stream kernel, else the dot4
                           kernel for <= 8 output channels per group on 1x1 or small filters, else
-                          implicit GEMM, else stem kernel for thin C, else direct */
+                          implicit GEMM, else the space-to-depth stem kernel (int8 output), else
+                          stem kernel for thin C, else direct */
   MIQ_ALGO_DIRECT = 1, /* VALU direct convolution: any shape, bandwidth-bound fallback */
   MIQ_ALGO_IGEMM = 2,  /* int8 MFMA implicit GEMM: needs (c/groups) % 16 == 0, 16-byte aligned tensors */
   MIQ_ALGO_STEM = 3,   /* int8 MFMA thin-channel kernel: c/groups < 16, groups == 1 */
@@ -78,7 +79,11 @@ typedef enum miq_algo {
   MIQ_ALGO_POINTWISE = 10 /* int8 MFMA GEMM over the flattened pixels of a 1x1 convolution, input
                           streamed into LDS by a loader wave: int8 output only, groups 1, stride 1,
                           no padding, c 64 or 128, k % 64 == 0, 16-byte aligned tensors, bias and
-                          scales */
+                          scales */,
+  MIQ_ALGO_STEM_S2D = 11 /* int8 MFMA stem kernel over a space-to-depth copy of the input built in LDS:
+                          int8 output only, groups 1, stride 2, dilation 1, 1 <= c <= 4, k % 64 ==
+                          0, ceil(r/2) * ceil(s/2) <= 16, w*c % 16 == 0, output width <= 112,
+                          16-byte aligned tensors, bias and scales */
 } miq_algo;
 
 /* Same member order and layout as Conv2DParams (/root/reference/src/conv_types.h:21-29). */

@@ -35,13 +35,15 @@ MIQ_ALGO_FLAT = 7
 MIQ_ALGO_DOT4 = 8
 MIQ_ALGO_PIPE = 9
 MIQ_ALGO_POINTWISE = 10
+MIQ_ALGO_STEM_S2D = 11
 
 # miq_f32_kernel: the fp32 passes' kernel families (miq_plan_f32)
 F32_KERNEL_NAMES = {0: "direct", 1: "igemm", 2: "igemm32", 3: "depthwise", 4: "bprop_igemm", 5: "grad_igemm",
                     6: "grad_depthwise"}
 ALGOS = {"auto": MIQ_ALGO_AUTO, "direct": MIQ_ALGO_DIRECT, "igemm": MIQ_ALGO_IGEMM, "stem": MIQ_ALGO_STEM,
          "band": MIQ_ALGO_BAND, "stream": MIQ_ALGO_STREAM, "flat": MIQ_ALGO_FLAT, "dot4": MIQ_ALGO_DOT4,
-         "pipe": MIQ_ALGO_PIPE, "pointwise": MIQ_ALGO_POINTWISE}
+         "pipe": MIQ_ALGO_PIPE, "pointwise": MIQ_ALGO_POINTWISE,
+         "stem_s2d": MIQ_ALGO_STEM_S2D}
 ALGO_NAMES = {v: k for k, v in ALGOS.items()}
 
 

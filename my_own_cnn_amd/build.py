@@ -28,6 +28,7 @@ SOURCES = [
     "qconv_direct.hip",
     "qconv_igemm.hip",
     "qconv_stem.hip",
+    "qconv_stem_s2d.hip",
     "qconv_band.hip",
     "qconv_stream.hip",
     "qconv_flat.hip",

@@ -299,6 +299,8 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
         *algo = MIQ_ALGO_DOT4;
       } else if (miq::igemm_eligible(*g, x, w, y, epi, nullptr)) {
         *algo = MIQ_ALGO_IGEMM;
+      } else if (miq::stem_s2d_eligible(*g, x, w, y, rq, epi, nullptr)) {
+        *algo = MIQ_ALGO_STEM_S2D;
       } else if (miq::stem_eligible(*g, x, w, y, epi, nullptr)) {
         *algo = MIQ_ALGO_STEM;
       } else {
@@ -340,6 +342,10 @@ int plan_i8(const miq_qconv_desc* d, const void* x, const void* w, const void* y
       if (!miq::pointwise_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       *algo = MIQ_ALGO_POINTWISE;
       break;
+    case MIQ_ALGO_STEM_S2D:
+      if (!miq::stem_s2d_eligible(*g, x, w, y, rq, epi, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      *algo = MIQ_ALGO_STEM_S2D;
+      break;
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "unknown algo value");
   }
@@ -374,6 +380,7 @@ int i8_entry(miq::Epi epi, const miq_qconv_desc* d, const int8_t* x, const int8_
     case MIQ_ALGO_DOT4: e = miq::launch_i8_dot4(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_PIPE: e = miq::launch_i8_pipe(g, epi, x, w, y, rq, s); break;
     case MIQ_ALGO_POINTWISE: e = miq::launch_i8_pointwise(g, x, w, static_cast<int8_t*>(y), rq, s); break;
+    case MIQ_ALGO_STEM_S2D: e = miq::launch_i8_stem_s2d(g, x, w, static_cast<int8_t*>(y), rq, s); break;
     default: e = miq::launch_i8_direct(g, epi, x, w, y, rq, s); break;
   }
   if (e != hipSuccess) return hip_fail(e, "int8 convolution launch");

@@ -109,32 +109,70 @@ __device__ __forceinline__ v4i lds_read16(unsigned addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>(static_cast<uintptr_t>(addr));
 }
 
-// int8 output of one lane: channels kc0 .. kc0 + 15 of one pixel, accumulators biased.
-// Each value is clamped, then rounded to nearest even by adding 1.5 * 2^23, which leaves
-// rint(v) in two's complement in the low mantissa bits; an SDWA v_add_f32 writes the low
-// byte of that sum straight into byte r of the packed word (dst_sel BYTE_r, the other bytes
-// preserved), so no v_perm_b32 / v_or_b32 packing is needed (12 fewer VALU operations per
-// 16 values).
+// Four rounded values (each v + 1.5 * 2^23, so that its low byte is rint(v) in two's
+// complement for |v| <= 128) packed into one word, low bytes in order: two v_perm_b32 and an
+// or.
+__device__ __forceinline__ unsigned pack4_magic(float a, float b, float c, float d) {
+  return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x0c0c0400u) |
+         __builtin_amdgcn_perm(__float_as_uint(d), __float_as_uint(c), 0x04000c0cu);
+}
+
+// The int8 output stage of one value: clamp(rint(float(acc) * m), lo, 127) (lo = -128, or 0
+// with ReLU), computed as med3(v, lo, 127) + 1.5 * 2^23: the bounds are integers, so clamping
+// first equals rounding first, and the addition rounds to nearest even and leaves rint in the
+// low byte.  v_med3_f32 returns its lower bound for a NaN input (the NaN rule of the
+// reference's saturation).  Every step writes a fresh register: read-modify-write packing of
+// one register (SDWA byte writes, v_cvt_pk_u8_f32 into a partly filled word) was measured to
+// stall the wave behind the matrix instructions in flight, and took the overlap of MFMA and
+// VALU work away.
+__device__ __forceinline__ float requant_magic(int acc, float m, float lo) {
+  return __builtin_amdgcn_fmed3f(static_cast<float>(acc) * m, lo, 127.0f) + 12582912.0f;
+}
+
+// int8 output of one lane: channels kc0 .. kc0 + 15 of one pixel (accumulator word j, value r
+// = channel 4j + r), accumulators biased.
 __device__ __forceinline__ v4i pack_i8(const v4i (&acc)[4], const v4f (&mult)[4], float lo) {
-  const float magic = 12582912.0f;
   v4i pk;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float c[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) c[r] = __builtin_amdgcn_fmed3f(static_cast<float>(acc[j][r]) * mult[j][r], lo, 127.0f);
-    unsigned u;
-    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
-        : "=v"(u) : "v"(c[0]), "v"(magic));
-    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-        : "+v"(u) : "v"(c[1]), "v"(magic));
-    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-        : "+v"(u) : "v"(c[2]), "v"(magic));
-    asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-        : "+v"(u) : "v"(c[3]), "v"(magic));
-    pk[j] = static_cast<int>(u);
+    for (int r = 0; r < 4; ++r) c[r] = requant_magic(acc[j][r], mult[j][r], lo);
+    pk[j] = static_cast<int>(pack4_magic(c[0], c[1], c[2], c[3]));
   }
   return pk;
+}
+
+// Values V .. VE - 1 (V = 4j + r) of a lane's 16 through requant_magic into f; each completed
+// word (r == 3) is packed into pk[j].
+template <int V, int VE>
+__device__ __forceinline__ void requant_values(const v4i (&acc)[4], const v4f (&mult)[4], float lo, float (&f)[16],
+                                               unsigned (&pk)[4]) {
+  if constexpr (V < VE) {
+    f[V] = requant_magic(acc[V / 4][V % 4], mult[V / 4][V % 4], lo);
+    if constexpr (V % 4 == 3) pk[V / 4] = pack4_magic(f[V - 3], f[V - 2], f[V - 1], f[V]);
+    requant_values<V + 1, VE>(acc, mult, lo, f, pk);
+  }
+}
+
+// One software-pipelined segment step of the filter-stationary int8 kernels: the KB x 4
+// MFMAs of the next segment (K-block I / 4, row block I % 4; the first K-block starts from the
+// bias) each followed by its share of the current segment's 16 output values, with a
+// scheduling barrier after each pair, so that each wave's output stage issues while its own
+// matrix instructions execute.  (Left to itself the compiler puts all matrix instructions
+// first and the output stage after them.)
+template <int KB, int I = 0>
+__device__ __forceinline__ void mma_requant_steps(const v4i (&A)[KB][4], const v4i (&B)[KB], const v4i (&bias)[4],
+                                                  v4i (&accn)[4], const v4i (&acc)[4], const v4f (&mult)[4], float lo,
+                                                  float (&f)[16], unsigned (&pk)[4]) {
+  if constexpr (I < 4 * KB) {
+    constexpr int b = I / 4;
+    constexpr int j = I % 4;
+    accn[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][j], B[b], b == 0 ? bias[j] : accn[j], 0, 0, 0);
+    requant_values<I * 16 / (4 * KB), (I + 1) * 16 / (4 * KB)>(acc, mult, lo, f, pk);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_requant_steps<KB, I + 1>(A, B, bias, accn, acc, mult, lo, f, pk);
+  }
 }
 
 // Wait states after a 16-byte store before another instruction may overwrite its data
@@ -150,23 +188,9 @@ __device__ __forceinline__ void store_gap(const V& data) {
   asm volatile("s_nop 1" : : "v"(data) : "memory");
 }
 
-// With ReLU the int8 result is clamp(rint(v), 0, 127) (NaN -> 0), so v_cvt_pk_u8_f32 --
-// round to nearest even, saturate to [0, 255], NaN -> 0 (checked on the device against
-// rint for ties, near-ties, NaN and infinities) -- rounds and packs each value of
-// med3(v, 0, 127) in one instruction.
+// With ReLU the int8 result is clamp(rint(v), 0, 127) (NaN -> 0): pack_i8 with lower bound 0.
 __device__ __forceinline__ v4i pack_u8_relu(const v4i (&acc)[4], const v4f (&mult)[4]) {
-  v4i pk;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    unsigned u = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = __builtin_amdgcn_fmed3f(static_cast<float>(acc[j][r]) * mult[j][r], 0.0f, 127.0f);
-      u = __builtin_amdgcn_cvt_pk_u8_f32(v, static_cast<unsigned>(r), u);
-    }
-    pk[j] = static_cast<int>(u);
-  }
-  return pk;
+  return pack_i8(acc, mult, 0.0f);
 }
 
 // Returns a copy of a kernel-argument struct with every 32-bit word already in an SGPR.

@@ -274,17 +274,10 @@ __global__ void __launch_bounds__(64 * kFlatWaves, 1) i8_flat_kernel(FlatArgs a_
   // one output value (j, r) of a 16-channel accumulator set: packing state in pk / u4
   auto epi_value = [&](const v4i (&acc)[4], int j, int r, const v4f& mj, v4i& pk, unsigned (&u4)[4], unsigned off) {
     if constexpr (EPI == kEpiI8) {
-      const float v = static_cast<float>(acc[j][r]) * mj[r];
-      if constexpr (RELU) {
-        pk[j] = static_cast<int>(__builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(v, 0.0f, 127.0f),
-                                                                 static_cast<unsigned>(r),
-                                                                 r == 0 ? 0u : static_cast<unsigned>(pk[j])));
-      } else {
-        u4[r] = __float_as_uint(__builtin_amdgcn_fmed3f(v, lo, 127.0f) + 12582912.0f);
-        if (r == 3)
-          pk[j] = static_cast<int>(__builtin_amdgcn_perm(u4[1], u4[0], 0x0c0c0400u) |
-                                   __builtin_amdgcn_perm(u4[3], u4[2], 0x04000c0cu));
-      }
+      u4[r] = __float_as_uint(requant_magic(acc[j][r], mj[r], lo));
+      if (r == 3)
+        pk[j] = static_cast<int>(pack4_magic(__uint_as_float(u4[0]), __uint_as_float(u4[1]), __uint_as_float(u4[2]),
+                                             __uint_as_float(u4[3])));
       if (j == 3 && r == 3) {
         __builtin_amdgcn_raw_buffer_store_b128(pk, ry, off, 0, kStoreAux);
         store_gap(pk);
@@ -310,17 +303,10 @@ __global__ void __launch_bounds__(64 * kFlatWaves, 1) i8_flat_kernel(FlatArgs a_
   auto tail_epilogue = [&](const v4i& tacc, unsigned off) {
     if constexpr (EPI == kEpiI8) {
       const v4f m = mult_of(simd);
-      unsigned u = 0, u4[4];
+      float c[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float v = static_cast<float>(tacc[r]) * m[r];
-        if constexpr (RELU) {
-          u = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(v, 0.0f, 127.0f), static_cast<unsigned>(r), u);
-        } else {
-          u4[r] = __float_as_uint(__builtin_amdgcn_fmed3f(v, lo, 127.0f) + 12582912.0f);
-        }
-      }
-      if constexpr (!RELU) u = __builtin_amdgcn_perm(u4[1], u4[0], 0x0c0c0400u) | __builtin_amdgcn_perm(u4[3], u4[2], 0x04000c0cu);
+      for (int r = 0; r < 4; ++r) c[r] = requant_magic(tacc[r], m[r], lo);
+      const unsigned u = pack4_magic(c[0], c[1], c[2], c[3]);
       __builtin_amdgcn_raw_buffer_store_b32(static_cast<int>(u), ry, off, 0, kStoreAux);
       asm volatile("s_nop 1" : : "v"(u) : "memory");
     } else if constexpr (EPI == kEpiAcc32) {

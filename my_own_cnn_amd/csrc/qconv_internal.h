@@ -139,6 +139,13 @@ bool pipe_eligible(const Geom& g, const void* x, const void* w, const void* y, c
 hipError_t launch_i8_pipe(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                           hipStream_t stream);
 
+// int8 MFMA stem kernel over a space-to-depth copy of the input (stride 2, 1 <= C <= 4, groups 1,
+// K % 64 == 0, ceil(R/2) * ceil(S/2) <= 16, int8 output).
+bool stem_s2d_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                       std::string* why);
+hipError_t launch_i8_stem_s2d(const Geom& g, const int8_t* x, const int8_t* w, int8_t* y, const Requant& rq,
+                              hipStream_t stream);
+
 // int8 MFMA pointwise kernel (1x1, stride 1, no padding, groups 1, C 64 or 128, K % 64 == 0):
 // a GEMM over the flattened pixels with the input streamed into LDS by a loader wave.
 bool pointwise_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,

@@ -106,37 +106,15 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 // 8 requantized outputs of one lane (channels 4j + i of its 8, j = 0, 1) as two packed dwords.
 template <bool RELU>
 __device__ __forceinline__ void pack8(const v4i& a0, const v4i& a1, const v4f (&m)[2], unsigned& d0, unsigned& d1) {
-  const v4i* acc[2] = {&a0, &a1};
-  unsigned d[2];
+  const float lo = RELU ? 0.0f : -128.0f;
+  float c[8];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    if constexpr (RELU) {
-      unsigned u = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = __builtin_amdgcn_fmed3f(static_cast<float>((*acc[j])[i]) * m[j][i], 0.0f, 127.0f);
-        u = __builtin_amdgcn_cvt_pk_u8_f32(v, static_cast<unsigned>(i), u);
-      }
-      d[j] = u;
-    } else {
-      const float magic = 12582912.0f;
-      float c[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) c[i] = __builtin_amdgcn_fmed3f(static_cast<float>((*acc[j])[i]) * m[j][i], -128.0f, 127.0f);
-      unsigned u;
-      asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD"
-          : "=v"(u) : "v"(c[0]), "v"(magic));
-      asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-          : "+v"(u) : "v"(c[1]), "v"(magic));
-      asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-          : "+v"(u) : "v"(c[2]), "v"(magic));
-      asm("v_add_f32_sdwa %0, %1, %2 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD"
-          : "+v"(u) : "v"(c[3]), "v"(magic));
-      d[j] = u;
-    }
+  for (int i = 0; i < 4; ++i) {
+    c[i] = requant_magic(a0[i], m[0][i], lo);
+    c[4 + i] = requant_magic(a1[i], m[1][i], lo);
   }
-  d0 = d[0];
-  d1 = d[1];
+  d0 = pack4_magic(c[0], c[1], c[2], c[3]);
+  d1 = pack4_magic(c[4], c[5], c[6], c[7]);
 }
 
 // s_waitcnt vmcnt(n) for a compile-time 0 <= n <= 63 (bits 3:0 and 15:14 of the immediate).

@@ -283,8 +283,8 @@ __global__ void __launch_bounds__(kPwThreads) i8_pointwise_kernel(PwArgs a_in) {
     store_gap(pk);
     yoff += ystep;
   };
-  // Software-pipelined by one segment: the matrix instructions of the next segment are
-  // issued before the requantization of this one, so the two overlap.
+  // Software-pipelined by one segment: each matrix instruction of the next segment is issued
+  // with a share of this segment's output stage (mma_requant_steps), so the two overlap.
   int s = st;
   if (s < nseg) {
     v4i acc[4];
@@ -293,10 +293,19 @@ __global__ void __launch_bounds__(kPwThreads) i8_pointwise_kernel(PwArgs a_in) {
     for (;;) {
       const int sn = s + kStreams;
       if (sn >= nseg) break;
-      v4i accn[4];
       wait_seg(sn);
-      mma(sn, accn);
-      emit(acc);
+      v4i B[KB];
+#pragma unroll
+      for (int b = 0; b < KB; ++b) B[b] = lds_read16(boff[b] + static_cast<unsigned>(sn) * kSegBytes);
+      v4i accn[4];
+      unsigned pk[4];
+      float f[16];
+      mma_requant_steps<KB>(A, B, bias_v, accn, acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+      const v4i pkv = {static_cast<int>(pk[0]), static_cast<int>(pk[1]), static_cast<int>(pk[2]),
+                       static_cast<int>(pk[3])};
+      __builtin_amdgcn_raw_buffer_store_b128(pkv, ry, yoff, 0, kStoreAux);
+      store_gap(pkv);
+      yoff += ystep;
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[j] = accn[j];
       s = sn;

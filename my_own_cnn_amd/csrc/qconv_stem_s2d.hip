@@ -1,0 +1,445 @@
+// int8 convolution for stride-2 thin-channel stems (c <= 4, e.g. the ResNet 7x7/2 stem with
+// c = 3) as a stride-1 convolution over a space-to-depth copy of the input built in LDS.
+//
+// Space to depth.  S2D pixel (I, J) holds the 2 x 2 input pixels (2I + a - ph, 2J + b - pw),
+// a, b in {0, 1}, c bytes each, in the order (a, b, channel), zero-padded to 16 bytes (one
+// MFMA chunk).  Output pixel (ho, wo) then reads the ceil(r/2) x ceil(s/2) s2d pixels
+// (ho + u, wo + v): tap (u, v) is one 16-byte chunk whose byte (2a + b)*c + ch meets filter
+// element (2u + a, 2v + b, ch), zero where 2u + a >= r or 2v + b >= s.  The reduction has
+// T = ceil(r/2) * ceil(s/2) chunks, KB = ceil(T/4) K-blocks of v_mfma_i32_16x16x64_i8 (the
+// 7x7 stem: 16 chunks, 4 K-blocks), and every MFMA operand is one aligned 16-byte LDS read:
+// lane (rho, g) of K-block kb reads chunk q = 4kb + g at s2d pixel (ho + q / V, wo0 + rho +
+// q % V).  Consecutive lanes read consecutive s2d pixels of one row, which the LDS serves
+// without bank conflicts (lanes that meet read the same address).
+//
+// Work.  A workgroup of 8 waves owns a band of BH output rows of one image and 64 output
+// channels.  It loads the band's 2 * (BH + ceil(r/2) - 1) input rows (global -> LDS DMA,
+// 1 KB per instruction, zeros outside the image) and the 64 channels' filter bytes, then
+// builds the s2d rows and the filter chunks (operand slots, swizzled so that every fragment
+// read is free of bank conflicts) with VALU work once per byte, and keeps the filter
+// fragments in registers.  Each wave then takes 16-pixel segments of the band's output rows
+// in turn; the matrix instructions of the next segment are issued before the requantization
+// of the current one, so the two overlap.  The output stage is the other int8 kernels'
+// (bias as the first MFMA's C operand; convert, scale, clamp, round; one 16-byte store of
+// 16 consecutive channels per lane, followed by store_gap()).
+
+#include "qconv_device.h"
+
+#include <algorithm>
+#include <atomic>
+
+namespace miq {
+namespace {
+
+constexpr int kSdWaves = 8;
+constexpr int kSdLds = 160 * 1024;
+constexpr int kSdPitch = 2048;  // bytes per staged s2d row: up to 128 s2d pixels
+
+struct S2dArgs {
+  const int8_t* x;
+  const int8_t* w;
+  const int32_t* bias;
+  const float* wscale;
+  int8_t* y;
+  int H, W, C, K, R, S, Ho, Wo, ph, pw;
+  int V, T;             // s2d taps per row (ceil(s/2)) and in all (ceil(r/2) * V)
+  int BH, bands_per_img, nbands, nblocks, SEGR;
+  int P, PLB, rows_ld;  // staged input row pitch (a multiple of 1 KB), its left pad, loads per row
+  int HS, ncols;        // s2d rows per band and s2d columns built per row
+  int RSC, nfilt;       // filter bytes per channel, filter load instructions
+  int filt_lds, ep_lds, slot_lds, raw_lds, s2d_lds;
+  float act_scale;
+  FastDivM fd_nbands, fd_bpi, fd_segr, fd_rowsld, fd_ncols;
+};
+
+static_assert(sizeof(S2dArgs) <= 256, "kernel arguments fit one s_load batch");
+
+// 8 bytes of an LDS byte array from byte o (any alignment), as two dwords.
+__device__ __forceinline__ unsigned long long lds_bytes8(const unsigned char* base, int o) {
+  const unsigned* p = reinterpret_cast<const unsigned*>(base + (o & ~3));
+  const unsigned sh = static_cast<unsigned>(o & 3);
+  const unsigned d0 = p[0], d1 = p[1], d2 = p[2];
+  const unsigned lo = __builtin_amdgcn_alignbyte(d1, d0, sh);
+  const unsigned hi = __builtin_amdgcn_alignbyte(d2, d1, sh);
+  return static_cast<unsigned long long>(lo) | (static_cast<unsigned long long>(hi) << 32);
+}
+
+// Filter chunk q of channel kl sits at 16-byte slot 16 kl + ((q + kl + 4 (kl / 16)) mod 16): the
+// 16 lanes of an MFMA lane group read 16 distinct slots modulo 16.
+__device__ __forceinline__ int s2d_slot(int kl, int q) { return 16 * kl + ((q + kl + 4 * (kl >> 4)) & 15); }
+
+// 2C bytes (C <= 4) from byte o of an LDS byte array (any alignment), in the low bytes.
+template <int C>
+__device__ __forceinline__ unsigned long long lds_pair(const unsigned char* base, int o) {
+  constexpr unsigned long long keep = C == 4 ? ~0ull : ((1ull << (16 * C)) - 1ull);
+  return lds_bytes8(base, o) & keep;
+}
+
+// One 16-byte chunk from two 2C-byte pieces: bytes [0, 2C) from lo, [2C, 4C) from hi, zeros
+// after.
+template <int C>
+__device__ __forceinline__ v4i s2d_chunk(unsigned long long lo, unsigned long long hi) {
+  unsigned long long w0, w1;
+  if constexpr (C == 4) {
+    w0 = lo;
+    w1 = hi;
+  } else {
+    w0 = lo | (hi << (16 * C));
+    w1 = hi >> (64 - 16 * C);
+  }
+  return v4i{static_cast<int>(w0), static_cast<int>(w0 >> 32), static_cast<int>(w1), static_cast<int>(w1 >> 32)};
+}
+
+// The 64 channels' filter chunks: chunk q = tap (u, v) = (q / V, q % V), for a = 0, 1 the 2C
+// bytes of filter row 2u + a, columns 2v and 2v + 1 (contiguous in KRSC); a column 2v + 1 = s
+// or a row 2u + a >= r contributes zeros; chunks past T are zero.
+template <int C>
+__device__ __forceinline__ void s2d_filter(const S2dArgs& a, const unsigned char* bytes, v4i* lds, int tid) {
+  const unsigned char* fb = bytes + a.filt_lds;
+  v4i* slots = lds + a.slot_lds / 16;
+  const int rowc = a.S * C;  // bytes of one filter row
+  for (int idx = tid; idx < 64 * 16; idx += 64 * kSdWaves) {
+    const int kl = idx >> 4;
+    const int q = idx & 15;
+    unsigned long long piece[2] = {0ull, 0ull};
+    if (q < a.T) {
+      const int u = q / a.V;
+      const int v = q - u * a.V;
+      // the second column of the pair exists unless 2v + 1 == s
+      const unsigned long long keep = 2 * v + 1 < a.S ? ~0ull : ((1ull << (8 * C)) - 1ull);
+#pragma unroll
+      for (int r2 = 0; r2 < 2; ++r2) {
+        const int r = 2 * u + r2;
+        if (r < a.R) piece[r2] = lds_pair<C>(fb, kl * a.RSC + r * rowc + 2 * v * C) & keep;
+      }
+    }
+    slots[s2d_slot(kl, q)] = s2d_chunk<C>(piece[0], piece[1]);
+  }
+}
+
+// The band's s2d rows: pixel (I, J) from staged input rows 2I and 2I + 1, 2C bytes each at
+// byte PLB + (2J - pw) * C.  Four pixels per thread and pass, their reads issued before their
+// writes (the compiler keeps LDS writes and later LDS reads in order).
+template <int C>
+__device__ __forceinline__ void s2d_rows(const S2dArgs& a, const unsigned char* bytes, v4i* lds, int tid) {
+  constexpr int kU = 4;
+  const unsigned char* raw = bytes + a.raw_lds;
+  const int total = a.HS * a.ncols;
+  for (int idx0 = tid; idx0 < total; idx0 += kU * 64 * kSdWaves) {
+    unsigned long long r0[kU], r1[kU];
+    int dst[kU];
+#pragma unroll
+    for (int e = 0; e < kU; ++e) {
+      const int idx = min(idx0 + e * 64 * kSdWaves, total - 1);  // repeats the last pixel past the end
+      const int I = fdiv(idx, a.fd_ncols);
+      const int J = idx - I * a.ncols;
+      const int o = a.PLB + (2 * J - a.pw) * C;
+      r0[e] = lds_pair<C>(raw + (2 * I) * a.P, o);
+      r1[e] = lds_pair<C>(raw + (2 * I + 1) * a.P, o);
+      dst[e] = (a.s2d_lds + I * kSdPitch) / 16 + J;
+    }
+#pragma unroll
+    for (int e = 0; e < kU; ++e) lds[dst[e]] = s2d_chunk<C>(r0[e], r1[e]);
+  }
+}
+
+template <int KB, bool RELU>
+__global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a_in) {
+  const S2dArgs a = preload_args(a_in);
+  extern __shared__ v4i sd_lds[];
+  const unsigned char* bytes = reinterpret_cast<const unsigned char*>(sd_lds);
+  const unsigned base = static_cast<unsigned>(reinterpret_cast<uintptr_t>(sd_lds) & 0xffffffffu);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rho = lane & 15;
+  const int g = lane >> 4;
+
+  const int lin = xcd_tile(blockIdx.x, a.nblocks);
+  const int ctile = fdiv(lin, a.fd_nbands);
+  const int band = lin - ctile * a.nbands;
+  const int n = fdiv(band, a.fd_bpi);
+  const int bi = band - n * a.bands_per_img;
+  const int k0 = ctile * 64;
+  const int ho0 = bi * a.BH;
+  const int band_rows = min(a.BH, a.Ho - ho0);
+
+  // ---- loads: filter instruction f (bytes [1024f + 16l, +16) of the tile's 64 * RSC
+  // contiguous KRSC bytes) and input instruction i = row * rows_ld + m go to wave f % 8 and
+  // i % 8; bias and scales to wave 0.  Input row rr of the band is image row 2*ho0 - ph + rr;
+  // staged row byte PLB + b holds row byte b (zeros outside the image).
+  {
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + static_cast<size_t>(k0) * a.RSC, 64 * a.RSC);
+    for (int f = wave; f < a.nfilt; f += kSdWaves)
+      load_lds16(rw, sd_lds + a.filt_lds / 16 + f * 64, 16u * lane, 1024u * f);
+  }
+  if (wave == 0) {
+    load_lds16(make_rsrc(a.bias ? a.bias + k0 : nullptr, a.bias ? 256 : 0), sd_lds + a.ep_lds / 16, 16u * lane, 0);
+    load_lds16(make_rsrc(a.wscale + k0, 256), sd_lds + a.ep_lds / 16 + 64, 16u * lane, 0);
+  }
+  {
+    const int rowb = a.W * a.C;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + static_cast<size_t>(n) * a.H * rowb, a.H * rowb);
+    const int hi0 = 2 * ho0 - a.ph;
+    const int ni = 2 * a.HS * a.rows_ld;
+    for (int i = wave; i < ni; i += kSdWaves) {
+      const int rr = fdiv(i, a.fd_rowsld);
+      const int m = i - rr * a.rows_ld;
+      const int hi = hi0 + rr;
+      const int b = 1024 * m + 16 * lane - a.PLB;
+      const unsigned soff =
+          static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) ? static_cast<unsigned>(hi * rowb) : 0x40000000u;
+      const unsigned voff = (b >= 0 && b + 16 <= rowb) ? static_cast<unsigned>(b) : 0x40000000u;
+      load_lds16(rx, sd_lds + a.raw_lds / 16 + i * 64, voff, soff);
+    }
+  }
+  wait_vmcnt(0);
+  barrier_only();
+
+  // ---- filter chunks, then (while the fragments are read) the s2d rows; compile-time channel
+  // count ----
+  switch (a.C) {
+    case 1: s2d_filter<1>(a, bytes, sd_lds, tid); break;
+    case 2: s2d_filter<2>(a, bytes, sd_lds, tid); break;
+    case 3: s2d_filter<3>(a, bytes, sd_lds, tid); break;
+    default: s2d_filter<4>(a, bytes, sd_lds, tid); break;
+  }
+  __syncthreads();
+
+  // filter fragments: A[kb][j], lane (rho, g) = channel 16*(rho/4) + 4j + rho%4, chunk 4kb + g
+  v4i A[KB][4];
+  {
+    const v4i* slots = sd_lds + a.slot_lds / 16;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) A[kb][j] = slots[s2d_slot(16 * (rho >> 2) + 4 * j + (rho & 3), 4 * kb + g)];
+  }
+  // bias and requantization multipliers of the lane's channels k0 + 16g + 4j + i
+  v4i bias_v[4];
+  v4f mult_v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bias_v[j] = sd_lds[a.ep_lds / 16 + 4 * g + j];
+    const v4i ws = sd_lds[a.ep_lds / 16 + 64 + 4 * g + j];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mult_v[j][i] = requant_multiplier(a.act_scale, __int_as_float(ws[i]));
+  }
+  switch (a.C) {
+    case 1: s2d_rows<1>(a, bytes, sd_lds, tid); break;
+    case 2: s2d_rows<2>(a, bytes, sd_lds, tid); break;
+    case 3: s2d_rows<3>(a, bytes, sd_lds, tid); break;
+    default: s2d_rows<4>(a, bytes, sd_lds, tid); break;
+  }
+  __syncthreads();
+  // this lane's B chunk of K-block kb within a segment: s2d row offset u * pitch, column
+  // rho + v (chunks past T read tap T - 1, whose filter chunk is zero)
+  unsigned boff[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int q = min(4 * kb + g, a.T - 1);
+    const int u = q / a.V;
+    const int v = q - u * a.V;
+    boff[kb] = base + static_cast<unsigned>(a.s2d_lds + u * kSdPitch + 16 * (rho + v));
+  }
+  const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + k0;
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + out0, band_rows * a.Wo * a.K);
+  const int nseg = band_rows * a.SEGR;
+
+  // Software-pipelined by one segment: each matrix instruction of the next segment is issued
+  // with a share of this segment's output stage (mma_requant_steps), so the two overlap.
+  auto seg_b = [&](int sg, v4i (&B)[KB]) {
+    const int t = fdiv(sg, a.fd_segr);
+    const int wo0 = 16 * (sg - t * a.SEGR);
+    const unsigned so = static_cast<unsigned>(t * kSdPitch + 16 * wo0);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) B[kb] = lds_read16(boff[kb] + so);
+  };
+  auto store = [&](int sg, const unsigned (&pk)[4]) {
+    const int t = fdiv(sg, a.fd_segr);
+    const int wo = 16 * (sg - t * a.SEGR) + rho;
+    const v4i pkv = {static_cast<int>(pk[0]), static_cast<int>(pk[1]), static_cast<int>(pk[2]),
+                     static_cast<int>(pk[3])};
+    // a pixel past the row's end gets an offset 2^30 higher: past num_records, dropped
+    const unsigned voff = static_cast<unsigned>((t * a.Wo + wo) * a.K + 16 * g) + (static_cast<unsigned>(wo >= a.Wo) << 30);
+    __builtin_amdgcn_raw_buffer_store_b128(pkv, ry, voff, 0, kStoreAux);
+    store_gap(pkv);
+  };
+  int sg = wave;
+  if (sg < nseg) {
+    v4i acc[4];
+    {
+      v4i B[KB];
+      seg_b(sg, B);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0][j], B[0], bias_v[j], 0, 0, 0);
+#pragma unroll
+      for (int kb = 1; kb < KB; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[kb][j], B[kb], acc[j], 0, 0, 0);
+    }
+    for (;;) {
+      const int sn = sg + kSdWaves;
+      if (sn >= nseg) break;
+      v4i B[KB];
+      seg_b(sn, B);
+      v4i accn[4];
+      unsigned pk[4];
+      float f[16];
+      mma_requant_steps<KB>(A, B, bias_v, accn, acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+      store(sg, pk);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = accn[j];
+      sg = sn;
+    }
+    unsigned pk[4];
+    float f[16];
+    requant_values<0, 16>(acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+    store(sg, pk);
+  }
+}
+
+struct S2dPlan {
+  int V, T, KB, BH, bands_per_img, HS, ncols, P, PLB, rows_ld, nfilt;
+  int filt_lds, ep_lds, slot_lds, raw_lds, s2d_lds;
+  size_t lds;
+};
+
+int sd_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+int sd_round_up(long long v, int m) { return static_cast<int>((v + m - 1) / m * m); }
+
+bool sd_plan(const Geom& g, S2dPlan* p, std::string* why) {
+  auto no = [&](const char* m) {
+    if (why) *why = m;
+    return false;
+  };
+  if (g.G != 1) return no("s2d stem kernel needs groups == 1");
+  if (g.sh != 2 || g.sw != 2) return no("s2d stem kernel needs stride 2");
+  if (g.dh != 1 || g.dw != 1) return no("s2d stem kernel needs dilation 1");
+  if (g.C < 1 || g.C > 4) return no("s2d stem kernel needs 1 <= c <= 4");
+  if (g.ph < 0 || g.pw < 0 || g.R < 1 || g.S < 1) return no("s2d stem kernel needs a filter and padding >= 0");
+  if (g.K % 64 != 0) return no("s2d stem kernel needs k % 64 == 0");
+  p->V = (g.S + 1) / 2;
+  p->T = ((g.R + 1) / 2) * p->V;
+  if (p->T > 16) return no("s2d stem kernel needs ceil(r/2) * ceil(s/2) <= 16");
+  p->KB = (p->T + 3) / 4;
+  const long long rowb = static_cast<long long>(g.W) * g.C;
+  if (rowb % 16 != 0) return no("s2d stem kernel needs w * c % 16 == 0");
+  if (static_cast<long long>(g.H) * rowb >= (1LL << 30)) return no("s2d stem kernel needs images below 2^30 bytes");
+  if (static_cast<long long>(g.Ho) * g.Wo * g.K >= (1LL << 30)) return no("s2d stem kernel needs outputs below 2^30 bytes");
+  const int segr = (g.Wo + 15) / 16;
+  p->ncols = 16 * segr + p->V - 1;
+  if (p->ncols > kSdPitch / 16) return no("s2d stem kernel needs output width + ceil(s/2) <= 113");
+  p->PLB = sd_round_up(static_cast<long long>(g.pw) * g.C, 16);
+  // the last byte a conversion read touches: 12 bytes from the last column's first byte
+  const long long last = p->PLB + (2LL * (p->ncols - 1) - g.pw) * g.C + 12;
+  p->P = sd_round_up(std::max<long long>(p->PLB + rowb, last), 1024);
+  p->rows_ld = p->P / 1024;
+  const long long RSC = static_cast<long long>(g.R) * g.S * g.C;
+  p->nfilt = static_cast<int>((64 * RSC + 1023) / 1024);
+  const int cus = sd_cu_count();
+  // filter bytes, 2 KB of bias and scales, 16 KB of operand slots, then per band the staged
+  // input rows and the s2d rows
+  const size_t fixed = static_cast<size_t>(p->nfilt) * 1024 + 2048 + 16384;
+  const int Ru = (g.R + 1) / 2;
+  bool found = false;
+  double best = 0.0;
+  for (int bh = 1; bh <= g.Ho; ++bh) {
+    const long long hs = bh + Ru - 1;
+    const size_t lds = fixed + static_cast<size_t>(2 * hs) * p->P + static_cast<size_t>(hs) * kSdPitch;
+    if (lds > static_cast<size_t>(kSdLds)) break;
+    const long long bands = (g.Ho + bh - 1) / bh;
+    const long long wgs = static_cast<long long>(g.N) * bands * (g.K / 64);
+    const long long rounds = (wgs + cus - 1) / cus;
+    const double cost = static_cast<double>(rounds) * ((bh * segr + kSdWaves - 1) / kSdWaves + 3);
+    if (!found || cost < best - 1e-9) {
+      found = true;
+      best = cost;
+      p->BH = bh;
+      p->bands_per_img = static_cast<int>(bands);
+      p->HS = static_cast<int>(hs);
+      p->lds = lds;
+    }
+  }
+  if (!found) return no("s2d stem kernel band does not fit in LDS");
+  p->filt_lds = 0;
+  p->ep_lds = p->nfilt * 1024;
+  p->slot_lds = p->ep_lds + 2048;
+  p->raw_lds = p->slot_lds + 16384;
+  p->s2d_lds = p->raw_lds + 2 * p->HS * p->P;
+  const long long blocks = static_cast<long long>(g.N) * p->bands_per_img * (g.K / 64);
+  if (blocks > 0x7fffffffLL) return no("grid too large");
+  return true;
+}
+
+bool sd_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+bool stem_s2d_eligible(const Geom& g, const void* x, const void* w, const void* y, const Requant& rq, Epi epi,
+                       std::string* why) {
+  if (epi != kEpiI8) {
+    if (why) *why = "s2d stem kernel: int8 outputs only";
+    return false;
+  }
+  if (!sd_aligned16(x) || !sd_aligned16(w) || !sd_aligned16(y) || !sd_aligned16(rq.wscale) ||
+      (rq.bias && !sd_aligned16(rq.bias))) {
+    if (why) *why = "s2d stem kernel needs 16-byte aligned x, w, y, bias and scales";
+    return false;
+  }
+  S2dPlan pl;
+  return sd_plan(g, &pl, why);
+}
+
+hipError_t launch_i8_stem_s2d(const Geom& g, const int8_t* x, const int8_t* w, int8_t* y, const Requant& rq,
+                              hipStream_t stream) {
+  if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
+  S2dPlan pl;
+  if (!sd_plan(g, &pl, nullptr)) return hipErrorInvalidConfiguration;
+  S2dArgs a;
+  a.x = x; a.w = w; a.bias = rq.bias; a.wscale = rq.wscale; a.y = y;
+  a.H = g.H; a.W = g.W; a.C = g.C; a.K = g.K; a.R = g.R; a.S = g.S; a.Ho = g.Ho; a.Wo = g.Wo;
+  a.ph = g.ph; a.pw = g.pw;
+  a.V = pl.V; a.T = pl.T;
+  a.BH = pl.BH; a.bands_per_img = pl.bands_per_img; a.nbands = g.N * pl.bands_per_img;
+  a.nblocks = a.nbands * (g.K / 64);
+  a.SEGR = (g.Wo + 15) / 16;
+  a.P = pl.P; a.PLB = pl.PLB; a.rows_ld = pl.rows_ld;
+  a.HS = pl.HS; a.ncols = pl.ncols;
+  a.RSC = g.R * g.S * g.C; a.nfilt = pl.nfilt;
+  a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.slot_lds = pl.slot_lds; a.raw_lds = pl.raw_lds;
+  a.s2d_lds = pl.s2d_lds;
+  a.act_scale = rq.act_scale;
+  a.fd_nbands = fastdiv_m(a.nbands);
+  a.fd_bpi = fastdiv_m(pl.bands_per_img);
+  a.fd_segr = fastdiv_m(a.SEGR);
+  a.fd_rowsld = fastdiv_m(pl.rows_ld);
+  a.fd_ncols = fastdiv_m(pl.ncols);
+  auto go = [&](auto kern) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(pl.lds));
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(a.nblocks)), dim3(64 * kSdWaves), pl.lds, stream, a);
+  };
+  const bool relu = rq.relu != 0;
+  switch (pl.KB) {
+    case 1: relu ? go(i8_stem_s2d_kernel<1, true>) : go(i8_stem_s2d_kernel<1, false>); break;
+    case 2: relu ? go(i8_stem_s2d_kernel<2, true>) : go(i8_stem_s2d_kernel<2, false>); break;
+    case 3: relu ? go(i8_stem_s2d_kernel<3, true>) : go(i8_stem_s2d_kernel<3, false>); break;
+    default: relu ? go(i8_stem_s2d_kernel<4, true>) : go(i8_stem_s2d_kernel<4, false>); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace miq

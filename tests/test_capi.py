@@ -173,7 +173,7 @@ def test_python_mirror_errors():
 
 
 @pytest.mark.parametrize("name,algo", [("tiny", "igemm"), ("r50_3x3", "band"), ("r50_1x1", "pointwise"),
-                                       ("down_s2", "stream"), ("stem", "stem")])
+                                       ("down_s2", "stream"), ("stem", "stem_s2d")])
 def test_plan_of_the_workloads(name, algo):
     wl = M.WORKLOADS[name]
     d = M.make_desc((wl.n, wl.h, wl.w, wl.c), (wl.k, wl.r, wl.s, wl.c), stride=wl.stride, padding=wl.pad,
@@ -459,7 +459,7 @@ def test_plan_block_f32():
     (((32, 56, 56, 64), (8, 3, 3, 64), {"padding": 1}), "igemm"),   # 576: the implicit GEMM measured faster
     (((32, 56, 56, 64), (12, 1, 1, 64), {}), "igemm"),         # 12 channels: equal, not taken
     (((32, 56, 56, 64), (16, 1, 1, 64), {}), "band"),          # band kernels win from 16 channels
-    (((32, 224, 224, 3), (64, 7, 7, 3), {"padding": 3, "stride": 2}), "stem"),  # C = 3 stem stays on MFMA
+    (((32, 224, 224, 3), (64, 7, 7, 3), {"padding": 3, "stride": 2}), "stem_s2d"),  # C = 3 stem stays on MFMA
 ])
 def test_auto_takes_the_dot4_kernel_where_it_measured_faster(shape, want):
     xs, ws, kw = shape
@@ -480,6 +480,25 @@ def test_pointwise_planner(xs, ws, kw, ok):
     d = M.make_desc(xs, ws, algo="pointwise", **kw)
     if ok:
         assert M.plan(d) == "pointwise"
+    else:
+        with pytest.raises(M.MiqError):
+            M.plan(d)
+
+
+@pytest.mark.parametrize("xs,ws,kw,ok", [
+    ((32, 224, 224, 3), (64, 7, 7, 3), {"stride": 2, "padding": 3}, True),
+    ((2, 20, 16, 1), (128, 3, 3, 1), {"stride": 2, "padding": 1}, True),
+    ((2, 20, 16, 3), (64, 7, 7, 3), {"stride": 1, "padding": 3}, False),   # stride 1
+    ((2, 20, 16, 8), (64, 3, 3, 8), {"stride": 2, "padding": 1}, False),   # c > 4
+    ((2, 20, 20, 3), (64, 7, 7, 3), {"stride": 2, "padding": 3}, False),   # w * c % 16 != 0
+    ((2, 20, 16, 3), (48, 7, 7, 3), {"stride": 2, "padding": 3}, False),   # k % 64 != 0
+    ((2, 40, 32, 1), (64, 9, 9, 1), {"stride": 2, "padding": 4}, False),   # 5 x 5 s2d taps > 16
+    ((2, 20, 16, 3), (64, 3, 3, 3), {"stride": 2, "padding": 1, "dilation": 2}, False),
+])
+def test_stem_s2d_planner(xs, ws, kw, ok):
+    d = M.make_desc(xs, ws, algo="stem_s2d", **kw)
+    if ok:
+        assert M.plan(d) == "stem_s2d"
     else:
         with pytest.raises(M.MiqError):
             M.plan(d)
