@@ -93,24 +93,28 @@ __device__ __forceinline__ v4i s2d_chunk(unsigned long long lo, unsigned long lo
 // The 64 channels' filter chunks: chunk q = tap (u, v) = (q / V, q % V), for a = 0, 1 the 2C
 // bytes of filter row 2u + a, columns 2v and 2v + 1 (contiguous in KRSC); a column 2v + 1 = s
 // or a row 2u + a >= r contributes zeros; chunks past T are zero.
-template <int C>
+template <int C, int FR, int FS>
 __device__ __forceinline__ void s2d_filter(const S2dArgs& a, const unsigned char* bytes, v4i* lds, int tid) {
+  const int R = FR ? FR : a.R;
+  const int S = FS ? FS : a.S;
+  const int V = FS ? (FS + 1) / 2 : a.V;
+  const int T = FR ? ((FR + 1) / 2) * V : a.T;
   const unsigned char* fb = bytes + a.filt_lds;
   v4i* slots = lds + a.slot_lds / 16;
-  const int rowc = a.S * C;  // bytes of one filter row
+  const int rowc = S * C;  // bytes of one filter row
   for (int idx = tid; idx < 64 * 16; idx += 64 * kSdWaves) {
     const int kl = idx >> 4;
     const int q = idx & 15;
     unsigned long long piece[2] = {0ull, 0ull};
-    if (q < a.T) {
-      const int u = q / a.V;
-      const int v = q - u * a.V;
+    if (q < T) {
+      const int u = q / V;
+      const int v = q - u * V;
       // the second column of the pair exists unless 2v + 1 == s
-      const unsigned long long keep = 2 * v + 1 < a.S ? ~0ull : ((1ull << (8 * C)) - 1ull);
+      const unsigned long long keep = 2 * v + 1 < S ? ~0ull : ((1ull << (8 * C)) - 1ull);
 #pragma unroll
       for (int r2 = 0; r2 < 2; ++r2) {
         const int r = 2 * u + r2;
-        if (r < a.R) piece[r2] = lds_pair<C>(fb, kl * a.RSC + r * rowc + 2 * v * C) & keep;
+        if (r < R) piece[r2] = lds_pair<C>(fb, kl * (R * rowc) + r * rowc + 2 * v * C) & keep;
       }
     }
     slots[s2d_slot(kl, q)] = s2d_chunk<C>(piece[0], piece[1]);
@@ -143,7 +147,9 @@ __device__ __forceinline__ void s2d_rows(const S2dArgs& a, const unsigned char* 
   }
 }
 
-template <int KB, bool RELU>
+// FC, FR, FS: the channel count and filter size when fixed at compile time (the 7x7 stem with
+// three channels), 0 where they come from the arguments.
+template <int KB, bool RELU, int FC, int FR, int FS>
 __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a_in) {
   const S2dArgs a = preload_args(a_in);
   extern __shared__ v4i sd_lds[];
@@ -199,11 +205,15 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
 
   // ---- filter chunks, then (while the fragments are read) the s2d rows; compile-time channel
   // count ----
-  switch (a.C) {
-    case 1: s2d_filter<1>(a, bytes, sd_lds, tid); break;
-    case 2: s2d_filter<2>(a, bytes, sd_lds, tid); break;
-    case 3: s2d_filter<3>(a, bytes, sd_lds, tid); break;
-    default: s2d_filter<4>(a, bytes, sd_lds, tid); break;
+  if constexpr (FC != 0) {
+    s2d_filter<FC, FR, FS>(a, bytes, sd_lds, tid);
+  } else {
+    switch (a.C) {
+      case 1: s2d_filter<1, 0, 0>(a, bytes, sd_lds, tid); break;
+      case 2: s2d_filter<2, 0, 0>(a, bytes, sd_lds, tid); break;
+      case 3: s2d_filter<3, 0, 0>(a, bytes, sd_lds, tid); break;
+      default: s2d_filter<4, 0, 0>(a, bytes, sd_lds, tid); break;
+    }
   }
   __syncthreads();
 
@@ -226,11 +236,15 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
 #pragma unroll
     for (int i = 0; i < 4; ++i) mult_v[j][i] = requant_multiplier(a.act_scale, __int_as_float(ws[i]));
   }
-  switch (a.C) {
-    case 1: s2d_rows<1>(a, bytes, sd_lds, tid); break;
-    case 2: s2d_rows<2>(a, bytes, sd_lds, tid); break;
-    case 3: s2d_rows<3>(a, bytes, sd_lds, tid); break;
-    default: s2d_rows<4>(a, bytes, sd_lds, tid); break;
+  if constexpr (FC != 0) {
+    s2d_rows<FC>(a, bytes, sd_lds, tid);
+  } else {
+    switch (a.C) {
+      case 1: s2d_rows<1>(a, bytes, sd_lds, tid); break;
+      case 2: s2d_rows<2>(a, bytes, sd_lds, tid); break;
+      case 3: s2d_rows<3>(a, bytes, sd_lds, tid); break;
+      default: s2d_rows<4>(a, bytes, sd_lds, tid); break;
+    }
   }
   __syncthreads();
   // this lane's B chunk of K-block kb within a segment: s2d row offset u * pitch, column
@@ -238,9 +252,11 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
   unsigned boff[KB];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
-    const int q = min(4 * kb + g, a.T - 1);
-    const int u = q / a.V;
-    const int v = q - u * a.V;
+    const int V = FS ? (FS + 1) / 2 : a.V;
+    const int T = FR ? ((FR + 1) / 2) * V : a.T;
+    const int q = min(4 * kb + g, T - 1);
+    const int u = q / V;
+    const int v = q - u * V;
     boff[kb] = base + static_cast<unsigned>(a.s2d_lds + u * kSdPitch + 16 * (rho + v));
   }
   const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + k0;
@@ -433,11 +449,15 @@ hipError_t launch_i8_stem_s2d(const Geom& g, const int8_t* x, const int8_t* w, i
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(a.nblocks)), dim3(64 * kSdWaves), pl.lds, stream, a);
   };
   const bool relu = rq.relu != 0;
-  switch (pl.KB) {
-    case 1: relu ? go(i8_stem_s2d_kernel<1, true>) : go(i8_stem_s2d_kernel<1, false>); break;
-    case 2: relu ? go(i8_stem_s2d_kernel<2, true>) : go(i8_stem_s2d_kernel<2, false>); break;
-    case 3: relu ? go(i8_stem_s2d_kernel<3, true>) : go(i8_stem_s2d_kernel<3, false>); break;
-    default: relu ? go(i8_stem_s2d_kernel<4, true>) : go(i8_stem_s2d_kernel<4, false>); break;
+  if (g.C == 3 && g.R == 7 && g.S == 7) {
+    relu ? go(i8_stem_s2d_kernel<4, true, 3, 7, 7>) : go(i8_stem_s2d_kernel<4, false, 3, 7, 7>);
+  } else {
+    switch (pl.KB) {
+      case 1: relu ? go(i8_stem_s2d_kernel<1, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<1, false, 0, 0, 0>); break;
+      case 2: relu ? go(i8_stem_s2d_kernel<2, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<2, false, 0, 0, 0>); break;
+      case 3: relu ? go(i8_stem_s2d_kernel<3, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<3, false, 0, 0, 0>); break;
+      default: relu ? go(i8_stem_s2d_kernel<4, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<4, false, 0, 0, 0>); break;
+    }
   }
   return hipGetLastError();
 }
