@@ -617,7 +617,7 @@ def bench_qi32(args) -> None:
         if (by, bx) == (1, 1):
             kern = M.plan_qi32(wl.n, wl.h, wl.w, wl.c, wl.r, wl.s, wl.k, p)
         else:
-            kern = "igemm"
+            kern = M.plan_block_qi32(wl.n, wl.h, wl.w, wl.c, wl.r, wl.s, wl.k, bp)
         if kern == "igemm" and (wl.c // wl.groups) % 4 != 0:
             kern = "igemm-scalar"
         gbs = nbytes / (ms * 1e-3) / 1e9

@@ -237,6 +237,13 @@ int miq_fprop_nhwc_qi32_ws(int32_t qp_kind, const float* x, const float* w, int3
 int miq_plan_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
                   const miq_conv2d_params* p, int32_t* algo);
 
+/* miq_plan_qi32 for blocked filters (the kernel launch_block_fprop_nhwc_qi32 runs with
+ * 256-byte aligned tensors): MIQ_ALGO_BAND (row bands inside one filter block, on the band
+ * kernel's conditions for the block's width), MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT.  No reference
+ * counterpart. */
+int miq_plan_block_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                        const miq_block_conv2d_params* p, int32_t* algo);
+
 /* ---- native int8 convolution ------------------------------------------------------- */
 /* No reference counterpart: the int8 activation / int8 weight / int32 bias /
  * per-channel scale / int8 output surface that the reference's quantization types

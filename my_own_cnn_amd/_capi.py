@@ -126,6 +126,7 @@ SIGNATURES = {
     "miq_fprop_nhwc_qi32_algo": (
         C.c_int, [_I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _P, _P, _I, _P]),
     "miq_plan_qi32": (C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _PI]),
+    "miq_plan_block_qi32": (C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(BlockConv2DParams), _PI]),
     "miq_fprop_nhwc_qi32_workspace_size": (
         C.c_int, [_I, _I, _I, _I, _I, _I, _I, C.POINTER(Conv2DParams), _I, C.POINTER(C.c_size_t)]),
     "miq_fprop_nhwc_qi32_ws": (

@@ -182,6 +182,13 @@ def plan_qi32(n: int, h: int, w: int, c: int, r: int, s: int, k: int, p=None) ->
     return {v: key for key, v in QI32_ALGOS.items()}[out.value]
 
 
+def plan_block_qi32(n: int, h: int, w: int, c: int, r: int, s: int, k: int, p: BlockConv2DParams) -> str:
+    """The kernel launch_block_fprop_nhwc_qi32 runs for this problem (aligned tensors)."""
+    out = C.c_int32()
+    check(lib().miq_plan_block_qi32(n, h, w, c, r, s, k, C.byref(p), C.byref(out)), "plan_block_qi32")
+    return {v: key for key, v in QI32_ALGOS.items()}[out.value]
+
+
 def launch_block_fprop_nhwc_qi32(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int,
                                  c: int, r: int, s: int, k: int, p: BlockConv2DParams, in_qp: Pointer = None,
                                  f_qp: Pointer = None, stream=None) -> None:

@@ -196,8 +196,8 @@ int stream_workspace(hipStream_t s, size_t bytes, void** out) {
 }
 
 // Bytes of workspace a float-code problem needs on the kernel `algo` (resolved, not AUTO).
-size_t qi32_workspace_bytes(const miq::Geom& g, int32_t algo) {
-  if (algo == MIQ_ALGO_BAND) return miq::qi32_band_workspace_bytes(g);
+size_t qi32_workspace_bytes(const miq::Geom& g, const miq::BlockGeom& bg, int32_t algo) {
+  if (algo == MIQ_ALGO_BAND) return miq::qi32_band_workspace_bytes(g, bg);
   if (algo == MIQ_ALGO_STREAM) return miq::qi32_route_workspace_bytes(g);
   return 0;
 }
@@ -243,7 +243,7 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND or STREAM");
   }
-  const size_t ws_bytes = qi32_workspace_bytes(g, algo);
+  const size_t ws_bytes = qi32_workspace_bytes(g, bg, algo);
   if (cw.given && cw.bytes < ws_bytes) {
     return fail(MIQ_ERR_INVALID_ARGUMENT, "workspace is smaller than miq_fprop_nhwc_qi32_workspace_size reports");
   }
@@ -497,7 +497,7 @@ int miq_fprop_nhwc_qi32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_
     default:
       return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND or STREAM");
   }
-  *bytes = out_elems(g) == 0 ? 0 : qi32_workspace_bytes(g, algo);
+  *bytes = out_elems(g) == 0 ? 0 : qi32_workspace_bytes(g, bg, algo);
   return MIQ_OK;
 }
 
@@ -515,6 +515,18 @@ int miq_fprop_nhwc_qi32_ws(int32_t qp_kind, const float* x, const float* w, int3
   cw.bytes = workspace_bytes;
   return qi32_entry(qp_kind == 0 ? miq::kQpU8 : miq::kQpS5, x, w, y, g, miq::BlockGeom{1, 1, g.Ho, g.Wo}, in_qp, f_qp,
                     stream, algo, cw);
+}
+
+int miq_plan_block_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
+                        const miq_block_conv2d_params* p, int32_t* algo) {
+  if (algo == nullptr) return fail(MIQ_ERR_NULL_POINTER, "algo output pointer is NULL");
+  miq::Geom g;
+  miq::BlockGeom bg;
+  const int st = infer_block_geom(n, h, wdt, c, r, s, k, p, &g, &bg);
+  if (st != MIQ_OK) return st;
+  static const char kAligned[16] __attribute__((aligned(256))) = {0};
+  *algo = qi32_auto(g, bg, kAligned, kAligned, kAligned);
+  return MIQ_OK;
 }
 
 int miq_plan_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,

@@ -87,7 +87,7 @@ bool qi32_band_eligible(const Geom& g, const BlockGeom& bg, const void* x, const
 // Device bytes of the workspace launch_qi32_band takes (the filter converted once per call to
 // int8 MFMA fragments, and range flags); the caller keeps it unused by other work until the
 // launches on `stream` have completed.
-size_t qi32_band_workspace_bytes(const Geom& g);
+size_t qi32_band_workspace_bytes(const Geom& g, const BlockGeom& bg);
 hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const float* x, const float* w, int32_t* y,
                             const void* in_qp, const void* f_qp, void* ws, hipStream_t stream);
 

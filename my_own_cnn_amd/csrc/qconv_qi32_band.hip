@@ -23,7 +23,10 @@
 //
 // Work decomposition, input-row layout, segment walk and skew are those of the int8 band
 // kernel: a workgroup of 8 waves owns BH output rows of one image and NT 64-channel tiles of
-// one group; each wave keeps its tile's filter in registers (KB = R*S*(C/groups)/64 K-blocks);
+// one group;  with blocked filters (the reference's launch_block_fprop_nhwc_qi32, output pixel
+// (ho, wo) taking filter block (ho / block_ho, wo / block_wo)) its rows and columns lie inside
+// one block (a band never crosses a block row; its columns are the block's block_wo) and it
+// loads that block's filter tiles; each wave keeps its tile's filter in registers (KB = R*S*(C/groups)/64 K-blocks);
 // 16-pixel segments run one per phase.  Output channels are not permuted: MFMA row block j
 // holds channels 16j .. 16j + 15, so the 4 lanes of a pixel store 64 contiguous bytes of int32.
 //
@@ -72,10 +75,11 @@ struct Qi32BandArgs {
   int halo_lds;                      // LDS byte offset of the rows (the filter is at 0); column sums, filter sums, wave marks follow
   int tap[kQbMaxKB];                 // K-block b: halo slot offset of (filter row, quad) << 8 | column shift
   int ntiles;
-  FastDivM fd_ntiles, fd_bpi, fd_ktpg, fd_rowi, fd_npb;
+  int Wb, bho, Bx, bpb;              // columns per workgroup (a block's), rows per block, column blocks, bands per block
+  FastDivM fd_ntiles, fd_bpi, fd_ktpg, fd_rowi, fd_npb, fd_bpb, fd_bx;
 };
 
-static_assert(sizeof(Qi32BandArgs) <= 256, "kernel arguments fit one s_load batch");
+static_assert(sizeof(Qi32BandArgs) <= 320, "kernel arguments fit one batch of s_load instructions");
 
 // Per-sample zero point from the raw parameter struct: uint8 at offset 0 of a 12-byte struct
 // (LinQuantU8), int8 at offset 0 of an 8-byte struct (LinQuantS5).  A buffer load (counted by
@@ -148,10 +152,15 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
   const int band = fdiv(lin, a.fd_ntiles);
   const int ctile = lin - band * a.ntiles;
   const int n = fdiv(band, a.fd_bpi);
-  const int bi = band - n * a.bands_per_img;
+  const int rem = band - n * a.bands_per_img;
+  const int blk = fdiv(rem, a.fd_bpb);  // filter block (by, bx) = (blk / Bx, blk % Bx)
+  const int bib = rem - blk * a.bpb;    // band within the block
+  const int by = fdiv(blk, a.fd_bx);
+  const int bx = blk - by * a.Bx;
   const int gi = fdiv(ctile, a.fd_ktpg);
   const int k0 = (ctile - gi * a.kt_per_group) * NT * 64;  // first channel (in group gi)
-  const int ho0 = bi * a.BH;
+  const int ho0 = by * a.bho + bib * a.BH;
+  const int wc0 = bx * a.Wb;  // first output column
   const int tw = MT ? wave / WPT : 0;
   const int wl = wave - tw * WPT;
   const int row_instr = a.NQ * a.NPB;
@@ -165,7 +174,7 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
   // ---- filter: the workgroup's NT tiles of int8 fragments from the prepass, contiguous,
   // by DMA (1 KB per instruction); then the range flags of its tiles' K-blocks
   const int kt64 = a.kt_per_group * NT;
-  const int tile0 = gi * kt64 + k0 / 64;
+  const int tile0 = (blk * (a.ntiles / a.kt_per_group) + gi) * kt64 + k0 / 64;
   {
     const __amdgpu_buffer_rsrc_t rf = make_rsrc(a.wfrag + static_cast<size_t>(tile0) * KB * 4096, NT * KB * 4096);
     for (int f = wave; f < NT * 4 * KB; f += kQbWaves) load_lds16(rf, filt + f * 64, 16u * lane, static_cast<unsigned>(f * 1024));
@@ -197,7 +206,7 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
     const int q = fdiv(rem, a.fd_npb);
     const int pb = rem - q * a.NPB;
     const int hi = hi0 + hr;
-    const int col = 16 * pb + 4 * (e & 3) + (lane >> 4) - a.pw;
+    const int col = wc0 + 16 * pb + 4 * (e & 3) + (lane >> 4) - a.pw;
     const bool ok = static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) &&
                     static_cast<unsigned>(col) < static_cast<unsigned>(a.W);
     jok[slot] = ok;
@@ -232,7 +241,7 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
   if (lane == 0) marks[wave] = wbad ? 1 : 0;
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  const int band_rows = min(a.BH, a.Ho - ho0);
+  const int band_rows = min(a.BH, a.bho - bib * a.BH);
   int any_bad = 0;
 #pragma unroll
   for (int v = 0; v < kQbWaves; ++v) any_bad |= marks[v];
@@ -242,16 +251,18 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
     // workgroup's outputs, channel fastest (the reference's loop order per output)
     const float* xn = a.x + static_cast<size_t>(n) * a.H * a.W * a.C + static_cast<size_t>(gi) * a.Cg;
     const int nk = NT * 64;
-    const int nout = band_rows * a.Wo * nk;
+    const int nout = band_rows * a.Wb * nk;
+    const int nblk = (a.bands_per_img / a.bpb);  // filter blocks
     for (int o = threadIdx.x; o < nout; o += 64 * kQbWaves) {
       const int c = o % nk;
       const int pix = o / nk;
       const int kg = k0 + c;
       if (kg >= a.Kg) continue;
-      const int t = pix / a.Wo;
-      const int wo = pix - t * a.Wo;
+      const int t = pix / a.Wb;
+      const int wo = wc0 + pix - t * a.Wb;
       const int ho = ho0 + t;
-      const float* wk = a.w + (static_cast<size_t>(gi) * a.Kg + kg) * kKdim;
+      // filter [K, By, Bx, R, S, C/groups]: channel gi * Kg + kg, block blk
+      const float* wk = a.w + ((static_cast<size_t>(gi) * a.Kg + kg) * nblk + blk) * kKdim;
       uint32_t acc = 0;
       for (int r = 0; r < a.R; ++r) {
         const int hi = ho * a.sh - a.ph + r * a.dh;
@@ -330,8 +341,8 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
 
   // Output: lane (pixel row_l, grp_l) stores channels 16j + 4 grp_l .. + 3 of acc[j]: the 4
   // lanes of a pixel write 64 contiguous bytes per store.
-  const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + static_cast<size_t>(gi) * a.Kg;
-  const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + out0, band_rows * a.Wo * a.K * 4);
+  const size_t out0 = ((static_cast<size_t>(n) * a.Ho + ho0) * a.Wo + wc0) * a.K + static_cast<size_t>(gi) * a.Kg;
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + out0, (band_rows * a.Wo - wc0) * a.K * 4);
   const unsigned lane_out = static_cast<unsigned>((row_l * a.K + kt0 + 4 * grp_l) * 4);
   const int nseg = band_rows * a.SEGR;
   int seg_t = 0, seg_c = wl;
@@ -341,7 +352,7 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
   }
   unsigned seg_in = static_cast<unsigned>(seg_t) * row_bytes + 1024u * static_cast<unsigned>(seg_c);
   int seg_out = (seg_t * a.Wo + 16 * seg_c) * a.K;
-  const unsigned lane_last = lane_out + (16 * (a.SEGR - 1) + row_l < a.Wo ? 0u : 0x40000000u);
+  const unsigned lane_last = lane_out + (16 * (a.SEGR - 1) + row_l < a.Wb ? 0u : 0x40000000u);
   auto seg_soff = [&]() { return static_cast<unsigned>(seg_out * 4); };
   auto seg_lane = [&]() { return seg_c == a.SEGR - 1 ? lane_last : lane_out; };
   auto seg_next = [&]() {
@@ -423,20 +434,25 @@ __global__ void __launch_bounds__(64 * kQbWaves, 1) qi32_band_kernel(Qi32BandArg
 // 16j + row; channels past K/groups are zeros.  Thread (channel c, quarter p) converts values
 // 4p + 16k, k = 0..3, so the 4 threads of a channel fill one 16-byte slot per k.  The block
 // writes 1 to its range flag when a value lies outside int8.
+// With blocked filters ([K, By, Bx, R, S, C/groups], nblk = By * Bx blocks) the tiles of block
+// fb come after those of blocks 0 .. fb - 1: tile = (fb * G + group) * kt64 + tile in group.
 template <QpKind Q>
 __global__ void __launch_bounds__(256) qi32_filter_prep_kernel(const float* w, int8_t* frag, int* flags, int Kg,
-                                                               int Kdim, int kt64, int KB) {
+                                                               int Kdim, int kt64, int KB, int G, int nblk) {
   constexpr unsigned kOff = Q == kQpU8 ? 128u : 0u;
   const int blk = blockIdx.x;
   const int tile = blk / KB;
   const int b = blk - tile * KB;
-  const int gi = tile / kt64;
+  const int gt = tile / kt64;  // fb * G + gi
+  const int fb = gt / G;
+  const int gi = gt - fb * G;
   const int c = threadIdx.x >> 2;
   const int p = threadIdx.x & 3;
-  const int kg = 64 * (tile - gi * kt64) + c;
+  const int kg = 64 * (tile - gt * kt64) + c;
   const bool ok = kg < Kg;
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + static_cast<size_t>(gi) * Kg * Kdim, Kg * Kdim * 4);
-  const unsigned src = static_cast<unsigned>((min(kg, Kg - 1) * Kdim + 64 * b + 4 * p) * 4);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(w + (static_cast<size_t>(gi) * Kg * nblk + fb) * Kdim, ((Kg - 1) * nblk + 1) * Kdim * 4);
+  const unsigned src = static_cast<unsigned>((min(kg, Kg - 1) * nblk * Kdim + 64 * b + 4 * p) * 4);
   v4f v[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) v[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rw, src + 64u * k, 0, 0));
@@ -477,27 +493,29 @@ bool qb_plan(const Geom& g, const BlockGeom& bg, Qi32BandPlan* p, std::string* w
     if (why) *why = m;
     return false;
   };
-  if (bg.By != 1 || bg.Bx != 1) return no("qi32 band kernel takes plain filters only");
+  // the workgroup's columns: a filter block's (all of them for a plain filter)
+  const int Wb = bg.bwo;
+  const int Hb = bg.bho;
   if (g.Cg % 64 != 0 || g.Cg == 0) return no("qi32 band kernel needs (c/groups) % 64 == 0");
   if (g.Kg <= 0 || g.Kg % 16 != 0) return no("qi32 band kernel needs (k/groups) % 16 == 0");
   if (g.sw != 1) return no("qi32 band kernel needs stride_w == 1");
   if (g.sh < 1 || g.dh < 1 || g.dw < 1 || g.ph < 0 || g.pw < 0) return no("qi32 band kernel needs positive stride/dilation");
-  if (g.Wo > 64 || g.Wo < 1 || g.Ho < 1) return no("qi32 band kernel needs 1 <= output width <= 64");
+  if (Wb > 64 || Wb < 1 || Hb < 1) return no("qi32 band kernel needs 1 <= output (block) width <= 64");
   if (g.R < 1 || g.S < 1) return no("qi32 band kernel needs a non-empty filter");
   const long long kb = static_cast<long long>(g.R) * g.S * (g.Cg / 64);
   if (kb > kQbMaxKB) return no("qi32 band kernel filter does not fit in registers (R*S*c/groups > 576)");
-  const long long hcols = static_cast<long long>(g.Wo) + static_cast<long long>(g.S - 1) * g.dw;
+  const long long hcols = static_cast<long long>(Wb) + static_cast<long long>(g.S - 1) * g.dw;
   if (hcols > 128) return no("qi32 band kernel needs output width + dilated filter width <= 128");
   if (static_cast<long long>(g.Ho) * g.Wo * g.K * 4 >= (1LL << 30)) return no("qi32 band kernel needs images below 2^30 output bytes");
   if (static_cast<long long>(g.H) * g.W * g.C * 4 >= (1LL << 31)) return no("qi32 band kernel needs images below 2^31 input bytes");
   if (static_cast<long long>(g.Kg) * g.R * g.S * g.Cg * 4 >= (1LL << 31)) return no("qi32 band kernel needs group filters below 2^31 bytes");
-  if (static_cast<long long>(g.G) * ((g.Kg + 63) / 64) * g.R * g.S * (g.Cg / 64) * 4096 >= (1LL << 31)) {
+  if (static_cast<long long>(bg.By) * bg.Bx * g.G * ((g.Kg + 63) / 64) * g.R * g.S * (g.Cg / 64) * 4096 >= (1LL << 31)) {
     return no("qi32 band kernel needs converted filters below 2^31 bytes");
   }
   p->KB = static_cast<int>(kb);
   p->NQ = g.Cg / 64;
   p->NPB = static_cast<int>((hcols + 15) / 16);
-  p->SEGR = (g.Wo + 15) / 16;
+  p->SEGR = (Wb + 15) / 16;
   const int kt64 = (g.Kg + 63) / 64;
   const int cus = qb_cu_count();
   // Cost in cycles of one round of workgroups (one per CU): the two waves of the busiest
@@ -509,13 +527,13 @@ bool qb_plan(const Geom& g, const BlockGeom& bg, Qi32BandPlan* p, std::string* w
   for (int nt = 1; nt <= kQbWaves; nt *= 2) {
     if (kt64 % nt != 0) continue;
     const int wpt = kQbWaves / nt;
-    for (int bh = 1; bh <= g.Ho; ++bh) {
+    for (int bh = 1; bh <= Hb; ++bh) {
       const long long hr = static_cast<long long>(bh - 1) * g.sh + static_cast<long long>(g.R - 1) * g.dh + 1;
       const long long ni = hr * p->NQ * p->NPB;
       if (ni > kQbWaves * 16) break;
       const size_t lds = qb_lds_bytes(p->KB, nt, ni);
       if (lds > static_cast<size_t>(kQbLds)) break;
-      const long long bands = (g.Ho + bh - 1) / bh;
+      const long long bands = static_cast<long long>(bg.By) * bg.Bx * ((Hb + bh - 1) / bh);
       const long long wgs = static_cast<long long>(g.N) * bands * g.G * (kt64 / nt);
       const long long rounds = (wgs + cus - 1) / cus;
       const long long nph = (static_cast<long long>(bh) * p->SEGR + wpt - 1) / wpt;
@@ -576,8 +594,9 @@ bool qi32_band_eligible(const Geom& g, const BlockGeom& bg, const void* x, const
   return qb_plan(g, bg, &pl, why);
 }
 
-size_t qi32_band_workspace_bytes(const Geom& g) {
-  const size_t nfblk = static_cast<size_t>(g.G) * ((g.Kg + 63) / 64) * g.R * g.S * (g.Cg / 64);
+size_t qi32_band_workspace_bytes(const Geom& g, const BlockGeom& bg) {
+  const size_t nfblk =
+      static_cast<size_t>(bg.By) * bg.Bx * g.G * ((g.Kg + 63) / 64) * g.R * g.S * (g.Cg / 64);
   return nfblk * 4096 + nfblk * 4;
 }
 
@@ -611,6 +630,12 @@ hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const
   }
   a.ntiles = g.G * pl.kt_per_group;
   a.fd_ntiles = fastdiv_m(a.ntiles);
+  a.Wb = bg.bwo;
+  a.bho = bg.bho;
+  a.Bx = bg.Bx;
+  a.bpb = (bg.bho + pl.BH - 1) / pl.BH;
+  a.fd_bpb = fastdiv_m(a.bpb);
+  a.fd_bx = fastdiv_m(bg.Bx);
   a.fd_bpi = fastdiv_m(pl.bands_per_img);
   a.fd_ktpg = fastdiv_m(pl.kt_per_group);
   a.fd_rowi = fastdiv_m(pl.NQ * pl.NPB);
@@ -628,7 +653,8 @@ hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const
   a.nblocks = static_cast<int>(nblocks);
   // the workspace (qi32_band_workspace_bytes) holds the prepass's fragments, then its flags
   const int kt64 = (g.Kg + 63) / 64;
-  const int nfblk = g.G * kt64 * pl.KB;
+  const int nblk = bg.By * bg.Bx;
+  const int nfblk = nblk * g.G * kt64 * pl.KB;
   const size_t frag_bytes = static_cast<size_t>(nfblk) * 4096;
   a.wfrag = static_cast<const int8_t*>(ws);
   a.flags_off = static_cast<int>(frag_bytes);
@@ -636,11 +662,11 @@ hipError_t launch_qi32_band(const Geom& g, const BlockGeom& bg, QpKind qp, const
   int* flags = reinterpret_cast<int*>(frag + frag_bytes);
   if (qp == kQpU8) {
     hipLaunchKernelGGL(qi32_filter_prep_kernel<kQpU8>, dim3(nfblk), dim3(256), 0, stream, w, frag, flags, g.Kg,
-                       g.R * g.S * g.Cg, kt64, pl.KB);
+                       g.R * g.S * g.Cg, kt64, pl.KB, g.G, nblk);
     qb_dispatch<kQpU8, kQbMaxKB>(pl.KB, a, pl, static_cast<unsigned>(nblocks), stream);
   } else {
     hipLaunchKernelGGL(qi32_filter_prep_kernel<kQpS5>, dim3(nfblk), dim3(256), 0, stream, w, frag, flags, g.Kg,
-                       g.R * g.S * g.Cg, kt64, pl.KB);
+                       g.R * g.S * g.Cg, kt64, pl.KB, g.G, nblk);
     qb_dispatch<kQpS5, kQbMaxKB>(pl.KB, a, pl, static_cast<unsigned>(nblocks), stream);
   }
   return hipGetLastError();

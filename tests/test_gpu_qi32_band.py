@@ -114,3 +114,80 @@ def test_qi32_band_full_c2_equals_igemm(device):
         # image 0 against the oracle as well
         want0 = oracle.conv_qi32(x[:1], wt, conv, zp[:1], fzp)
         np.testing.assert_array_equal(a[:1], want0)
+
+
+# blocked filters [K, By, Bx, R, S, C/groups] (launch_block_fprop_nhwc_qi32) on the band route:
+# kind, n, h, w, c, k, r, s, conv7, code range, (By, Bx)
+BLOCK_CASES = [
+    ("u8", 2, 14, 14, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), (0, 255), (2, 2)),      # 7 x 7 blocks
+    ("s5", 2, 16, 32, 64, 48, 3, 3, (1, 1, 1, 1, 1, 1, 1), (-16, 15), (2, 4)),     # partial tile, 8 x 8 blocks
+    ("u8", 1, 9, 60, 128, 64, 1, 1, (0, 0, 1, 1, 1, 1, 1), (0, 255), (3, 3)),      # block width 20: a partial segment
+    ("u8", 2, 12, 16, 128, 128, 3, 3, (1, 1, 1, 1, 1, 1, 2), (0, 255), (2, 2)),    # groups 2
+    ("u8", 1, 17, 24, 64, 64, 3, 3, (1, 1, 2, 1, 1, 1, 1), (0, 255), (3, 2)),      # stride_h 2 (Ho 9)
+    ("s5", 1, 8, 64, 64, 32, 3, 3, (1, 1, 1, 1, 1, 1, 1), (-16, 15), (1, 1)),      # a 1 x 1 block grid
+    ("u8", 2, 56, 56, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), (0, 255), (4, 4)),      # C2's rows, 14 x 14 blocks
+]
+
+
+def run_block(kind, x, wt, conv, zp, fzp, block, device):
+    n, h, w, c = x.shape
+    k, r, s = wt.shape[0], wt.shape[3], wt.shape[4]
+    tin, in_qp = qparams_dev(kind, zp, device)
+    _, f_qp = qparams_dev(kind, [fzp], device)
+    p = M.BlockConv2DParams(M.Conv2DParams(*conv), block[0], block[1])
+    ho, wo = M.infer_conv_shape(n, h, w, c, r, s, k, M.Conv2DParams(*conv))
+    y = torch.full((n, ho, wo, k), -7, dtype=torch.int32, device=device)
+    M.launch_block_fprop_nhwc_qi32(tin, dev(x, device), dev(wt, device), y, n, h, w, c, r, s, k, p, in_qp, f_qp)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def make_block_case(case, seed):
+    kind, n, h, w, c, k, r, s, conv, (lo, hi), block = case
+    rng = np.random.default_rng(seed)
+    g = conv[6]
+    x = rng.uniform(lo, hi, size=(n, h, w, c)).astype(np.float32)
+    wt = rng.uniform(lo, hi, size=(k, block[0], block[1], r, s, c // g)).astype(np.float32)
+    zlo, zhi = (0, 255) if kind == "u8" else (-128, 127)
+    zp = rng.integers(zlo, zhi, size=n, endpoint=True).astype(np.int32)
+    fzp = int(rng.integers(zlo, zhi, endpoint=True))
+    return x, wt, zp, fzp
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES,
+                         ids=[f"{c[0]}_h{c[2]}w{c[3]}c{c[4]}k{c[5]}r{c[6]}g{c[8][6]}b{c[10][0]}x{c[10][1]}" for c in BLOCK_CASES])
+def test_qi32_band_blocked_bit_exact(device, case):
+    kind, n, h, w, c, k, r, s, conv, _, block = case
+    p = M.BlockConv2DParams(M.Conv2DParams(*conv), block[0], block[1])
+    assert M.plan_block_qi32(n, h, w, c, r, s, k, p) == "band"
+    x, wt, zp, fzp = make_block_case(case, 6400 + BLOCK_CASES.index(case))
+    print(f"qi32 blocked band case {case}", flush=True)
+    want = oracle.conv_qi32(x, wt, conv, zp, fzp, block=block)
+    np.testing.assert_array_equal(run_block(kind, x, wt, conv, zp, fzp, block, device), want)
+
+
+def test_qi32_band_blocked_codes_outside_int8(device):
+    """A code outside int8 in one image: its workgroups compute directly (with the block's
+    filter), the others keep the MFMA path."""
+    case = ("u8", 3, 12, 16, 64, 64, 3, 3, (1, 1, 1, 1, 1, 1, 1), (0, 255), (2, 2))
+    x, wt, zp, fzp = make_block_case(case, 6500)
+    x[1, 7, 9, 5] = 300.0
+    wt[3, 1, 0, 2, 1, 7] = -1.0  # every workgroup of the block stages a filter value outside int8
+    want = oracle.conv_qi32(x, wt, case[8], zp, fzp, block=(2, 2))
+    np.testing.assert_array_equal(run_block("u8", x, wt, case[8], zp, fzp, (2, 2), device), want)
+
+
+def test_qi32_band_blocked_full_c2(device):
+    """C2 with 2 x 2 and 4 x 4 filter blocks at full size (N = 32): the band route, images 0
+    and 31 against the oracle."""
+    conv = (1, 1, 1, 1, 1, 1, 1)
+    for block in ((2, 2), (4, 4)):
+        case = ("u8", 32, 56, 56, 64, 64, 3, 3, conv, (0, 255), block)
+        x, wt, zp, fzp = make_block_case(case, 6600 + block[0])
+        p = M.BlockConv2DParams(M.Conv2DParams(*conv), block[0], block[1])
+        assert M.plan_block_qi32(32, 56, 56, 64, 3, 3, 64, p) == "band"
+        print(f"qi32 blocked full C2 {block}", flush=True)
+        y = run_block("u8", x, wt, conv, zp, fzp, block, device)
+        for i in (0, 31):
+            want = oracle.conv_qi32(x[i:i + 1], wt, conv, zp[i:i + 1], fzp, block=block)
+            np.testing.assert_array_equal(y[i:i + 1], want, err_msg=f"{block} image {i}")
