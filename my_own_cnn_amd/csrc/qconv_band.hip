@@ -52,8 +52,8 @@
 // (C2 7.27 -> 7.41 us).
 //
 // Epilogue.  Accumulators start at the bias; the output is convert, scale, clamp, round
-// (the 1.5*2^23 addition; with ReLU, v_cvt_pk_u8_f32 rounds to nearest even and packs) and
-// one 16-byte store of 16 consecutive channels per lane, the arithmetic of the other int8
+// (the 1.5*2^23 addition, four results packed with two v_perm_b32 and an or) and one
+// 16-byte store of 16 consecutive channels per lane, the arithmetic of the other int8
 // kernels.  Every 16-byte store is followed by store_gap() on its data registers.
 
 #include "qconv_device.h"

@@ -40,8 +40,8 @@
 // consecutive channels of one pixel.
 //
 // Output.  Accumulators start at the bias; convert, scale, clamp and round to nearest even
-// exactly as the other int8 kernels (v_cvt_pk_u8_f32 with ReLU, the 1.5 * 2^23 addition
-// without).  A wave writes its 32 channels of a segment into an LDS staging area (96 bytes per
+// exactly as the other int8 kernels (clamp to [lo, 127], the 1.5 * 2^23 addition, bytes
+// packed with v_perm_b32).  A wave writes its 32 channels of a segment into an LDS staging area (96 bytes per
 // pixel) and counts the half staged; the wave that stages the second half stores the whole
 // segment (16 pixels x 64 channels, one contiguous kilobyte of NHWC output) with one 16-byte
 // write-through non-temporal store per lane, followed by store_gap() on its data registers.

@@ -1,7 +1,7 @@
 // int8 pointwise (1x1, stride 1, no padding) convolution with 64 or 128 input channels:
 // a GEMM over the flattened output pixels (P = n*h*w, each pixel's C input bytes contiguous in
-// NHWC), filter-stationary v_mfma_i32_16x16x64_i8, with the input streamed into LDS by a
-// loader wave while eight compute waves consume it.
+// NHWC), filter-stationary v_mfma_i32_16x16x64_i8, with the input streamed into LDS by four
+// loader waves while eight compute waves consume it.
 //
 // Work.  The P pixels are cut into 16-pixel segments; the segments are split into contiguous
 // ranges.  A workgroup owns one range and NT (1 or 2) 64-channel output tiles: NT*64 channels.
@@ -15,18 +15,21 @@
 // Filter-stationary.  Each compute wave keeps its tile's filter in registers (KB x 4 fragments
 // of 16 bytes per lane).  Row i of row block j holds channel 16*(i/4) + 4j + i%4, so lane
 // (rho, g) ends with channels 16g .. 16g + 15 of pixel rho: one contiguous 16-byte output.
+// The compute waves load the filter slice, bias and scales themselves (global -> LDS DMA,
+// spread over the eight), wait for their own share and count it in an LDS word; each starts
+// once the count reaches eight.
 //
-// Loader wave (wave 8).  It issues every load of the workgroup: the filter slice and the bias
-// and scales first, then the range's input segments in order (one 1 KB buffer_load ... lds per
-// 8 pixels x 128 channel bytes or 16 pixels x 64, global -> LDS without registers).  It keeps
-// a fixed number of segments in flight: after issuing segment i it waits (vmcnt, a compile-time
-// count) for segment i - F and publishes the count of landed segments in an LDS word
-// (lds_publish: a store that does not wait for the loader's later loads); the compute waves
-// poll that word (relaxed atomic
-// loads, s_sleep between polls, bounded) before reading a segment.  The loader issues no
-// stores, so its vmcnt waits count its own loads only, and the compute waves never wait on
-// vmcnt at all.  LDS operations of one wave complete in order, so a count seen raised means
-// the segments below it are in LDS.
+// Loader waves (waves 8 .. 11).  Loader l loads the range's input segments l, l + 4, ... in
+// order (one 1 KB buffer_load ... lds per 8 pixels x 128 channel bytes or 16 pixels x 64,
+// global -> LDS without registers).  It keeps a fixed number of segments in flight: after
+// issuing its k-th segment it waits (vmcnt, a compile-time count) for its segment k - F and
+// publishes the count of its landed segments in its own LDS word (lds_publish: a store that
+// does not wait for the loader's later loads); a compute wave polls the word of the segment's
+// loader (relaxed atomic loads, s_sleep between polls, bounded) before reading the segment.
+// Loaders issue no stores, so their vmcnt waits count their own loads only, and the compute
+// waves never wait on vmcnt after the filter.  LDS operations of one wave complete in order,
+// so a count seen raised means the segments below it are in LDS.  Loader 0 zeroes the count
+// words before the one barrier of the kernel.
 //
 // LDS layout (16-byte slots).  Input segment s of the range, pixel p (0..15) of it, chunk u
 // (16 channels): slot s*16*C/16 + p*C/16 + (u ^ f(p)), f(p) = (p >> 1) & 7 (C = 128) or
@@ -38,9 +41,9 @@
 // classes (the half-wave, equal-popcount-parity lane-quad rule measured on gfx950).
 //
 // Epilogue.  Accumulators start at the bias (the first MFMA's C operand is the bias registers);
-// the output is convert, scale, clamp, round (1.5*2^23 addition written to its byte by an
-// SDWA add; with ReLU v_cvt_pk_u8_f32 rounds and packs), the arithmetic of the other int8
-// kernels.  Every 16-byte store is followed by store_gap() on its data registers.
+// the output is convert, scale, clamp, round (the 1.5*2^23 addition, bytes packed with
+// v_perm_b32), the arithmetic of the other int8 kernels, interleaved with the next
+// segment's matrix instructions (mma_requant_steps).  Every 16-byte store is followed by store_gap() on its data registers.
 
 #include "qconv_device.h"
 

@@ -1,5 +1,5 @@
 """The pointwise kernel (algo 'pointwise': 1x1 convolutions as a GEMM over the flattened pixels,
-input streamed into LDS by a loader wave) against the CPU oracle: every output byte bit-exact,
+input streamed into LDS by loader waves) against the CPU oracle: every output byte bit-exact,
 with and without ReLU and bias, on shapes that exercise its planner (one or two 64-channel tiles
 per workgroup, 64 or 128 input channels, a last segment partly past the pixels, ranges of one
 segment or of many, more workgroups than CUs), and the full ResNet-50 1x1 layer (C3) against the
