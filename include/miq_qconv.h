@@ -203,15 +203,17 @@ int miq_block_fprop_nhwc_qi32_s5(const float* x, const float* w, int32_t* y,
  * x, w and y, (c/groups) % 64 == 0, (k/groups) % 16 == 0, stride_w 1, output width <= 64,
  * r*s*c/groups <= 576), MIQ_ALGO_STREAM (the int8 stream kernel on a padded offset-int8 copy
  * of the input: c/groups % 64 == 0, k/groups % 128 == 0, stride_w <= 4, 16-byte aligned
- * tensors), MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT.  Results are identical for every choice.  No
- * reference counterpart: it exists for tests and benchmarks. */
+ * tensors), MIQ_ALGO_STEM_S2D (the space-to-depth stem kernel on a padded offset-int8 copy:
+ * groups 1, 1 <= c <= 4, stride 2, dilation 1, k % 64 == 0, ceil(r/2) * ceil(s/2) <= 16,
+ * 16-byte aligned tensors), MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT.  Results are identical for every
+ * choice.  No reference counterpart: it exists for tests and benchmarks. */
 int miq_fprop_nhwc_qi32_algo(int32_t qp_kind, const float* x, const float* w, int32_t* y,
                              int32_t n, int32_t h, int32_t wdt, int32_t c,
                              int32_t r, int32_t s, int32_t k, const miq_conv2d_params* p,
                              const void* in_qp, const void* f_qp, int32_t algo, void* stream);
 
-/* Bytes of device workspace miq_fprop_nhwc_qi32_ws needs for this shape and algo (the row-band
- * and stream kernels' prepass output; 0 for the others and for an empty output), for 256-byte
+/* Bytes of device workspace miq_fprop_nhwc_qi32_ws needs for this shape and algo (the row-band,
+ * stream and stem routes' prepass output; 0 for the others and for an empty output), for 256-byte
  * aligned tensors (misaligned ones can only take kernels that need none).  No GPU access.  No
  * reference counterpart: it sizes the caller-provided form of the workspace that
  * launch_fprop_nhwc_qi32_impl (/root/reference/src/cuda_kernels.cu:1351-1354) allocates. */
@@ -232,8 +234,8 @@ int miq_fprop_nhwc_qi32_ws(int32_t qp_kind, const float* x, const float* w, int3
                            size_t workspace_bytes, void* stream);
 
 /* The kernel the float-code entry points run for a plain-filter problem with 256-byte aligned
- * tensors: writes MIQ_ALGO_BAND, MIQ_ALGO_STREAM, MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT to *algo.  No reference
- * counterpart. */
+ * tensors: writes MIQ_ALGO_BAND, MIQ_ALGO_STREAM, MIQ_ALGO_STEM_S2D, MIQ_ALGO_IGEMM or MIQ_ALGO_DIRECT
+ * to *algo.  No reference counterpart. */
 int miq_plan_qi32(int32_t n, int32_t h, int32_t wdt, int32_t c, int32_t r, int32_t s, int32_t k,
                   const miq_conv2d_params* p, int32_t* algo);
 

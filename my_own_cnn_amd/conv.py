@@ -138,14 +138,14 @@ def launch_fprop_nhwc_qi32(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Point
              _stream(stream)), "launch_fprop_nhwc_qi32")
 
 
-QI32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2, "band": 4, "stream": 5}
+QI32_ALGOS = {"auto": 0, "direct": 1, "igemm": 2, "band": 4, "stream": 5, "stem_s2d": 11}
 
 
 def fprop_nhwc_qi32_algo(tin: DataType, d_x: Pointer, d_w: Pointer, d_y: Pointer, n: int, h: int, w: int, c: int,
                          r: int, s: int, k: int, p=None, in_qp: Pointer = None, f_qp: Pointer = None,
                          algo: str = "auto", stream=None, workspace: Pointer = None, workspace_bytes: int = 0) -> None:
-    """launch_fprop_nhwc_qi32 with an explicit kernel ("auto", "band", "stream", "igemm" or
-    "direct"); every choice gives the same int32 results.  `workspace`: a device buffer of at
+    """launch_fprop_nhwc_qi32 with an explicit kernel ("auto", "band", "stream", "stem_s2d",
+    "igemm" or "direct"); every choice gives the same int32 results.  `workspace`: a device buffer of at
     least qi32_workspace_size() bytes, which makes the call allocation-free
     (miq_fprop_nhwc_qi32_ws); None uses the library's per-stream workspace."""
     tin = DataType(tin)

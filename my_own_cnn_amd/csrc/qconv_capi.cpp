@@ -199,14 +199,16 @@ int stream_workspace(hipStream_t s, size_t bytes, void** out) {
 size_t qi32_workspace_bytes(const miq::Geom& g, const miq::BlockGeom& bg, int32_t algo) {
   if (algo == MIQ_ALGO_BAND) return miq::qi32_band_workspace_bytes(g, bg);
   if (algo == MIQ_ALGO_STREAM) return miq::qi32_route_workspace_bytes(g);
+  if (algo == MIQ_ALGO_STEM_S2D) return miq::qi32_stem_route_workspace_bytes(g);
   return 0;
 }
 
 // The kernel AUTO runs for a float-code problem: the row-band kernel, else the stream route,
-// else the implicit GEMM, else the direct kernel.
+// else the stem route, else the implicit GEMM, else the direct kernel.
 int32_t qi32_auto(const miq::Geom& g, const miq::BlockGeom& bg, const void* x, const void* w, const void* y) {
   if (miq::qi32_band_eligible(g, bg, x, w, y, nullptr)) return MIQ_ALGO_BAND;
   if (miq::qi32_route_eligible(g, bg, x, w, y, nullptr)) return MIQ_ALGO_STREAM;
+  if (miq::qi32_stem_route_eligible(g, bg, x, w, y, nullptr)) return MIQ_ALGO_STEM_S2D;
   if (miq::qi32_igemm_eligible(g, bg, x, w, nullptr)) return MIQ_ALGO_IGEMM;
   return MIQ_ALGO_DIRECT;
 }
@@ -240,8 +242,12 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
     case MIQ_ALGO_STREAM:
       if (!miq::qi32_route_eligible(g, bg, x, w, y, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       break;
+    case MIQ_ALGO_STEM_S2D:
+      if (!miq::qi32_stem_route_eligible(g, bg, x, w, y, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
+      break;
     default:
-      return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND or STREAM");
+      return fail(MIQ_ERR_INVALID_ARGUMENT,
+                  "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND, STREAM or STEM_S2D");
   }
   const size_t ws_bytes = qi32_workspace_bytes(g, bg, algo);
   if (cw.given && cw.bytes < ws_bytes) {
@@ -265,6 +271,11 @@ int qi32_entry(miq::QpKind qk, const float* x, const float* w, int32_t* y, const
     case MIQ_ALGO_STREAM: {
       e = miq::launch_qi32_route(g, qk, x, w, y, in_qp, f_qp, ws, hs);
       if (e != hipSuccess) return hip_fail(e, "qi32 stream route launch");
+      return MIQ_OK;
+    }
+    case MIQ_ALGO_STEM_S2D: {
+      e = miq::launch_qi32_stem_route(g, qk, x, w, y, in_qp, f_qp, ws, hs);
+      if (e != hipSuccess) return hip_fail(e, "qi32 stem route launch");
       return MIQ_OK;
     }
     case MIQ_ALGO_IGEMM:
@@ -494,8 +505,14 @@ int miq_fprop_nhwc_qi32_workspace_size(int32_t n, int32_t h, int32_t wdt, int32_
     case MIQ_ALGO_STREAM:
       if (!miq::qi32_route_eligible(g, bg, kAligned, kAligned, kAligned, &why)) return fail(MIQ_ERR_UNSUPPORTED, why);
       break;
+    case MIQ_ALGO_STEM_S2D:
+      if (!miq::qi32_stem_route_eligible(g, bg, kAligned, kAligned, kAligned, &why)) {
+        return fail(MIQ_ERR_UNSUPPORTED, why);
+      }
+      break;
     default:
-      return fail(MIQ_ERR_INVALID_ARGUMENT, "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND or STREAM");
+      return fail(MIQ_ERR_INVALID_ARGUMENT,
+                  "float-code convolution algo must be AUTO, DIRECT, IGEMM, BAND, STREAM or STEM_S2D");
   }
   *bytes = out_elems(g) == 0 ? 0 : qi32_workspace_bytes(g, bg, algo);
   return MIQ_OK;

@@ -101,6 +101,16 @@ size_t qi32_route_workspace_bytes(const Geom& g);
 hipError_t launch_qi32_route(const Geom& g, QpKind qp, const float* x, const float* w, int32_t* y, const void* in_qp,
                              const void* f_qp, void* ws, hipStream_t stream);
 
+// int32 accumulators on float codes through the space-to-depth stem kernel (stride-2
+// thin-channel layers): a prepass to a padded offset-int8 image (rows padded to a multiple of
+// 16 bytes) and int8 filter in the workspace, the s2d kernel with the offset corrections, an
+// exact direct pass only when a code leaves int8.
+bool qi32_stem_route_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, const void* y,
+                              std::string* why);
+size_t qi32_stem_route_workspace_bytes(const Geom& g);
+hipError_t launch_qi32_stem_route(const Geom& g, QpKind qp, const float* x, const float* w, int32_t* y,
+                                  const void* in_qp, const void* f_qp, void* ws, hipStream_t stream);
+
 // int8 VALU direct convolution: any geometry.
 hipError_t launch_i8_direct(const Geom& g, Epi epi, const int8_t* x, const int8_t* w, void* y, const Requant& rq,
                             hipStream_t stream);
@@ -145,6 +155,12 @@ bool stem_s2d_eligible(const Geom& g, const void* x, const void* w, const void* 
                        std::string* why);
 hipError_t launch_i8_stem_s2d(const Geom& g, const int8_t* x, const int8_t* w, int8_t* y, const Requant& rq,
                               hipStream_t stream);
+// The same kernel on offset codes with int32 outputs (the float-code stem route): `g` is the
+// padded problem (padding 0, its own Ho and Wo), T the filter row sums, qrec the per-image
+// records {dx, dw, Kdim * dx * dw, 0}.
+bool stem_s2d_qi32_plan_ok(const Geom& g, std::string* why);
+hipError_t launch_stem_s2d_qi32(const Geom& g, const int8_t* x, const int8_t* w, const int32_t* T,
+                                const int32_t* qrec, int32_t* y, hipStream_t stream);
 
 // int8 MFMA pointwise kernel (1x1, stride 1, no padding, groups 1, C 64 or 128, K % 64 == 0):
 // a GEMM over the flattened pixels with the input streamed into LDS by a loader wave.

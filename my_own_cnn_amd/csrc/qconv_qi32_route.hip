@@ -20,6 +20,12 @@
 //   2. the stream kernel (kEpiQi32) on the padded image.
 //   3. qi32_route_fallback_kernel: every workgroup ORs the flags; unless one is set it exits at
 //      once, else the grid recomputes every output directly from the float codes (exact).
+//
+// The stem route (stride-2 layers with 1..4 channels) is the same scheme on the space-to-depth
+// stem kernel: qi32_stem_prep_kernel writes the image as rows of Wq pixels (Wq >= W + 2 pw,
+// Wq * C a multiple of 16 bytes, every byte past the image zx - o) and the filter value by
+// value (Kdim need not be a multiple of 4); the s2d kernel in its int32 mode sums W(p) from its
+// own fragments under a mask of the filter's taps; the same flag pass follows.
 
 #include "qconv_device.h"
 
@@ -194,6 +200,131 @@ __global__ void __launch_bounds__(kRtThreads) qi32_route_fallback_kernel(RouteFa
   }
 }
 
+// ---- the stem route (thin-channel stride-2 layers, the space-to-depth stem kernel): the
+// image into rows of Wq pixels (Wq >= W + 2 pw, Wq * C a multiple of 16 bytes), padded taps at
+// zx - o; the filter value by value ----
+struct StemPrepArgs {
+  const float* x;
+  const float* w;
+  const unsigned char* in_qp;
+  const unsigned char* f_qp;
+  int8_t* xp;      // [N][Hp][Wq][C]
+  int8_t* wq;      // [K][Kdim]
+  int32_t* T;      // [K]
+  int32_t* qrec;   // [N][4]
+  int32_t* flags;  // [nfb + nib]
+  int N, H, W, C, K, Kdim, ph, pw, Hp, cpr;  // cpr: 16-byte chunks per padded row (Wq * C / 16)
+  int nfb;                                   // filter blocks: 4 channels each
+  int rows;                                  // N * Hp padded rows, one wave each
+};
+
+constexpr int kStemRowMax = 4096;  // bytes of one padded row (Wq * C) at most
+
+template <QpKind Q>
+__global__ void __launch_bounds__(kRtThreads) qi32_stem_prep_kernel(StemPrepArgs a) {
+  constexpr unsigned kOff = Q == kQpU8 ? 128u : 0u;
+  const int t = threadIdx.x;
+  bool bad = false;
+  if (static_cast<int>(blockIdx.x) < a.nfb) {
+    // ---- filter: channel c = 4 * block + t / 64, its codes t % 64, + 64, ... ----
+    const int c = 4 * static_cast<int>(blockIdx.x) + (t >> 6);
+    const int l = t & 63;
+    int sum = 0;
+    if (c < a.K) {
+      const float* src = a.w + static_cast<size_t>(c) * a.Kdim;
+      int8_t* dst = a.wq + static_cast<size_t>(c) * a.Kdim;
+      for (int i = l; i < a.Kdim; i += 64) {
+        const unsigned u = static_cast<unsigned>(static_cast<int32_t>(src[i])) - kOff;
+        bad |= (u + 128u) > 255u;
+        sum += static_cast<int>(u);
+        dst[i] = static_cast<int8_t>(u & 0xffu);
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o);
+    if (l == 0 && c < a.K) a.T[c] = sum;
+    if (blockIdx.x == 0) {
+      const unsigned dw = kOff - static_cast<unsigned>(rt_zero_point<Q>(a.f_qp, 0));
+      for (int n = t; n < a.N; n += kRtThreads) {
+        const unsigned dx = kOff - static_cast<unsigned>(rt_zero_point<Q>(a.in_qp, n));
+        const v4i rec = {static_cast<int>(dx), static_cast<int>(dw),
+                         static_cast<int>(static_cast<unsigned>(a.Kdim) * dx * dw), 0};
+        *reinterpret_cast<v4i*>(a.qrec + 4 * n) = rec;
+      }
+    }
+  } else {
+    // ---- input: one padded row per wave, built in LDS (codes at byte pw * C, the rest zx - o)
+    // and written as 16-byte chunks; codes come in 16-byte loads where a row is a whole number
+    // of them ----
+    __shared__ unsigned char rowbuf[kRtThreads / 64][kStemRowMax];
+    const int wv = t >> 6;
+    const int lane = t & 63;
+    const int row = 4 * (static_cast<int>(blockIdx.x) - a.nfb) + wv;  // n * Hp + hp
+    if (row < a.rows) {
+      unsigned char* buf = rowbuf[wv];
+      const int hp = row % a.Hp;
+      const int n = row / a.Hp;
+      const int hi = hp - a.ph;
+      const int rowb = a.W * a.C;
+      const int wqb = 16 * a.cpr;
+      const int lead = a.pw * a.C;
+      const unsigned pad = static_cast<unsigned>(rt_zero_point<Q>(a.in_qp, n)) - kOff;
+      const bool row_ok = hi >= 0 && hi < a.H;
+      for (int b = lane; b < wqb; b += 64) {
+        if (!row_ok || b < lead || b >= lead + rowb) buf[b] = static_cast<unsigned char>(pad & 0xffu);
+      }
+      if (row_ok) {
+        const float* src = a.x + (static_cast<size_t>(n) * a.H + hi) * rowb;
+        if ((rowb & 3) == 0) {
+          // four 16-byte loads per lane in flight, then their conversions
+          const int nq = rowb / 4;
+          for (int q0 = 0; q0 < nq; q0 += 256) {
+            v4f v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int q = q0 + 64 * i + lane;
+              v[i] = q < nq ? *reinterpret_cast<const v4f*>(src + 4 * q) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int q = q0 + 64 * i + lane;
+              if (q < nq) {
+                unsigned word = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const unsigned u = static_cast<unsigned>(static_cast<int32_t>(v[i][e])) - kOff;
+                  bad |= (u + 128u) > 255u;
+                  word |= (u & 0xffu) << (8 * e);
+                }
+                if ((lead & 3) == 0) {
+                  *reinterpret_cast<unsigned*>(buf + lead + 4 * q) = word;
+                } else {
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) buf[lead + 4 * q + e] = static_cast<unsigned char>(word >> (8 * e));
+                }
+              }
+            }
+          }
+        } else {
+          for (int i = lane; i < rowb; i += 64) {
+            const unsigned u = static_cast<unsigned>(static_cast<int32_t>(src[i])) - kOff;
+            bad |= (u + 128u) > 255u;
+            buf[lead + i] = static_cast<unsigned char>(u & 0xffu);
+          }
+        }
+      }
+      // this wave's LDS writes complete before its reads (one wave's LDS operations are in order)
+      for (int c = lane; c < a.cpr; c += 64) {
+        const v4i o = *reinterpret_cast<const v4i*>(buf + 16 * c);
+        *reinterpret_cast<v4i*>(a.xp + (static_cast<size_t>(row) * a.cpr + c) * 16) = o;
+        store_gap(o);
+      }
+    }
+  }
+  const int any = __syncthreads_or(bad ? 1 : 0);
+  if (t == 0) a.flags[blockIdx.x] = any ? 1 : 0;
+}
+
 struct RouteLayout {
   Geom gp;  // the padded problem the stream kernel runs
   size_t xp_off, wq_off, t_off, q_off, f_off, bytes;
@@ -223,6 +354,36 @@ RouteLayout route_layout(const Geom& g) {
 }
 
 bool rt_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct StemLayout {
+  Geom gp;  // the padded problem the s2d kernel runs: rows of Wq pixels, no padding, the same Ho, Wo
+  size_t xp_off, wq_off, t_off, q_off, f_off, bytes;
+  int nfb, nib, cpr;
+  long long nchunks;
+};
+
+StemLayout stem_layout(const Geom& g) {
+  StemLayout L;
+  L.gp = g;
+  L.gp.H = g.H + 2 * g.ph;
+  int wq = g.W + 2 * g.pw;
+  while ((static_cast<long long>(wq) * g.C) % 16 != 0) ++wq;
+  L.gp.W = wq;
+  L.gp.ph = 0;
+  L.gp.pw = 0;
+  L.cpr = static_cast<int>(static_cast<long long>(wq) * g.C / 16);
+  L.nchunks = static_cast<long long>(g.N) * L.gp.H * L.cpr;
+  const long long kdim = static_cast<long long>(g.R) * g.S * g.C;
+  L.nfb = (g.K + 3) / 4;
+  L.nib = static_cast<int>((static_cast<long long>(g.N) * L.gp.H + 3) / 4);  // 4 padded rows per block
+  L.xp_off = 0;
+  L.wq_off = rt_align(static_cast<size_t>(L.nchunks) * 16);
+  L.t_off = rt_align(L.wq_off + static_cast<size_t>(g.K) * kdim);
+  L.q_off = rt_align(L.t_off + static_cast<size_t>(g.K) * 4);
+  L.f_off = rt_align(L.q_off + static_cast<size_t>(g.N) * 16);
+  L.bytes = rt_align(L.f_off + static_cast<size_t>(L.nfb + L.nib) * 4);
+  return L;
+}
 
 }  // namespace
 
@@ -274,6 +435,72 @@ hipError_t launch_qi32_route(const Geom& g, QpKind qp, const float* x, const flo
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   e = launch_i8_stream_qi32(L.gp, pa.xp, pa.wq, pa.T, pa.qrec, y, stream);
+  if (e != hipSuccess) return e;
+  RouteFallbackArgs fa;
+  fa.x = x; fa.w = w; fa.y = y;
+  fa.in_qp = pa.in_qp; fa.f_qp = pa.f_qp;
+  fa.flags = pa.flags;
+  fa.nflags = L.nfb + L.nib;
+  fa.g = g;
+  fa.total = static_cast<long long>(g.N) * g.Ho * g.Wo * g.K;
+  if (qp == kQpU8) {
+    hipLaunchKernelGGL(qi32_route_fallback_kernel<kQpU8>, dim3(256), dim3(kRtThreads), 0, stream, fa);
+  } else {
+    hipLaunchKernelGGL(qi32_route_fallback_kernel<kQpS5>, dim3(256), dim3(kRtThreads), 0, stream, fa);
+  }
+  return hipGetLastError();
+}
+
+bool qi32_stem_route_eligible(const Geom& g, const BlockGeom& bg, const void* x, const void* w, const void* y,
+                              std::string* why) {
+  auto no = [&](const char* m) {
+    if (why) *why = m;
+    return false;
+  };
+  if (bg.By != 1 || bg.Bx != 1) return no("qi32 stem route takes plain filters only");
+  if (!rt_aligned16(x) || !rt_aligned16(w) || !rt_aligned16(y)) return no("qi32 stem route needs 16-byte aligned x, w and y");
+  if (g.G != 1 || g.C < 1 || g.C > 4 || g.H < 1 || g.W < 1) {
+    return no("qi32 stem route needs groups == 1, 1 <= c <= 4 and a non-empty image");
+  }
+  if (g.ph < 0 || g.pw < 0) return no("qi32 stem route needs padding >= 0");
+  const StemLayout L = stem_layout(g);
+  if (L.nchunks >= (1LL << 31) - kRtThreads || static_cast<long long>(g.N) * L.gp.H >= (1LL << 31) - 4) {
+    return no("qi32 stem route: padded input too large");
+  }
+  if (16LL * L.cpr > kStemRowMax) return no("qi32 stem route needs padded rows of at most 4096 bytes");
+  if (static_cast<long long>(g.N) * g.H * g.W * g.C >= (1LL << 40)) return no("qi32 stem route: input too large");
+  return stem_s2d_qi32_plan_ok(L.gp, why);
+}
+
+size_t qi32_stem_route_workspace_bytes(const Geom& g) { return stem_layout(g).bytes; }
+
+hipError_t launch_qi32_stem_route(const Geom& g, QpKind qp, const float* x, const float* w, int32_t* y,
+                                  const void* in_qp, const void* f_qp, void* ws, hipStream_t stream) {
+  if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
+  const StemLayout L = stem_layout(g);
+  char* base = static_cast<char*>(ws);
+  StemPrepArgs pa;
+  pa.x = x; pa.w = w;
+  pa.in_qp = static_cast<const unsigned char*>(in_qp);
+  pa.f_qp = static_cast<const unsigned char*>(f_qp);
+  pa.xp = reinterpret_cast<int8_t*>(base + L.xp_off);
+  pa.wq = reinterpret_cast<int8_t*>(base + L.wq_off);
+  pa.T = reinterpret_cast<int32_t*>(base + L.t_off);
+  pa.qrec = reinterpret_cast<int32_t*>(base + L.q_off);
+  pa.flags = reinterpret_cast<int32_t*>(base + L.f_off);
+  pa.N = g.N; pa.H = g.H; pa.W = g.W; pa.C = g.C; pa.K = g.K; pa.Kdim = g.R * g.S * g.C;
+  pa.ph = g.ph; pa.pw = g.pw; pa.Hp = L.gp.H; pa.cpr = L.cpr;
+  pa.nfb = L.nfb;
+  pa.rows = g.N * L.gp.H;
+  const dim3 pgrid(static_cast<unsigned>(L.nfb + L.nib));
+  if (qp == kQpU8) {
+    hipLaunchKernelGGL(qi32_stem_prep_kernel<kQpU8>, pgrid, dim3(kRtThreads), 0, stream, pa);
+  } else {
+    hipLaunchKernelGGL(qi32_stem_prep_kernel<kQpS5>, pgrid, dim3(kRtThreads), 0, stream, pa);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = launch_stem_s2d_qi32(L.gp, pa.xp, pa.wq, pa.T, pa.qrec, y, stream);
   if (e != hipSuccess) return e;
   RouteFallbackArgs fa;
   fa.x = x; fa.w = w; fa.y = y;

@@ -38,9 +38,9 @@ constexpr int kSdPitch = 2048;  // bytes per staged s2d row: up to 128 s2d pixel
 struct S2dArgs {
   const int8_t* x;
   const int8_t* w;
-  const int32_t* bias;
-  const float* wscale;
-  int8_t* y;
+  const int32_t* bias;   // int8 outputs: bias; Q32: the filter row sums T (offset codes)
+  const float* wscale;   // int8 outputs: scales; Q32: the per-image records {dx, dw, Kdim * dx * dw, 0}
+  void* y;               // int8, or int32 for Q32
   int H, W, C, K, R, S, Ho, Wo, ph, pw;
   int V, T;             // s2d taps per row (ceil(s/2)) and in all (ceil(r/2) * V)
   int BH, bands_per_img, nbands, nblocks, SEGR;
@@ -149,7 +149,33 @@ __device__ __forceinline__ void s2d_rows(const S2dArgs& a, const unsigned char* 
 
 // FC, FR, FS: the channel count and filter size when fixed at compile time (the 7x7 stem with
 // three channels), 0 where they come from the arguments.
-template <int KB, bool RELU, int FC, int FR, int FS>
+// This lane's window-sum mask of K-block kb: 0x01 at the bytes of its chunk q = 4kb + g (tap
+// (u, v) = (q / V, q % V)) that meet a filter element: byte (2a + b) * C + ch with
+// 2u + a < R, 2v + b < S, ch < C; zero for chunks past T.
+__device__ __forceinline__ v4i s2d_window_mask(int R, int S, int C, int V, int T, int kb, int g) {
+  const int q = 4 * kb + g;
+  const int u = q / V;
+  const int v = q - u * V;
+  v4i m = {0, 0, 0, 0};
+  if (q < T) {
+#pragma unroll
+    for (int byte = 0; byte < 16; ++byte) {
+      const int pc = byte / C;   // pixel (2a + b) of the 2 x 2 block
+      const int ab = pc < 4 ? pc : 4;
+      const bool ok = ab < 4 && 2 * u + (ab >> 1) < R && 2 * v + (ab & 1) < S;
+      if (ok) m[byte >> 2] |= 1 << (8 * (byte & 3));
+    }
+  }
+  return m;
+}
+
+// Q32: the int32 route of the reference's float-code API on offset codes (x' = code - o on an
+// image padded with zx - o, w' = code - o): accumulators start at dx * T(k) + Kdim * dx * dw,
+// each lane sums its chunks' input bytes under s2d_window_mask (v_dot4), the 4 lanes of a
+// pixel add theirs to the window sum W(p), and the store adds dw * W(p); outputs are int32 in
+// natural channel order (MFMA row block j, row rho <-> channel 16j + rho), so the 4 lanes of a
+// pixel write 64 contiguous bytes per instruction.
+template <int KB, bool RELU, int FC, int FR, int FS, bool Q32>
 __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a_in) {
   const S2dArgs a = preload_args(a_in);
   extern __shared__ v4i sd_lds[];
@@ -182,7 +208,11 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
   }
   if (wave == 0) {
     load_lds16(make_rsrc(a.bias ? a.bias + k0 : nullptr, a.bias ? 256 : 0), sd_lds + a.ep_lds / 16, 16u * lane, 0);
-    load_lds16(make_rsrc(a.wscale + k0, 256), sd_lds + a.ep_lds / 16 + 64, 16u * lane, 0);
+    if constexpr (Q32) {
+      load_lds16(make_rsrc(a.wscale + 4 * static_cast<size_t>(n), 16), sd_lds + a.ep_lds / 16 + 64, 16u * lane, 0);
+    } else {
+      load_lds16(make_rsrc(a.wscale + k0, 256), sd_lds + a.ep_lds / 16 + 64, 16u * lane, 0);
+    }
   }
   {
     const int rowb = a.W * a.C;
@@ -217,24 +247,42 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
   }
   __syncthreads();
 
-  // filter fragments: A[kb][j], lane (rho, g) = channel 16*(rho/4) + 4j + rho%4, chunk 4kb + g
+  // filter fragments: A[kb][j], lane (rho, g) = channel 16*(rho/4) + 4j + rho%4 (Q32: 16j +
+  // rho), chunk 4kb + g
   v4i A[KB][4];
   {
     const v4i* slots = sd_lds + a.slot_lds / 16;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) A[kb][j] = slots[s2d_slot(16 * (rho >> 2) + 4 * j + (rho & 3), 4 * kb + g)];
+      for (int j = 0; j < 4; ++j)
+        A[kb][j] = slots[s2d_slot(Q32 ? 16 * j + rho : 16 * (rho >> 2) + 4 * j + (rho & 3), 4 * kb + g)];
   }
-  // bias and requantization multipliers of the lane's channels k0 + 16g + 4j + i
+  // bias and requantization multipliers of the lane's channels k0 + 16g + 4j + i; Q32: the
+  // accumulator start dx * T + Kdim * dx * dw of channels k0 + 16j + 4g + i
   v4i bias_v[4];
   v4f mult_v[4];
+  unsigned qdw = 0;
+  if constexpr (Q32) {
+    const v4i rec = sd_lds[a.ep_lds / 16 + 64];
+    const unsigned dx = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(rec[0]));
+    qdw = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(rec[1]));
+    const unsigned c0 = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(rec[2]));
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    bias_v[j] = sd_lds[a.ep_lds / 16 + 4 * g + j];
-    const v4i ws = sd_lds[a.ep_lds / 16 + 64 + 4 * g + j];
+    for (int j = 0; j < 4; ++j) {
+      const v4i tv = sd_lds[a.ep_lds / 16 + 4 * j + g];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mult_v[j][i] = requant_multiplier(a.act_scale, __int_as_float(ws[i]));
+      for (int i = 0; i < 4; ++i) bias_v[j][i] = static_cast<int>(dx * static_cast<unsigned>(tv[i]) + c0);
+      mult_v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bias_v[j] = sd_lds[a.ep_lds / 16 + 4 * g + j];
+      const v4i ws = sd_lds[a.ep_lds / 16 + 64 + 4 * g + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mult_v[j][i] = requant_multiplier(a.act_scale, __int_as_float(ws[i]));
+    }
   }
   if constexpr (FC != 0) {
     s2d_rows<FC>(a, bytes, sd_lds, tid);
@@ -259,12 +307,12 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
     const int v = q - u * V;
     boff[kb] = base + static_cast<unsigned>(a.s2d_lds + u * kSdPitch + 16 * (rho + v));
   }
+  constexpr int kOutBytes = Q32 ? 4 : 1;
   const size_t out0 = (static_cast<size_t>(n) * a.Ho + ho0) * a.Wo * a.K + k0;
-  const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + out0, band_rows * a.Wo * a.K);
+  const __amdgpu_buffer_rsrc_t ry =
+      make_rsrc(static_cast<char*>(a.y) + out0 * kOutBytes, band_rows * a.Wo * a.K * kOutBytes);
   const int nseg = band_rows * a.SEGR;
 
-  // Software-pipelined by one segment: each matrix instruction of the next segment is issued
-  // with a share of this segment's output stage (mma_requant_steps), so the two overlap.
   auto seg_b = [&](int sg, v4i (&B)[KB]) {
     const int t = fdiv(sg, a.fd_segr);
     const int wo0 = 16 * (sg - t * a.SEGR);
@@ -272,47 +320,113 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) B[kb] = lds_read16(boff[kb] + so);
   };
-  auto store = [&](int sg, const unsigned (&pk)[4]) {
+  // a pixel past the row's end gets an offset 2^30 higher: past num_records, dropped
+  auto out_voff = [&](int sg, int ch) {
     const int t = fdiv(sg, a.fd_segr);
     const int wo = 16 * (sg - t * a.SEGR) + rho;
-    const v4i pkv = {static_cast<int>(pk[0]), static_cast<int>(pk[1]), static_cast<int>(pk[2]),
-                     static_cast<int>(pk[3])};
-    // a pixel past the row's end gets an offset 2^30 higher: past num_records, dropped
-    const unsigned voff = static_cast<unsigned>((t * a.Wo + wo) * a.K + 16 * g) + (static_cast<unsigned>(wo >= a.Wo) << 30);
-    __builtin_amdgcn_raw_buffer_store_b128(pkv, ry, voff, 0, kStoreAux);
-    store_gap(pkv);
+    return static_cast<unsigned>(((t * a.Wo + wo) * a.K + ch) * kOutBytes) + (static_cast<unsigned>(wo >= a.Wo) << 30);
   };
   int sg = wave;
-  if (sg < nseg) {
-    v4i acc[4];
-    {
-      v4i B[KB];
-      seg_b(sg, B);
+  if constexpr (Q32) {
+    // window-sum masks of this lane's chunks
+    v4i wm[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      wm[kb] = s2d_window_mask(FR ? FR : a.R, FS ? FS : a.S, FC ? FC : a.C, FS ? (FS + 1) / 2 : a.V,
+                               FR ? ((FR + 1) / 2) * ((FS + 1) / 2) : a.T, kb, g);
+    }
+    auto mma_seg = [&](const v4i (&B)[KB], v4i (&acc)[4], int& ws) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0][j], B[0], bias_v[j], 0, 0, 0);
 #pragma unroll
       for (int kb = 1; kb < KB; ++kb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[kb][j], B[kb], acc[j], 0, 0, 0);
+      // the dwords that hold input bytes (4C of 16; the rest of a chunk is zero)
+      constexpr int kDw = FC ? (4 * FC + 3) / 4 : 4;
+      ws = 0;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int d = 0; d < kDw; ++d) ws = __builtin_amdgcn_sdot4(B[kb][d], wm[kb][d], ws, false);
+    };
+    auto store32 = [&](int sg_, const v4i (&acc)[4], int ws) {
+      ws += __shfl_xor(ws, 16);
+      ws += __shfl_xor(ws, 32);
+      const unsigned corr = qdw * static_cast<unsigned>(ws);
+      const unsigned vo = out_voff(sg_, 4 * g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v4i v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = static_cast<int>(static_cast<unsigned>(acc[j][i]) + corr);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, vo + 64u * j, 0, kStoreAux);
+        store_gap(v);
+      }
+    };
+    if (sg < nseg) {
+      v4i acc[4];
+      int ws;
+      {
+        v4i B[KB];
+        seg_b(sg, B);
+        mma_seg(B, acc, ws);
+      }
+      for (;;) {
+        const int sn = sg + kSdWaves;
+        if (sn >= nseg) break;
+        v4i B[KB], accn[4];
+        int wsn;
+        seg_b(sn, B);
+        mma_seg(B, accn, wsn);
+        store32(sg, acc, ws);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = accn[j];
+        ws = wsn;
+        sg = sn;
+      }
+      store32(sg, acc, ws);
     }
-    for (;;) {
-      const int sn = sg + kSdWaves;
-      if (sn >= nseg) break;
-      v4i B[KB];
-      seg_b(sn, B);
-      v4i accn[4];
+  } else {
+    auto store = [&](int sg_, const unsigned (&pk)[4]) {
+      const v4i pkv = {static_cast<int>(pk[0]), static_cast<int>(pk[1]), static_cast<int>(pk[2]),
+                       static_cast<int>(pk[3])};
+      __builtin_amdgcn_raw_buffer_store_b128(pkv, ry, out_voff(sg_, 16 * g), 0, kStoreAux);
+      store_gap(pkv);
+    };
+    // Software-pipelined by one segment: each matrix instruction of the next segment is issued
+    // with a share of this segment's output stage (mma_requant_steps), so the two overlap.
+    if (sg < nseg) {
+      v4i acc[4];
+      {
+        v4i B[KB];
+        seg_b(sg, B);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0][j], B[0], bias_v[j], 0, 0, 0);
+#pragma unroll
+        for (int kb = 1; kb < KB; ++kb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[kb][j], B[kb], acc[j], 0, 0, 0);
+      }
+      for (;;) {
+        const int sn = sg + kSdWaves;
+        if (sn >= nseg) break;
+        v4i B[KB];
+        seg_b(sn, B);
+        v4i accn[4];
+        unsigned pk[4];
+        float f[16];
+        mma_requant_steps<KB>(A, B, bias_v, accn, acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+        store(sg, pk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = accn[j];
+        sg = sn;
+      }
       unsigned pk[4];
       float f[16];
-      mma_requant_steps<KB>(A, B, bias_v, accn, acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+      requant_values<0, 16>(acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
       store(sg, pk);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = accn[j];
-      sg = sn;
     }
-    unsigned pk[4];
-    float f[16];
-    requant_values<0, 16>(acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
-    store(sg, pk);
   }
 }
 
@@ -336,7 +450,7 @@ int sd_cu_count() {
 
 int sd_round_up(long long v, int m) { return static_cast<int>((v + m - 1) / m * m); }
 
-bool sd_plan(const Geom& g, S2dPlan* p, std::string* why) {
+bool sd_plan(const Geom& g, S2dPlan* p, std::string* why, int out_bytes = 1) {
   auto no = [&](const char* m) {
     if (why) *why = m;
     return false;
@@ -354,7 +468,9 @@ bool sd_plan(const Geom& g, S2dPlan* p, std::string* why) {
   const long long rowb = static_cast<long long>(g.W) * g.C;
   if (rowb % 16 != 0) return no("s2d stem kernel needs w * c % 16 == 0");
   if (static_cast<long long>(g.H) * rowb >= (1LL << 30)) return no("s2d stem kernel needs images below 2^30 bytes");
-  if (static_cast<long long>(g.Ho) * g.Wo * g.K >= (1LL << 30)) return no("s2d stem kernel needs outputs below 2^30 bytes");
+  if (static_cast<long long>(g.Ho) * g.Wo * g.K * out_bytes >= (1LL << 30)) {
+    return no("s2d stem kernel needs outputs below 2^30 bytes per image");
+  }
   const int segr = (g.Wo + 15) / 16;
   p->ncols = 16 * segr + p->V - 1;
   if (p->ncols > kSdPitch / 16) return no("s2d stem kernel needs output width + ceil(s/2) <= 113");
@@ -419,13 +535,12 @@ bool stem_s2d_eligible(const Geom& g, const void* x, const void* w, const void* 
   return sd_plan(g, &pl, why);
 }
 
-hipError_t launch_i8_stem_s2d(const Geom& g, const int8_t* x, const int8_t* w, int8_t* y, const Requant& rq,
-                              hipStream_t stream) {
-  if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
-  S2dPlan pl;
-  if (!sd_plan(g, &pl, nullptr)) return hipErrorInvalidConfiguration;
+namespace {
+
+S2dArgs sd_args(const Geom& g, const S2dPlan& pl, const int8_t* x, const int8_t* w, void* y, const int32_t* bias,
+                const float* wscale, float act_scale) {
   S2dArgs a;
-  a.x = x; a.w = w; a.bias = rq.bias; a.wscale = rq.wscale; a.y = y;
+  a.x = x; a.w = w; a.bias = bias; a.wscale = wscale; a.y = y;
   a.H = g.H; a.W = g.W; a.C = g.C; a.K = g.K; a.R = g.R; a.S = g.S; a.Ho = g.Ho; a.Wo = g.Wo;
   a.ph = g.ph; a.pw = g.pw;
   a.V = pl.V; a.T = pl.T;
@@ -437,26 +552,68 @@ hipError_t launch_i8_stem_s2d(const Geom& g, const int8_t* x, const int8_t* w, i
   a.RSC = g.R * g.S * g.C; a.nfilt = pl.nfilt;
   a.filt_lds = pl.filt_lds; a.ep_lds = pl.ep_lds; a.slot_lds = pl.slot_lds; a.raw_lds = pl.raw_lds;
   a.s2d_lds = pl.s2d_lds;
-  a.act_scale = rq.act_scale;
+  a.act_scale = act_scale;
   a.fd_nbands = fastdiv_m(a.nbands);
   a.fd_bpi = fastdiv_m(pl.bands_per_img);
   a.fd_segr = fastdiv_m(a.SEGR);
   a.fd_rowsld = fastdiv_m(pl.rows_ld);
   a.fd_ncols = fastdiv_m(pl.ncols);
-  auto go = [&](auto kern) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(pl.lds));
-    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(a.nblocks)), dim3(64 * kSdWaves), pl.lds, stream, a);
-  };
+  return a;
+}
+
+template <typename Kern>
+void sd_go(Kern kern, const S2dArgs& a, const S2dPlan& pl, hipStream_t stream) {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(pl.lds));
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(a.nblocks)), dim3(64 * kSdWaves), pl.lds, stream, a);
+}
+
+}  // namespace
+
+hipError_t launch_i8_stem_s2d(const Geom& g, const int8_t* x, const int8_t* w, int8_t* y, const Requant& rq,
+                              hipStream_t stream) {
+  if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
+  S2dPlan pl;
+  if (!sd_plan(g, &pl, nullptr)) return hipErrorInvalidConfiguration;
+  const S2dArgs a = sd_args(g, pl, x, w, y, rq.bias, rq.wscale, rq.act_scale);
   const bool relu = rq.relu != 0;
   if (g.C == 3 && g.R == 7 && g.S == 7) {
-    relu ? go(i8_stem_s2d_kernel<4, true, 3, 7, 7>) : go(i8_stem_s2d_kernel<4, false, 3, 7, 7>);
+    relu ? sd_go(i8_stem_s2d_kernel<4, true, 3, 7, 7, false>, a, pl, stream)
+         : sd_go(i8_stem_s2d_kernel<4, false, 3, 7, 7, false>, a, pl, stream);
   } else {
     switch (pl.KB) {
-      case 1: relu ? go(i8_stem_s2d_kernel<1, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<1, false, 0, 0, 0>); break;
-      case 2: relu ? go(i8_stem_s2d_kernel<2, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<2, false, 0, 0, 0>); break;
-      case 3: relu ? go(i8_stem_s2d_kernel<3, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<3, false, 0, 0, 0>); break;
-      default: relu ? go(i8_stem_s2d_kernel<4, true, 0, 0, 0>) : go(i8_stem_s2d_kernel<4, false, 0, 0, 0>); break;
+      case 1: relu ? sd_go(i8_stem_s2d_kernel<1, true, 0, 0, 0, false>, a, pl, stream)
+                   : sd_go(i8_stem_s2d_kernel<1, false, 0, 0, 0, false>, a, pl, stream); break;
+      case 2: relu ? sd_go(i8_stem_s2d_kernel<2, true, 0, 0, 0, false>, a, pl, stream)
+                   : sd_go(i8_stem_s2d_kernel<2, false, 0, 0, 0, false>, a, pl, stream); break;
+      case 3: relu ? sd_go(i8_stem_s2d_kernel<3, true, 0, 0, 0, false>, a, pl, stream)
+                   : sd_go(i8_stem_s2d_kernel<3, false, 0, 0, 0, false>, a, pl, stream); break;
+      default: relu ? sd_go(i8_stem_s2d_kernel<4, true, 0, 0, 0, false>, a, pl, stream)
+                    : sd_go(i8_stem_s2d_kernel<4, false, 0, 0, 0, false>, a, pl, stream); break;
+    }
+  }
+  return hipGetLastError();
+}
+
+bool stem_s2d_qi32_plan_ok(const Geom& g, std::string* why) {
+  S2dPlan pl;
+  return sd_plan(g, &pl, why, 4);
+}
+
+hipError_t launch_stem_s2d_qi32(const Geom& g, const int8_t* x, const int8_t* w, const int32_t* T,
+                                const int32_t* qrec, int32_t* y, hipStream_t stream) {
+  if (static_cast<long long>(g.N) * g.Ho * g.Wo * g.K == 0) return hipSuccess;
+  S2dPlan pl;
+  if (!sd_plan(g, &pl, nullptr, 4)) return hipErrorInvalidConfiguration;
+  const S2dArgs a = sd_args(g, pl, x, w, y, T, reinterpret_cast<const float*>(qrec), 1.0f);
+  if (g.C == 3 && g.R == 7 && g.S == 7) {
+    sd_go(i8_stem_s2d_kernel<4, false, 3, 7, 7, true>, a, pl, stream);
+  } else {
+    switch (pl.KB) {
+      case 1: sd_go(i8_stem_s2d_kernel<1, false, 0, 0, 0, true>, a, pl, stream); break;
+      case 2: sd_go(i8_stem_s2d_kernel<2, false, 0, 0, 0, true>, a, pl, stream); break;
+      case 3: sd_go(i8_stem_s2d_kernel<3, false, 0, 0, 0, true>, a, pl, stream); break;
+      default: sd_go(i8_stem_s2d_kernel<4, false, 0, 0, 0, true>, a, pl, stream); break;
     }
   }
   return hipGetLastError();

@@ -68,6 +68,7 @@ QI32_FULL = {
     "c2_u8": ("u8", "r50_3x3", (0.0, 255.0), 7100),
     "c2_s5": ("s5", "r50_3x3", (-16.0, 15.0), 7200),
     "c4_u8": ("u8", "down_s2", (0.0, 255.0), 7300),
+    "c5_u8": ("u8", "stem", (0.0, 255.0), 7400),
 }
 
 

@@ -1,7 +1,7 @@
-"""The float-code convolution (launch_fprop_nhwc_qi32, the reference's own API) at the full C2
-and C4 sizes against the sha256 of the reference's cpu_fprop_nhwc_qi32 on the same inputs
+"""The float-code convolution (launch_fprop_nhwc_qi32, the reference's own API) at the full C2,
+C4 and C5 sizes against the sha256 of the reference's cpu_fprop_nhwc_qi32 on the same inputs
 (tests/golden/qi32_full.json, written from oracle/_ref): AUTO (the row-band kernel on C2, the
-stream route on C4), the caller-workspace entry point miq_fprop_nhwc_qi32_ws, and that entry
+stream route on C4, the stem route on C5), the caller-workspace entry point miq_fprop_nhwc_qi32_ws, and that entry
 point recorded into a HIP graph and replayed, with eager work and synchronisations between
 replays and no device memory allocated by the captured call."""
 import hashlib
@@ -16,7 +16,7 @@ from tests.test_gpu_parity import dev, qparams_dev
 
 pytestmark = pytest.mark.gpu
 
-PLAN = {"c2_u8": "band", "c2_s5": "band", "c4_u8": "stream"}
+PLAN = {"c2_u8": "band", "c2_s5": "band", "c4_u8": "stream", "c5_u8": "stem_s2d"}
 
 
 def _problem(name, device):
@@ -62,7 +62,7 @@ def test_qi32_full_size_matches_reference_sha(device, name):
     assert _sha(y2) == g["sha256"]
 
 
-@pytest.mark.parametrize("name", ["c2_u8", "c4_u8"])
+@pytest.mark.parametrize("name", ["c2_u8", "c4_u8", "c5_u8"])
 def test_qi32_ws_in_a_graph(device, name):
     g = cases.qi32_full_goldens()[name]
     pr = _problem(name, device)

@@ -118,7 +118,7 @@ def test_oracle_against_reference_random():
 
 @pytest.mark.parametrize("name", list(cases.QI32_FULL))
 def test_qi32_full_size_against_reference_sha(name):
-    """The oracle's float-code convolution at the full C2 / C4 sizes equals the reference's own
+    """The oracle's float-code convolution at the full C2 / C4 / C5 sizes equals the reference's own
     cpu_fprop_nhwc_qi32 on the same inputs (sha256 of the int32 outputs, written from
     oracle/_ref by tests/golden/make_qi32_full.py)."""
     g = cases.qi32_full_goldens()[name]
