@@ -175,6 +175,57 @@ __device__ __forceinline__ void mma_requant_steps(const v4i (&A)[KB][4], const v
   }
 }
 
+// Stage S of value V (= 4j + r) of requant_magic, one instruction each: 0 convert, 1 scale,
+// 2 clamp, 3 round (+ 1.5 * 2^23).  Same operations and order as requant_magic, so the same
+// bits.
+template <int V, int S>
+__device__ __forceinline__ void requant_stage(const v4i (&acc)[4], const v4f (&mult)[4], float lo, float (&c)[16]) {
+  if constexpr (V >= 0 && V < 16) {
+    if constexpr (S == 0) c[V] = static_cast<float>(acc[V / 4][V % 4]);
+    if constexpr (S == 1) c[V] = c[V] * mult[V / 4][V % 4];
+    if constexpr (S == 2) c[V] = __builtin_amdgcn_fmed3f(c[V], lo, 127.0f);
+    if constexpr (S == 3) c[V] = c[V] + 12582912.0f;
+  }
+}
+
+// The output stage of gap I of a 16-MFMA segment step, software-pipelined over the values:
+// stage 3 of value I - 3, 2 of I - 2, 1 of I - 1 and 0 of I, so the gap's four instructions
+// are independent of each other (a value's four stages are a chain of dependent
+// instructions, and one value per gap would issue them back to back).  A word is packed in
+// the gap that rounds its last value.
+template <int I>
+__device__ __forceinline__ void requant_gap(const v4i (&acc)[4], const v4f (&mult)[4], float lo, float (&c)[16],
+                                            unsigned (&pk)[4]) {
+  requant_stage<I - 3, 3>(acc, mult, lo, c);
+  requant_stage<I - 2, 2>(acc, mult, lo, c);
+  requant_stage<I - 1, 1>(acc, mult, lo, c);
+  requant_stage<I, 0>(acc, mult, lo, c);
+  if constexpr (I - 3 >= 0 && I - 3 < 16 && (I - 3) % 4 == 3) {
+    constexpr int V = I - 3;
+    pk[V / 4] = pack4_magic(c[V - 3], c[V - 2], c[V - 1], c[V]);
+  }
+}
+
+// mma_requant_steps for KB = 4 (one value per matrix instruction) with the pipelined output
+// stage; the last three values' remaining stages (gaps 16 to 18) follow the last MFMA.
+template <int I = 0>
+__device__ __forceinline__ void mma_requant_pipe4(const v4i (&A)[4][4], const v4i (&B)[4], const v4i (&bias)[4],
+                                                  v4i (&accn)[4], const v4i (&acc)[4], const v4f (&mult)[4], float lo,
+                                                  float (&c)[16], unsigned (&pk)[4]) {
+  if constexpr (I < 16) {
+    constexpr int b = I / 4;
+    constexpr int j = I % 4;
+    accn[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][j], B[b], b == 0 ? bias[j] : accn[j], 0, 0, 0);
+    requant_gap<I>(acc, mult, lo, c, pk);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_requant_pipe4<I + 1>(A, B, bias, accn, acc, mult, lo, c, pk);
+  } else {
+    requant_gap<16>(acc, mult, lo, c, pk);
+    requant_gap<17>(acc, mult, lo, c, pk);
+    requant_gap<18>(acc, mult, lo, c, pk);
+  }
+}
+
 // Wait states after a 16-byte store before another instruction may overwrite its data
 // registers.  A vector-memory store of more than 64 bits needs one wait state before a
 // VALU write of its data VGPRs; the compiler leaves none when the store ends a loop body

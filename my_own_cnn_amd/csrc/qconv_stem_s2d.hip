@@ -19,9 +19,10 @@
 // read is free of bank conflicts) with VALU work once per byte, and keeps the filter
 // fragments in registers.  Each wave then takes 16-pixel segments of the band's output rows
 // in turn; the matrix instructions of the next segment are issued before the requantization
-// of the current one, so the two overlap.  The output stage is the other int8 kernels'
-// (bias as the first MFMA's C operand; convert, scale, clamp, round; one 16-byte store of
-// 16 consecutive channels per lane, followed by store_gap()).
+// of the current one (mma_requant_pipe4 for the 16-chunk filters), so the two overlap.  The
+// output stage is the other int8 kernels' (bias as the first MFMA's C operand; convert,
+// scale, clamp, round; one 16-byte store of 16 consecutive channels per lane, followed by
+// store_gap()).
 
 #include "qconv_device.h"
 
@@ -49,7 +50,7 @@ struct S2dArgs {
   int RSC, nfilt;       // filter bytes per channel, filter load instructions
   int filt_lds, ep_lds, slot_lds, raw_lds, s2d_lds;
   float act_scale;
-  FastDivM fd_nbands, fd_bpi, fd_segr, fd_rowsld, fd_ncols;
+  FastDivM fd_nbands, fd_bpi, fd_segr, fd_rowsld, fd_npairs;
 };
 
 static_assert(sizeof(S2dArgs) <= 256, "kernel arguments fit one s_load batch");
@@ -64,9 +65,21 @@ __device__ __forceinline__ unsigned long long lds_bytes8(const unsigned char* ba
   return static_cast<unsigned long long>(lo) | (static_cast<unsigned long long>(hi) << 32);
 }
 
-// Filter chunk q of channel kl sits at 16-byte slot 16 kl + ((q + kl + 4 (kl / 16)) mod 16): the
-// 16 lanes of an MFMA lane group read 16 distinct slots modulo 16.
-__device__ __forceinline__ int s2d_slot(int kl, int q) { return 16 * kl + ((q + kl + 4 * (kl >> 4)) & 15); }
+// Filter chunk q of channel kl sits at 16-byte slot 16 kl + ((q + 2 kl + 8 (kl / 16)) mod 16).  A
+// ds_read_b128 serves 16 lanes per cycle: one half-wave's lane quads 4i .. 4i + 3 whose quad
+// index i has one popcount parity.  In both channel orders of the fragments (int8 outputs and
+// int32 outputs) those 16 lanes read 16 distinct slots modulo 16, so the fragment reads are free
+// of bank conflicts.
+__device__ __forceinline__ int s2d_slot(int kl, int q) { return 16 * kl + ((q + 2 * kl + 8 * (kl >> 4)) & 15); }
+
+// 16 bytes to LDS byte address addr, issued by inline assembly: the compiler puts a wait for
+// all of the wave's outstanding global -> LDS loads in front of any LDS store it emits (it
+// cannot tell the loads' LDS destinations apart), and the filter chunks are written while the
+// input rows are still loading.  The caller waits for lgkmcnt(0) before the barrier that
+// publishes the stores.
+__device__ __forceinline__ void sd_lds_store16(unsigned addr, v4i v) {
+  asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
 
 // 2C bytes (C <= 4) from byte o of an LDS byte array (any alignment), in the low bytes.
 template <int C>
@@ -94,13 +107,13 @@ __device__ __forceinline__ v4i s2d_chunk(unsigned long long lo, unsigned long lo
 // bytes of filter row 2u + a, columns 2v and 2v + 1 (contiguous in KRSC); a column 2v + 1 = s
 // or a row 2u + a >= r contributes zeros; chunks past T are zero.
 template <int C, int FR, int FS>
-__device__ __forceinline__ void s2d_filter(const S2dArgs& a, const unsigned char* bytes, v4i* lds, int tid) {
+__device__ __forceinline__ void s2d_filter(const S2dArgs& a, const unsigned char* bytes, unsigned base, int tid) {
   const int R = FR ? FR : a.R;
   const int S = FS ? FS : a.S;
   const int V = FS ? (FS + 1) / 2 : a.V;
   const int T = FR ? ((FR + 1) / 2) * V : a.T;
   const unsigned char* fb = bytes + a.filt_lds;
-  v4i* slots = lds + a.slot_lds / 16;
+  const unsigned slots = base + static_cast<unsigned>(a.slot_lds);
   const int rowc = S * C;  // bytes of one filter row
   for (int idx = tid; idx < 64 * 16; idx += 64 * kSdWaves) {
     const int kl = idx >> 4;
@@ -117,33 +130,72 @@ __device__ __forceinline__ void s2d_filter(const S2dArgs& a, const unsigned char
         if (r < R) piece[r2] = lds_pair<C>(fb, kl * (R * rowc) + r * rowc + 2 * v * C) & keep;
       }
     }
-    slots[s2d_slot(kl, q)] = s2d_chunk<C>(piece[0], piece[1]);
+    sd_lds_store16(slots + 16u * static_cast<unsigned>(s2d_slot(kl, q)), s2d_chunk<C>(piece[0], piece[1]));
+  }
+}
+
+// The 4C bytes of an s2d pixel pair (2m, 2m + 1) in one staged row, from the four dwords at
+// and after its first byte's dword (sh = that byte's offset inside it): the first pixel's 2C
+// bytes in p0, the second's in p1.
+template <int C>
+__device__ __forceinline__ void s2d_pair_pieces(const unsigned (&w)[4], unsigned sh, unsigned long long& p0,
+                                                unsigned long long& p1) {
+  const unsigned a0 = __builtin_amdgcn_alignbyte(w[1], w[0], sh);
+  const unsigned a1 = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
+  const unsigned a2 = __builtin_amdgcn_alignbyte(w[3], w[2], sh);
+  const unsigned long long lo = static_cast<unsigned long long>(a0) | (static_cast<unsigned long long>(a1) << 32);
+  if constexpr (C == 4) {
+    // 4C = 16 bytes: the pair starts on a dword (PLB and pw C = 4 pw are multiples of 4), sh = 0
+    p0 = lo;
+    p1 = static_cast<unsigned long long>(w[2]) | (static_cast<unsigned long long>(w[3]) << 32);
+  } else {
+    constexpr unsigned long long keep = (1ull << (16 * C)) - 1ull;
+    const unsigned long long hi = static_cast<unsigned long long>(a2);
+    p0 = lo & keep;
+    p1 = ((lo >> (16 * C)) | (hi << (64 - 16 * C))) & keep;
   }
 }
 
 // The band's s2d rows: pixel (I, J) from staged input rows 2I and 2I + 1, 2C bytes each at
-// byte PLB + (2J - pw) * C.  Four pixels per thread and pass, their reads issued before their
-// writes (the compiler keeps LDS writes and later LDS reads in order).
+// byte PLB + (2J - pw) * C.  A thread builds pixel pairs (2m, 2m + 1): the pair's 4C bytes of a
+// row start at a byte offset sh = (PLB - pw C) mod 4 that is the same for every pair, so each
+// row is read as four aligned dwords, consecutive lanes 12 bytes apart (distinct banks).  Two
+// pairs per thread and pass, their reads issued before their writes.  A pair past the last
+// column (ncols odd) writes the unused slot ncols.
 template <int C>
 __device__ __forceinline__ void s2d_rows(const S2dArgs& a, const unsigned char* bytes, v4i* lds, int tid) {
-  constexpr int kU = 4;
-  const unsigned char* raw = bytes + a.raw_lds;
-  const int total = a.HS * a.ncols;
+  constexpr int kU = 2;
+  const unsigned* raw = reinterpret_cast<const unsigned*>(bytes + a.raw_lds);
+  const int npairs = (a.ncols + 1) >> 1;
+  const int total = a.HS * npairs;
+  const int o0 = a.PLB - a.pw * C;  // >= 0: PLB is pw * C rounded up to 16
+  const unsigned sh = static_cast<unsigned>(o0 & 3);
   for (int idx0 = tid; idx0 < total; idx0 += kU * 64 * kSdWaves) {
-    unsigned long long r0[kU], r1[kU];
+    unsigned w0[kU][4], w1[kU][4];
     int dst[kU];
 #pragma unroll
     for (int e = 0; e < kU; ++e) {
-      const int idx = min(idx0 + e * 64 * kSdWaves, total - 1);  // repeats the last pixel past the end
-      const int I = fdiv(idx, a.fd_ncols);
-      const int J = idx - I * a.ncols;
-      const int o = a.PLB + (2 * J - a.pw) * C;
-      r0[e] = lds_pair<C>(raw + (2 * I) * a.P, o);
-      r1[e] = lds_pair<C>(raw + (2 * I + 1) * a.P, o);
-      dst[e] = (a.s2d_lds + I * kSdPitch) / 16 + J;
+      const int idx = min(idx0 + e * 64 * kSdWaves, total - 1);  // repeats the last pair past the end
+      const int I = fdiv(idx, a.fd_npairs);
+      const int m = idx - I * npairs;
+      const int d = (o0 + 4 * m * C) >> 2;
+      const unsigned* r0 = raw + (2 * I) * (a.P >> 2) + d;
+      const unsigned* r1 = r0 + (a.P >> 2);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        w0[e][k] = r0[k];
+        w1[e][k] = r1[k];
+      }
+      dst[e] = (a.s2d_lds + I * kSdPitch) / 16 + 2 * m;
     }
 #pragma unroll
-    for (int e = 0; e < kU; ++e) lds[dst[e]] = s2d_chunk<C>(r0[e], r1[e]);
+    for (int e = 0; e < kU; ++e) {
+      unsigned long long x0, x1, y0, y1;
+      s2d_pair_pieces<C>(w0[e], sh, x0, x1);
+      s2d_pair_pieces<C>(w1[e], sh, y0, y1);
+      lds[dst[e]] = s2d_chunk<C>(x0, y0);
+      lds[dst[e] + 1] = s2d_chunk<C>(x1, y1);
+    }
   }
 }
 
@@ -214,11 +266,11 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
       load_lds16(make_rsrc(a.wscale + k0, 256), sd_lds + a.ep_lds / 16 + 64, 16u * lane, 0);
     }
   }
+  const int ni = 2 * a.HS * a.rows_ld;
   {
     const int rowb = a.W * a.C;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + static_cast<size_t>(n) * a.H * rowb, a.H * rowb);
     const int hi0 = 2 * ho0 - a.ph;
-    const int ni = 2 * a.HS * a.rows_ld;
     for (int i = wave; i < ni; i += kSdWaves) {
       const int rr = fdiv(i, a.fd_rowsld);
       const int m = i - rr * a.rows_ld;
@@ -230,22 +282,23 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
       load_lds16(rx, sd_lds + a.raw_lds / 16 + i * 64, voff, soff);
     }
   }
-  wait_vmcnt(0);
+  // ---- the filter and parameter loads (issued before the rows, and loads complete in order)
+  // have landed once this wave has at most its row loads outstanding; the filter chunks and
+  // the fragments' register copy then overlap the input rows' loads ----
+  wait_vmcnt(ni > wave ? (ni - wave + kSdWaves - 1) / kSdWaves : 0);
   barrier_only();
-
-  // ---- filter chunks, then (while the fragments are read) the s2d rows; compile-time channel
-  // count ----
   if constexpr (FC != 0) {
-    s2d_filter<FC, FR, FS>(a, bytes, sd_lds, tid);
+    s2d_filter<FC, FR, FS>(a, bytes, base, tid);
   } else {
     switch (a.C) {
-      case 1: s2d_filter<1, 0, 0>(a, bytes, sd_lds, tid); break;
-      case 2: s2d_filter<2, 0, 0>(a, bytes, sd_lds, tid); break;
-      case 3: s2d_filter<3, 0, 0>(a, bytes, sd_lds, tid); break;
-      default: s2d_filter<4, 0, 0>(a, bytes, sd_lds, tid); break;
+      case 1: s2d_filter<1, 0, 0>(a, bytes, base, tid); break;
+      case 2: s2d_filter<2, 0, 0>(a, bytes, base, tid); break;
+      case 3: s2d_filter<3, 0, 0>(a, bytes, base, tid); break;
+      default: s2d_filter<4, 0, 0>(a, bytes, base, tid); break;
     }
   }
-  __syncthreads();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  barrier_only();
 
   // filter fragments: A[kb][j], lane (rho, g) = channel 16*(rho/4) + 4j + rho%4 (Q32: 16j +
   // rho), chunk 4kb + g
@@ -284,6 +337,9 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
       for (int i = 0; i < 4; ++i) mult_v[j][i] = requant_multiplier(a.act_scale, __int_as_float(ws[i]));
     }
   }
+  // ---- the input rows have landed: the s2d rows ----
+  wait_vmcnt(0);
+  barrier_only();
   if constexpr (FC != 0) {
     s2d_rows<FC>(a, bytes, sd_lds, tid);
   } else {
@@ -416,7 +472,11 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
         v4i accn[4];
         unsigned pk[4];
         float f[16];
-        mma_requant_steps<KB>(A, B, bias_v, accn, acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+        if constexpr (KB == 4) {
+          mma_requant_pipe4(A, B, bias_v, accn, acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+        } else {
+          mma_requant_steps<KB>(A, B, bias_v, accn, acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+        }
         store(sg, pk);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = accn[j];
@@ -475,8 +535,8 @@ bool sd_plan(const Geom& g, S2dPlan* p, std::string* why, int out_bytes = 1) {
   p->ncols = 16 * segr + p->V - 1;
   if (p->ncols > kSdPitch / 16) return no("s2d stem kernel needs output width + ceil(s/2) <= 113");
   p->PLB = sd_round_up(static_cast<long long>(g.pw) * g.C, 16);
-  // the last byte a conversion read touches: 12 bytes from the last column's first byte
-  const long long last = p->PLB + (2LL * (p->ncols - 1) - g.pw) * g.C + 12;
+  // the end of the last row read: four dwords from the last pixel pair's first byte
+  const long long last = p->PLB + (4LL * ((p->ncols + 1) / 2 - 1) - g.pw) * g.C + 16;
   p->P = sd_round_up(std::max<long long>(p->PLB + rowb, last), 1024);
   p->rows_ld = p->P / 1024;
   const long long RSC = static_cast<long long>(g.R) * g.S * g.C;
@@ -557,7 +617,7 @@ S2dArgs sd_args(const Geom& g, const S2dPlan& pl, const int8_t* x, const int8_t*
   a.fd_bpi = fastdiv_m(pl.bands_per_img);
   a.fd_segr = fastdiv_m(a.SEGR);
   a.fd_rowsld = fastdiv_m(pl.rows_ld);
-  a.fd_ncols = fastdiv_m(pl.ncols);
+  a.fd_npairs = fastdiv_m((pl.ncols + 1) / 2);
   return a;
 }
 
