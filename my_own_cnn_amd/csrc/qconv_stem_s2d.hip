@@ -134,6 +134,59 @@ __device__ __forceinline__ void s2d_filter(const S2dArgs& a, const unsigned char
   }
 }
 
+// The 7x7 three-channel filter's chunks, a thread per (channel kl, tap row u) = (t / 4, t % 4):
+// filter rows 2u and 2u + 1 (21 bytes each; row 7 does not exist) read as seven aligned
+// dwords each, their column pairs v = 0 .. 3 (6 bytes at 6v; v = 3 holds column 6 only) the
+// chunks (u, v).  A ds_write_b128 stores 8 consecutive lanes per cycle (128 bytes, measured:
+// its bank conflicts follow slot mod 8 over those lanes, unlike the reads).  The thread writes
+// chunk (v + lane / 2 + 2 (lane / 4)) mod 4 in its v-th store, which puts every 8 consecutive
+// lanes on 8 distinct slots modulo 8.
+__device__ __forceinline__ void s2d_filter_773(const S2dArgs& a, const unsigned char* bytes, unsigned base, int tid) {
+  const unsigned* fw = reinterpret_cast<const unsigned*>(bytes + a.filt_lds);
+  const unsigned slots = base + static_cast<unsigned>(a.slot_lds);
+  const int rot = (tid >> 1) + 2 * (tid >> 2);
+  for (int t = tid; t < 64 * 4; t += 64 * kSdWaves) {
+    const int kl = t >> 2;
+    const int u = t & 3;
+    unsigned long long pc[2][4];
+#pragma unroll
+    for (int r2 = 0; r2 < 2; ++r2) {
+      const int r = 2 * u + r2;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) pc[r2][v] = 0ull;
+      if (r < 7) {
+        const int s0 = kl * 147 + r * 21;
+        const unsigned* p = fw + (s0 >> 2);
+        const unsigned sh = static_cast<unsigned>(s0 & 3);
+        unsigned w[7];
+#pragma unroll
+        for (int k = 0; k < 7; ++k) w[k] = p[k];
+        unsigned al[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) al[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], sh);
+        const unsigned long long w01 = al[0] | (static_cast<unsigned long long>(al[1]) << 32);
+        const unsigned long long w23 = al[2] | (static_cast<unsigned long long>(al[3]) << 32);
+        const unsigned long long w45 = al[4] | (static_cast<unsigned long long>(al[5]) << 32);
+        constexpr unsigned long long k6 = (1ull << 48) - 1ull;
+        pc[r2][0] = w01 & k6;                             // bytes 0 .. 5
+        pc[r2][1] = ((w01 >> 48) | (w23 << 16)) & k6;     // bytes 6 .. 11
+        pc[r2][2] = ((w23 >> 32) | (w45 << 32)) & k6;     // bytes 12 .. 17
+        pc[r2][3] = (w45 >> 16) & ((1ull << 24) - 1ull);  // bytes 18 .. 20 (column 6)
+      }
+    }
+    v4i ch[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) ch[v] = s2d_chunk<3>(pc[0][v], pc[1][v]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int vv = (v + rot) & 3;
+      const v4i c01 = (vv & 1) ? ch[1] : ch[0];
+      const v4i c23 = (vv & 1) ? ch[3] : ch[2];
+      sd_lds_store16(slots + 16u * static_cast<unsigned>(s2d_slot(kl, 4 * u + vv)), (vv & 2) ? c23 : c01);
+    }
+  }
+}
+
 // The 4C bytes of an s2d pixel pair (2m, 2m + 1) in one staged row, from the four dwords at
 // and after its first byte's dword (sh = that byte's offset inside it): the first pixel's 2C
 // bytes in p0, the second's in p1.
@@ -159,9 +212,10 @@ __device__ __forceinline__ void s2d_pair_pieces(const unsigned (&w)[4], unsigned
 // The band's s2d rows: pixel (I, J) from staged input rows 2I and 2I + 1, 2C bytes each at
 // byte PLB + (2J - pw) * C.  A thread builds pixel pairs (2m, 2m + 1): the pair's 4C bytes of a
 // row start at a byte offset sh = (PLB - pw C) mod 4 that is the same for every pair, so each
-// row is read as four aligned dwords, consecutive lanes 12 bytes apart (distinct banks).  Two
-// pairs per thread and pass, their reads issued before their writes.  A pair past the last
-// column (ncols odd) writes the unused slot ncols.
+// row is read as four aligned dwords, consecutive lanes 12 bytes apart (distinct banks).  Lanes
+// 4 .. 7 of every 8 write the pair's second chunk first, so the 8 consecutive lanes of each
+// ds_write_b128 cycle meet 8 distinct slots modulo 8.  Two pairs per thread and pass, their reads issued before
+// their writes.  A pair past the last column (ncols odd) writes the unused slot ncols.
 template <int C>
 __device__ __forceinline__ void s2d_rows(const S2dArgs& a, const unsigned char* bytes, v4i* lds, int tid) {
   constexpr int kU = 2;
@@ -193,8 +247,11 @@ __device__ __forceinline__ void s2d_rows(const S2dArgs& a, const unsigned char* 
       unsigned long long x0, x1, y0, y1;
       s2d_pair_pieces<C>(w0[e], sh, x0, x1);
       s2d_pair_pieces<C>(w1[e], sh, y0, y1);
-      lds[dst[e]] = s2d_chunk<C>(x0, y0);
-      lds[dst[e] + 1] = s2d_chunk<C>(x1, y1);
+      const v4i c0 = s2d_chunk<C>(x0, y0);
+      const v4i c1 = s2d_chunk<C>(x1, y1);
+      const bool sw = (tid >> 2) & 1;
+      lds[dst[e] + (sw ? 1 : 0)] = sw ? c1 : c0;
+      lds[dst[e] + (sw ? 0 : 1)] = sw ? c0 : c1;
     }
   }
 }
@@ -288,7 +345,11 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
   wait_vmcnt(ni > wave ? (ni - wave + kSdWaves - 1) / kSdWaves : 0);
   barrier_only();
   if constexpr (FC != 0) {
-    s2d_filter<FC, FR, FS>(a, bytes, base, tid);
+    if constexpr (FC == 3 && FR == 7 && FS == 7) {
+      s2d_filter_773(a, bytes, base, tid);
+    } else {
+      s2d_filter<FC, FR, FS>(a, bytes, base, tid);
+    }
   } else {
     switch (a.C) {
       case 1: s2d_filter<1, 0, 0>(a, bytes, base, tid); break;
