@@ -164,8 +164,23 @@ struct RouteFallbackArgs {
 // every output in the reference's loop order (codes truncated, centred, padded taps skipped).
 template <QpKind Q>
 __global__ void __launch_bounds__(kRtThreads) qi32_route_fallback_kernel(RouteFallbackArgs a) {
+  // the flags in 16-byte loads, eight in flight per thread (a loop of dependent 4-byte loads
+  // paid one L2 round trip per flag group); the scalar tail and unaligned workspaces word by word
   int any = 0;
-  for (int i = threadIdx.x; i < a.nflags; i += kRtThreads) any |= a.flags[i];
+  const bool vec = (reinterpret_cast<uintptr_t>(a.flags) & 15u) == 0;
+  const int nv = vec ? a.nflags >> 2 : 0;
+  const v4i* f4 = reinterpret_cast<const v4i*>(a.flags);
+  for (int i0 = threadIdx.x; i0 < nv; i0 += 8 * kRtThreads) {
+    v4i f[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kRtThreads;
+      f[u] = i < nv ? f4[i] : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) any |= f[u][0] | f[u][1] | f[u][2] | f[u][3];
+  }
+  for (int i = 4 * nv + static_cast<int>(threadIdx.x); i < a.nflags; i += kRtThreads) any |= a.flags[i];
   if (!__syncthreads_or(any)) return;
   const Geom& g = a.g;
   const int zw = rt_zero_point<Q>(a.f_qp, 0);
@@ -233,11 +248,22 @@ __global__ void __launch_bounds__(kRtThreads) qi32_stem_prep_kernel(StemPrepArgs
     if (c < a.K) {
       const float* src = a.w + static_cast<size_t>(c) * a.Kdim;
       int8_t* dst = a.wq + static_cast<size_t>(c) * a.Kdim;
-      for (int i = l; i < a.Kdim; i += 64) {
-        const unsigned u = static_cast<unsigned>(static_cast<int32_t>(src[i])) - kOff;
-        bad |= (u + 128u) > 255u;
-        sum += static_cast<int>(u);
-        dst[i] = static_cast<int8_t>(u & 0xffu);
+      // four codes per lane in flight before the first conversion (the byte stores may alias
+      // the loads as far as the compiler knows, so a plain loop ran one load round trip each)
+      for (int i0 = l; i0 < a.Kdim; i0 += 4 * 64) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = i0 + 64 * u < a.Kdim ? src[i0 + 64 * u] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + 64 * u;
+          if (i < a.Kdim) {
+            const unsigned q = static_cast<unsigned>(static_cast<int32_t>(v[u])) - kOff;
+            bad |= (q + 128u) > 255u;
+            sum += static_cast<int>(q);
+            dst[i] = static_cast<int8_t>(q & 0xffu);
+          }
+        }
       }
     }
 #pragma unroll
