@@ -29,6 +29,12 @@ SHAPES = [
     (1, 9, 16, 3, 64, 3, 2, 1, 0),      # unequal filter and padding
     (1, 224, 224, 3, 64, 7, 7, 3, 3),   # one full stem image
     (5, 33, 16, 3, 64, 7, 7, 3, 3),
+    # the row build reads each pixel pair's 4C bytes from an offset (PLB - pw C) mod 4 into its
+    # first dword: 1 and 2 for three channels, 2 for two and for one channel
+    (2, 15, 32, 3, 64, 3, 3, 1, 1),
+    (1, 12, 48, 3, 64, 5, 5, 2, 2),
+    (2, 11, 24, 2, 64, 3, 3, 1, 1),
+    (1, 10, 32, 1, 64, 5, 5, 2, 2),
 ]
 
 
