@@ -30,6 +30,7 @@
 #include "qconv_device.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace miq {
 namespace {
@@ -230,10 +231,9 @@ struct StemPrepArgs {
   int32_t* flags;  // [nfb + nib]
   int N, H, W, C, K, Kdim, ph, pw, Hp, cpr;  // cpr: 16-byte chunks per padded row (Wq * C / 16)
   int nfb;                                   // filter blocks: 4 channels each
-  int rows;                                  // N * Hp padded rows, one wave each
+  long long nchunks;                         // N * Hp * cpr 16-byte chunks of the padded input
 };
 
-constexpr int kStemRowMax = 4096;  // bytes of one padded row (Wq * C) at most
 
 template <QpKind Q>
 __global__ void __launch_bounds__(kRtThreads) qi32_stem_prep_kernel(StemPrepArgs a) {
@@ -279,72 +279,78 @@ __global__ void __launch_bounds__(kRtThreads) qi32_stem_prep_kernel(StemPrepArgs
       }
     }
   } else {
-    // ---- input: one padded row per wave, built in LDS (codes at byte pw * C, the rest zx - o)
-    // and written as 16-byte chunks; codes come in 16-byte loads where a row is a whole number
-    // of them ----
-    __shared__ unsigned char rowbuf[kRtThreads / 64][kStemRowMax];
-    const int wv = t >> 6;
-    const int lane = t & 63;
-    const int row = 4 * (static_cast<int>(blockIdx.x) - a.nfb) + wv;  // n * Hp + hp
-    if (row < a.rows) {
-      unsigned char* buf = rowbuf[wv];
+    // ---- input: a thread per 16-byte chunk c of padded row `row` (= n * Hp + hp): byte b is
+    // code (16c + b - pw C) of image row hp - ph where that lies in the image, else zx - o.
+    // With rows of whole float4s the 16 codes come from the five aligned float4s around them
+    // (neighbouring threads share the lines), picked at the offset (-pw C) mod 4 every chunk
+    // shares; other rows read code by code ----
+    const long long idx = static_cast<long long>(static_cast<int>(blockIdx.x) - a.nfb) * kRtThreads + t;
+    if (idx < a.nchunks) {
+      const int row = static_cast<int>(idx / a.cpr);
+      const int c = static_cast<int>(idx - static_cast<long long>(row) * a.cpr);
       const int hp = row % a.Hp;
       const int n = row / a.Hp;
       const int hi = hp - a.ph;
       const int rowb = a.W * a.C;
-      const int wqb = 16 * a.cpr;
       const int lead = a.pw * a.C;
       const unsigned pad = static_cast<unsigned>(rt_zero_point<Q>(a.in_qp, n)) - kOff;
       const bool row_ok = hi >= 0 && hi < a.H;
-      for (int b = lane; b < wqb; b += 64) {
-        if (!row_ok || b < lead || b >= lead + rowb) buf[b] = static_cast<unsigned char>(pad & 0xffu);
-      }
-      if (row_ok) {
-        const float* src = a.x + (static_cast<size_t>(n) * a.H + hi) * rowb;
-        if ((rowb & 3) == 0) {
-          // four 16-byte loads per lane in flight, then their conversions
-          const int nq = rowb / 4;
-          for (int q0 = 0; q0 < nq; q0 += 256) {
-            v4f v[4];
+      const int b0 = 16 * c - lead;  // code index of byte 0
+      const float* src = a.x + (static_cast<size_t>(n) * a.H + (row_ok ? hi : 0)) * rowb;
+      unsigned word[4];
+      if (row_ok && (rowb & 3) == 0) {
+        const int f0 = b0 >= 0 ? b0 >> 2 : -((3 - b0) >> 2);  // floor(b0 / 4)
+        const int nq = rowb >> 2;
+        v4f v[5];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int q = q0 + 64 * i + lane;
-              v[i] = q < nq ? *reinterpret_cast<const v4f*>(src + 4 * q) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < 5; ++k) {
+          const int q = f0 + k;
+          v[k] = (q >= 0 && q < nq) ? *reinterpret_cast<const v4f*>(src + 4 * q) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        const int sh = b0 - 4 * f0;  // 0 .. 3, the same for every chunk
+        auto pick = [&](auto shc) {
+          constexpr int S = decltype(shc)::value;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            unsigned wd = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int b = 4 * d + e;
+              const int pos = b + S;  // float position in the window v[0..4]
+              const int code = b0 + b;
+              const bool in = code >= 0 && code < rowb;
+              const unsigned u = in ? static_cast<unsigned>(static_cast<int32_t>(v[pos >> 2][pos & 3])) - kOff : pad;
+              bad |= (u + 128u) > 255u;
+              wd |= (u & 0xffu) << (8 * e);
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int q = q0 + 64 * i + lane;
-              if (q < nq) {
-                unsigned word = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const unsigned u = static_cast<unsigned>(static_cast<int32_t>(v[i][e])) - kOff;
-                  bad |= (u + 128u) > 255u;
-                  word |= (u & 0xffu) << (8 * e);
-                }
-                if ((lead & 3) == 0) {
-                  *reinterpret_cast<unsigned*>(buf + lead + 4 * q) = word;
-                } else {
-#pragma unroll
-                  for (int e = 0; e < 4; ++e) buf[lead + 4 * q + e] = static_cast<unsigned char>(word >> (8 * e));
-                }
-              }
-            }
+            word[d] = wd;
           }
-        } else {
-          for (int i = lane; i < rowb; i += 64) {
-            const unsigned u = static_cast<unsigned>(static_cast<int32_t>(src[i])) - kOff;
+        };
+        switch (sh) {
+          case 0: pick(std::integral_constant<int, 0>{}); break;
+          case 1: pick(std::integral_constant<int, 1>{}); break;
+          case 2: pick(std::integral_constant<int, 2>{}); break;
+          default: pick(std::integral_constant<int, 3>{}); break;
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          unsigned wd = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int code = b0 + 4 * d + e;
+            const bool in = row_ok && code >= 0 && code < rowb;
+            const unsigned u = in ? static_cast<unsigned>(static_cast<int32_t>(src[code])) - kOff : pad;
             bad |= (u + 128u) > 255u;
-            buf[lead + i] = static_cast<unsigned char>(u & 0xffu);
+            wd |= (u & 0xffu) << (8 * e);
           }
+          word[d] = wd;
         }
       }
-      // this wave's LDS writes complete before its reads (one wave's LDS operations are in order)
-      for (int c = lane; c < a.cpr; c += 64) {
-        const v4i o = *reinterpret_cast<const v4i*>(buf + 16 * c);
-        *reinterpret_cast<v4i*>(a.xp + (static_cast<size_t>(row) * a.cpr + c) * 16) = o;
-        store_gap(o);
-      }
+      const v4i o = {static_cast<int>(word[0]), static_cast<int>(word[1]), static_cast<int>(word[2]),
+                     static_cast<int>(word[3])};
+      *reinterpret_cast<v4i*>(a.xp + idx * 16) = o;
+      store_gap(o);
     }
   }
   const int any = __syncthreads_or(bad ? 1 : 0);
@@ -401,7 +407,7 @@ StemLayout stem_layout(const Geom& g) {
   L.nchunks = static_cast<long long>(g.N) * L.gp.H * L.cpr;
   const long long kdim = static_cast<long long>(g.R) * g.S * g.C;
   L.nfb = (g.K + 3) / 4;
-  L.nib = static_cast<int>((static_cast<long long>(g.N) * L.gp.H + 3) / 4);  // 4 padded rows per block
+  L.nib = static_cast<int>((L.nchunks + kRtThreads - 1) / kRtThreads);  // a 16-byte chunk per thread
   L.xp_off = 0;
   L.wq_off = rt_align(static_cast<size_t>(L.nchunks) * 16);
   L.t_off = rt_align(L.wq_off + static_cast<size_t>(g.K) * kdim);
@@ -493,7 +499,6 @@ bool qi32_stem_route_eligible(const Geom& g, const BlockGeom& bg, const void* x,
   if (L.nchunks >= (1LL << 31) - kRtThreads || static_cast<long long>(g.N) * L.gp.H >= (1LL << 31) - 4) {
     return no("qi32 stem route: padded input too large");
   }
-  if (16LL * L.cpr > kStemRowMax) return no("qi32 stem route needs padded rows of at most 4096 bytes");
   if (static_cast<long long>(g.N) * g.H * g.W * g.C >= (1LL << 40)) return no("qi32 stem route: input too large");
   return stem_s2d_qi32_plan_ok(L.gp, why);
 }
@@ -517,7 +522,7 @@ hipError_t launch_qi32_stem_route(const Geom& g, QpKind qp, const float* x, cons
   pa.N = g.N; pa.H = g.H; pa.W = g.W; pa.C = g.C; pa.K = g.K; pa.Kdim = g.R * g.S * g.C;
   pa.ph = g.ph; pa.pw = g.pw; pa.Hp = L.gp.H; pa.cpr = L.cpr;
   pa.nfb = L.nfb;
-  pa.rows = g.N * L.gp.H;
+  pa.nchunks = L.nchunks;
   const dim3 pgrid(static_cast<unsigned>(L.nfb + L.nib));
   if (qp == kQpU8) {
     hipLaunchKernelGGL(qi32_stem_prep_kernel<kQpU8>, pgrid, dim3(kRtThreads), 0, stream, pa);
