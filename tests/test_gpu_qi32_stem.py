@@ -30,6 +30,7 @@ CASES = [
     ("u8", 2, 11, 24, 3, 64, 7, 7, (0, 0, 2, 2, 1, 1, 1), (0, 255)),       # no padding
     ("u8", 1, 9, 16, 3, 64, 3, 2, (3, 1, 2, 2, 1, 1, 1), (0, 255)),        # unequal filter and padding
     ("u8", 1, 224, 224, 3, 64, 7, 7, (3, 3, 2, 2, 1, 1, 1), (0, 255)),     # one full stem image
+    ("u8", 1, 12, 32, 3, 64, 5, 5, (2, 2, 2, 2, 1, 1, 1), (0, 255)),      # codes 2 past a float4 boundary
 ]
 
 
