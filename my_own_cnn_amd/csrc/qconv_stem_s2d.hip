@@ -489,6 +489,14 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
         seg_b(sg, B);
         mma_seg(B, acc, ws);
       }
+      // the first segment is stored before the pipelined loop starts (stores bound the loop)
+      if (sg + kSdWaves < nseg) {
+        store32(sg, acc, ws);
+        sg += kSdWaves;
+        v4i B[KB];
+        seg_b(sg, B);
+        mma_seg(B, acc, ws);
+      }
       for (;;) {
         const int sn = sg + kSdWaves;
         if (sn >= nseg) break;
@@ -524,6 +532,26 @@ __global__ void __launch_bounds__(64 * kSdWaves, 1) i8_stem_s2d_kernel(S2dArgs a
         for (int kb = 1; kb < KB; ++kb)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[kb][j], B[kb], acc[j], 0, 0, 0);
+      }
+      // the first segment's output goes out before the pipelined loop starts: the stores are the
+      // main loop's bound, and they start one segment earlier
+      {
+        const int sn = sg + kSdWaves;
+        if (sn < nseg) {
+          unsigned pk[4];
+          float f[16];
+          requant_values<0, 16>(acc, mult_v, RELU ? 0.0f : -128.0f, f, pk);
+          store(sg, pk);
+          sg = sn;
+          v4i B[KB];
+          seg_b(sg, B);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0][j], B[0], bias_v[j], 0, 0, 0);
+#pragma unroll
+          for (int kb = 1; kb < KB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[kb][j], B[kb], acc[j], 0, 0, 0);
+        }
       }
       for (;;) {
         const int sn = sg + kSdWaves;
